@@ -1,0 +1,158 @@
+/*
+ * smaul_rocm.h -- C ABI of the MI355X (gfx950) tiled-FP8 MoE forward library
+ * (libsmaul_rocm.so).
+ *
+ * Storage format (unchanged from the reference, kernel/fp8_tile.py:199-215):
+ *   codes  uint8 [out_f, in_f]            E4M3 with 0x7F/0xFF decoding to +-448
+ *   scales fp32  [out_f, ceil(in_f/tile)] one scale per (output row, K tile)
+ *   decoded weight W[o, k] = lut[codes[o, k]] * scales[o, k / tile]
+ *
+ * Conventions of every entry point:
+ *   - all pointers are device pointers unless stated otherwise;
+ *   - work is enqueued on `stream`, asynchronously; nothing synchronises;
+ *   - nothing allocates: callers pass outputs and, where needed, a workspace
+ *     whose size comes from the matching *_workspace_size query;
+ *   - the return value is SMAUL_OK or an error code; smaul_last_error() gives
+ *     a message for the calling thread's most recent failure.
+ *
+ * Activation dtypes: SMAUL_DTYPE_BF16 or SMAUL_DTYPE_F32.  bf16 activations are
+ * fed to bf16 MFMA directly; fp32 activations are split into two bf16 terms
+ * (hi + lo) so the product keeps ~16 more bits than a single bf16 rounding.
+ */
+#ifndef SMAUL_ROCM_H
+#define SMAUL_ROCM_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  SMAUL_OK = 0,
+  SMAUL_ERR_INVALID = 1,      /* bad argument (size, pointer, dtype)          */
+  SMAUL_ERR_UNSUPPORTED = 2,  /* valid for the reference, not supported here  */
+  SMAUL_ERR_HIP = 3           /* a HIP runtime call or launch failed          */
+};
+
+enum { SMAUL_DTYPE_F32 = 0, SMAUL_DTYPE_BF16 = 1 };
+
+/* Library version as an integer (major*10000 + minor*100 + patch). */
+int smaul_version(void);
+
+/* Message of the calling thread's last failure ("" if none). */
+const char* smaul_last_error(void);
+
+/*
+ * Dense tiled-FP8 linear: y[rows, out_f] = x[rows, in_f] . decode(w, s)^T.
+ * Replaces the reference backend entry fp8_forward
+ *   kernel/compute.py:125-135 (CpuBackend.fp8_forward) and
+ *   kernel/fp8_cpu.cpp:100-141 (native fp8_forward).
+ * x: x_dtype [rows, in_f] row-major; w: uint8 [out_f, in_f]; s: fp32
+ * [out_f, ceil(in_f/tile)]; y: y_dtype [rows, out_f].  tile must be a
+ * positive multiple of 32 (SMAUL_ERR_UNSUPPORTED otherwise).  rows may be 0.
+ */
+int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* s,
+                     void* y, int y_dtype, int64_t rows, int64_t in_f, int64_t out_f,
+                     int64_t tile, hipStream_t stream);
+
+/*
+ * MoE router: logits = x . gate_w^T (+ gate_b), prob = softmax(logits),
+ * (topv, topi) = top-k of prob with torch's CPU selection order, topw =
+ * topv / sum(topv) (uniform 1/k when the sum is below 1e-6).
+ * Replaces model.py:558-570 (SwiFFN_MoE.forward router, softmax, topk, renorm).
+ * x: x_dtype [T, d]; gate_w fp32 [E, d]; gate_b fp32 [E] or NULL.
+ * Outputs: prob fp32 [T, E]; topi int64 [T, k]; topw fp32 [T, k].
+ * 1 <= k <= E <= 64.
+ */
+int smaul_moe_router(const void* x, int x_dtype, const float* gate_w, const float* gate_b,
+                     float* prob, int64_t* topi, float* topw,
+                     int64_t T, int64_t d, int64_t E, int64_t k, hipStream_t stream);
+
+/*
+ * Deterministic dispatch: for each expert e, the tokens t with a positive
+ * routing weight for e, in ascending t (the boolean-mask gather order of
+ * model.py:574-581).  Replaces the per-expert mask/gather loop there.
+ * Inputs: topi int64 [T, k], topw fp32 [T, k].
+ * Outputs (int32 unless noted):
+ *   counts  [E]       tokens per expert (model.py:577 `n`)
+ *   seg_off [E+1]     first logical row of each expert's segment
+ *   tile_off[E+1]     first m-tile of each expert for row tiles of `block_m`
+ *   perm_row[T*k]     logical row -> token index (first seg_off[E] valid)
+ *   perm_w  fp32 [T*k] logical row -> routing weight
+ *   inv     [T*k]     token slot (t*k + j) -> logical row, -1 if not dispatched
+ * block_m must be 16, 32, 64, 128 or 256.
+ */
+int smaul_moe_dispatch(const int64_t* topi, const float* topw, int32_t* counts,
+                       int32_t* seg_off, int32_t* tile_off, int32_t* perm_row, float* perm_w,
+                       int32_t* inv, int64_t T, int64_t E, int64_t k, int64_t block_m,
+                       hipStream_t stream);
+
+/*
+ * Grouped expert GEMMs over the dispatched segments (SwiFFN, model.py:289-290).
+ * Expert weights are addressed through device arrays of device pointers, one
+ * entry per expert, so each expert's FP8Linear buffers are used in place.
+ *
+ * smaul_moe_gate_up: hdn[r, :] = cast(silu(cast(x[perm_row[r]] . Wg^T)) *
+ *   cast(x[perm_row[r]] . Wu^T)) where cast is to act_dtype (a no-op for fp32)
+ *   -- the rounding points of SwiFFN.forward with FP8Linear outputs in x.dtype.
+ *   x: act_dtype [T, d]; hdn: act_dtype [T*k, h].
+ * smaul_moe_down: yperm[r, :] = cast(hdn[r] . Wd^T); yperm: act_dtype [T*k, d].
+ * seg_off/tile_off come from smaul_moe_dispatch with block_m = smaul_moe_block_m().
+ * max_tiles is an upper bound on tile_off[E] (ceil(T*k/block_m) + E).
+ */
+int smaul_moe_block_m(int64_t T, int64_t k, int64_t E);
+
+int smaul_moe_gate_up(const void* x, int act_dtype, const int32_t* perm_row,
+                      const uint8_t* const* gate_w, const float* const* gate_s,
+                      const uint8_t* const* up_w, const float* const* up_s,
+                      void* hdn, const int32_t* seg_off, const int32_t* tile_off,
+                      int64_t max_tiles, int64_t E, int64_t d, int64_t h, int64_t tile,
+                      int64_t block_m, hipStream_t stream);
+
+int smaul_moe_down(const void* hdn, int act_dtype, const uint8_t* const* down_w,
+                   const float* const* down_s, void* yperm, const int32_t* seg_off,
+                   const int32_t* tile_off, int64_t max_tiles, int64_t E, int64_t d,
+                   int64_t h, int64_t tile, int64_t block_m, hipStream_t stream);
+
+/*
+ * Combine: out[t] = cast( sum over t's dispatched experts in ascending expert
+ * id of float(yperm[inv[t,j]]) * topw[t,j] ), accumulated in fp32 from +0 with
+ * no fused multiply-add -- model.py:571,582,585.
+ * yperm: act_dtype [T*k, d]; out: act_dtype [T, d].
+ */
+int smaul_moe_combine(const void* yperm, int act_dtype, const int64_t* topi,
+                      const float* topw, const int32_t* inv, void* out, int64_t T,
+                      int64_t d, int64_t k, hipStream_t stream);
+
+/*
+ * The whole MoE layer (router -> dispatch -> gate_up -> down -> combine) in
+ * one call; SwiFFN_MoE.forward of model.py:557-585.  `workspace` must hold
+ * smaul_moe_workspace_size(...) bytes (256-byte aligned).  prob/topi/topw are
+ * the router outputs (kept by the module as last_prob / last_topi); counts is
+ * int32 [E] (expert_token_counts; last_executed is counts > 0).
+ */
+int64_t smaul_moe_workspace_size(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
+                                 int act_dtype);
+
+int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
+                      const uint8_t* const* gate_w8, const float* const* gate_s,
+                      const uint8_t* const* up_w8, const float* const* up_s,
+                      const uint8_t* const* down_w8, const float* const* down_s,
+                      void* out, float* prob, int64_t* topi, float* topw, int32_t* counts,
+                      void* workspace, int64_t workspace_bytes,
+                      int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile,
+                      hipStream_t stream);
+
+/*
+ * Host-side self-test of the top-k selection order used by the router (no GPU
+ * involved): writes the k indices the router would select for `vals` [n].
+ * Exposed only so the CPU test suite can check the order against torch.topk.
+ */
+int smaul_selftest_topk(const float* vals, int64_t n, int64_t k, int64_t* out_idx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SMAUL_ROCM_H */

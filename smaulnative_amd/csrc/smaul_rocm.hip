@@ -1,0 +1,990 @@
+// libsmaul_rocm.so -- tiled-FP8 MoE forward for MI355X (gfx950 / CDNA4).
+//
+// Kernels:
+//   fp8_gemm_kernel   grouped (or dense) GEMM over E4M3 codes + per-tile fp32
+//                     scales.  bf16 MFMA (v_mfma_f32_16x16x32_bf16); codes are
+//                     decoded to bf16 once per workgroup while staging to LDS
+//                     (v_cvt_scalef32_pk_bf16_fp8); each output keeps an fp32
+//                     partial per scale tile and adds scale * partial when the
+//                     tile ends, which is exact algebra of
+//                     sum_k x[k] * lut[w[k]] * s[k / tile]  (fp8_cpu.cpp:49-98).
+//                     Optional SwiGLU epilogue (gate and up in one workgroup).
+//   router_kernel     fp32 router GEMV + softmax + top-k + renormalisation.
+//   dispatch_kernel   deterministic per-expert token order (ballot ranks).
+//   combine_kernel    weighted un-permute in ascending expert order.
+//
+// Host-side entry points are the extern "C" functions declared in
+// include/smaul_rocm.h.  Nothing here allocates device memory or synchronises.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "smaul_rocm.h"
+#include "topk_select.h"
+
+#define SMAUL_VERSION 100
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SMAUL_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return SMAUL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// scalar helpers
+// ---------------------------------------------------------------------------
+// fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (torch's
+// c10::BFloat16 conversion, the `.to(torch.bfloat16)` of the reference).
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Split an fp32 value into two bf16 terms: x ~= hi + lo (error <= 2^-18 |x|).
+__device__ __forceinline__ void split_bf16(float x, uint32_t& hi, uint32_t& lo) {
+  hi = f2bf(x);
+  lo = f2bf(x - bf2f(hi));
+}
+
+// The reference codebook decodes 0x7F/0xFF to +-448 where OCP E4M3FN has NaN;
+// every other code is identical.  Rewrite those two codes to 0x7E/0xFE (also
+// +-448) so the hardware OCP conversion is exact for all 256 codes.
+__device__ __forceinline__ uint32_t canon4(uint32_t w) {
+  const uint32_t t = w & 0x7f7f7f7fu;
+  const uint32_t m = (t + 0x01010101u) & 0x80808080u;  // bit 7 set where t == 0x7f
+  return w - (m >> 7);
+}
+
+// 4 E4M3 codes (bytes 0..3 of w) -> 4 bf16 packed in two dwords, exact.
+__device__ __forceinline__ void decode4(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  w = canon4(w);
+  bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+  bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+  lo = __builtin_bit_cast(uint32_t, a);
+  hi = __builtin_bit_cast(uint32_t, b);
+}
+
+__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
+
+// ---------------------------------------------------------------------------
+// grouped / dense FP8 GEMM
+// ---------------------------------------------------------------------------
+struct GemmArgs {
+  const void* x;               // activations: bf16 or fp32, row stride ldx elements
+  const int32_t* row_idx;      // logical row -> x row (nullptr: identity)
+  int64_t ldx;
+  // Per-expert weights.  If wp != nullptr the e-th expert's codes are wp[e],
+  // otherwise w + e * w_estride (same for scales and the SwiGLU "up" set).
+  const uint8_t* const* wp;
+  const float* const* sp;
+  const uint8_t* const* wp2;
+  const float* const* sp2;
+  const uint8_t* w;
+  const float* s;
+  const uint8_t* w2;
+  const float* s2;
+  int64_t w_estride, s_estride;
+  void* y;                     // output rows in logical order, row stride ldy
+  int64_t ldy;
+  int64_t K, N, nt, tile;
+  const int32_t* seg_off;      // [E+1] (nullptr: dense, R rows, one expert)
+  const int32_t* tile_off;     // [E+1]
+  int64_t R;
+  int E;
+};
+
+template <int BM, int BNO, int WM, int WN, bool SWIGLU, int NSPLIT, bool OUT_BF16, bool VEC>
+struct GemmCfg {
+  static constexpr int NT = WM * WN * 64;
+  static constexpr int NB = SWIGLU ? 2 * BNO : BNO;  // staged weight rows
+  static constexpr int TM = BM / WM;
+  static constexpr int TNO = BNO / WN;
+  static constexpr int FM = TM / 16;
+  static constexpr int FN = TNO / 16;                  // output col tiles per wave
+  static constexpr int NJ = SWIGLU ? 2 * FN : FN;      // weight col tiles per wave
+  static constexpr int LDK = 64 + 8;                   // padded LDS row (bf16 elements)
+  static_assert(TM % 16 == 0 && TNO % 16 == 0, "wave tile must be a multiple of 16");
+  // staging chunk counts per thread
+  static constexpr int A_CH = NSPLIT == 1 ? (BM * 8) / NT : (BM * 16) / NT;
+  static constexpr int B_CH = (NB * 4) / NT;
+  static_assert(A_CH >= 1 && (NSPLIT == 1 ? BM * 8 : BM * 16) % NT == 0, "A staging split");
+  static_assert(B_CH >= 1 && (NB * 4) % NT == 0, "B staging split");
+};
+
+template <int BM, int BNO, int WM, int WN, bool SWIGLU, int NSPLIT, bool OUT_BF16, bool VEC>
+__global__ void __launch_bounds__(WM * WN * 64)
+fp8_gemm_kernel(GemmArgs p) {
+  using C = GemmCfg<BM, BNO, WM, WN, SWIGLU, NSPLIT, OUT_BF16, VEC>;
+  constexpr int NT = C::NT, NB = C::NB, TM = C::TM, TNO = C::TNO, FM = C::FM, FN = C::FN,
+                NJ = C::NJ, LDK = C::LDK;
+
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2][NSPLIT][BM][LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[2][NB][LDK];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // ---- which expert / rows does this workgroup own -------------------------
+  const int mt = blockIdx.y;
+  int e = 0, row0, rows_here;
+  if (p.seg_off) {
+    const int total = p.tile_off[p.E];
+    if (mt >= total) return;
+    while (p.tile_off[e + 1] <= mt) ++e;
+    row0 = p.seg_off[e] + (mt - p.tile_off[e]) * BM;
+    rows_here = min(BM, p.seg_off[e + 1] - row0);
+  } else {
+    row0 = mt * BM;
+    rows_here = (int)min<int64_t>(BM, p.R - row0);
+  }
+  if (rows_here <= 0) return;
+  const int n0 = blockIdx.x * BNO;
+  const int64_t K = p.K, N = p.N, nt = p.nt;
+
+  const uint8_t* W1 = p.wp ? p.wp[e] : p.w + e * p.w_estride;
+  const float* S1 = p.sp ? p.sp[e] : p.s + e * p.s_estride;
+  const uint8_t* W2 = nullptr;
+  const float* S2 = nullptr;
+  if constexpr (SWIGLU) {
+    W2 = p.wp2 ? p.wp2[e] : p.w2 + e * p.w_estride;
+    S2 = p.sp2 ? p.sp2[e] : p.s2 + e * p.s_estride;
+  }
+
+  // ---- per-thread staging assignments --------------------------------------
+  // A: chunk c -> (row, k offset); bf16: 8 chunks of 8 elements per 64-K row,
+  // fp32: 16 chunks of 4 elements.
+  constexpr int A_PER_ROW = NSPLIT == 1 ? 8 : 16;
+  constexpr int A_ELEMS = 64 / A_PER_ROW;
+  const char* arow[C::A_CH];
+  int akoff[C::A_CH], arl[C::A_CH];
+#pragma unroll
+  for (int i = 0; i < C::A_CH; ++i) {
+    const int c = tid + i * NT;
+    const int r = c / A_PER_ROW;
+    arl[i] = r;
+    akoff[i] = (c % A_PER_ROW) * A_ELEMS;
+    if (r < rows_here) {
+      const int64_t lr = row0 + r;
+      const int64_t xr = p.row_idx ? (int64_t)p.row_idx[lr] : lr;
+      arow[i] = (const char*)p.x + xr * p.ldx * (NSPLIT == 1 ? 2 : 4);
+    } else {
+      arow[i] = nullptr;
+    }
+  }
+  // B: chunk c -> (staged weight row, k offset), 4 chunks of 16 codes per row.
+  const uint8_t* brow[C::B_CH];
+  int bkoff[C::B_CH], brl[C::B_CH];
+#pragma unroll
+  for (int i = 0; i < C::B_CH; ++i) {
+    const int c = tid + i * NT;
+    const int r = c >> 2;
+    brl[i] = r;
+    bkoff[i] = (c & 3) * 16;
+    int64_t col;
+    const uint8_t* base;
+    if (SWIGLU && r >= BNO) {
+      col = n0 + (r - BNO);
+      base = W2;
+    } else {
+      col = n0 + r;
+      base = W1;
+    }
+    brow[i] = col < N ? base + col * K : nullptr;
+  }
+
+  // staging registers
+  uint4 ra[C::A_CH];
+  uint4 rb[C::B_CH];
+
+  auto load_stage = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < C::A_CH; ++i) {
+      const int64_t kk = k0 + akoff[i];
+      if constexpr (VEC) {
+        if (arow[i] && kk < K) {
+          ra[i] = *(const uint4*)(arow[i] + kk * (NSPLIT == 1 ? 2 : 4));
+        } else {
+          ra[i] = make_uint4(0, 0, 0, 0);
+        }
+      } else {
+        uint32_t v[4] = {0, 0, 0, 0};
+        if (arow[i]) {
+          if constexpr (NSPLIT == 1) {
+            const uint16_t* src = (const uint16_t*)arow[i];
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+              if (kk + q < K) v[q >> 1] |= (uint32_t)src[kk + q] << ((q & 1) * 16);
+          } else {
+            const uint32_t* src = (const uint32_t*)arow[i];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (kk + q < K) v[q] = src[kk + q];
+          }
+        }
+        ra[i] = make_uint4(v[0], v[1], v[2], v[3]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_CH; ++i) {
+      const int64_t kk = k0 + bkoff[i];
+      if constexpr (VEC) {
+        if (brow[i] && kk < K) {
+          rb[i] = *(const uint4*)(brow[i] + kk);
+        } else {
+          rb[i] = make_uint4(0, 0, 0, 0);
+        }
+      } else {
+        uint32_t v[4] = {0, 0, 0, 0};
+        if (brow[i]) {
+#pragma unroll
+          for (int q = 0; q < 16; ++q)
+            if (kk + q < K) v[q >> 2] |= (uint32_t)brow[i][kk + q] << ((q & 3) * 8);
+        }
+        rb[i] = make_uint4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  };
+
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < C::A_CH; ++i) {
+      if constexpr (NSPLIT == 1) {
+        *(uint4*)&sA[buf][0][arl[i]][akoff[i]] = ra[i];
+      } else {
+        const float f[4] = {__uint_as_float(ra[i].x), __uint_as_float(ra[i].y),
+                            __uint_as_float(ra[i].z), __uint_as_float(ra[i].w)};
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) split_bf16(f[q], h[q], l[q]);
+        *(uint2*)&sA[buf][0][arl[i]][akoff[i]] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        *(uint2*)&sA[buf][NSPLIT - 1][arl[i]][akoff[i]] =
+            make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_CH; ++i) {
+      uint32_t d[8];
+      decode4(rb[i].x, d[0], d[1]);
+      decode4(rb[i].y, d[2], d[3]);
+      decode4(rb[i].z, d[4], d[5]);
+      decode4(rb[i].w, d[6], d[7]);
+      uint4* dst = (uint4*)&sB[buf][brl[i]][bkoff[i]];
+      dst[0] = make_uint4(d[0], d[1], d[2], d[3]);
+      dst[1] = make_uint4(d[4], d[5], d[6], d[7]);
+    }
+  };
+
+  // ---- accumulators --------------------------------------------------------
+  f32x4_t acc[FM][NJ];
+  f32x4_t part[FM][NJ];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      part[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+
+  // weight column (global) of col tile j for this lane, and its scale base
+  const float* scol[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const bool up = SWIGLU && j >= FN;
+    const int jj = up ? j - FN : j;
+    const int64_t col = n0 + wn * TNO + jj * 16 + (lane & 15);
+    const float* sb = up ? S2 : S1;
+    scol[j] = col < N ? sb + col * nt : nullptr;
+  }
+  // LDS row of col tile j inside sB
+  int bl_row[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const bool up = SWIGLU && j >= FN;
+    const int jj = up ? j - FN : j;
+    bl_row[j] = (up ? BNO : 0) + wn * TNO + jj * 16 + (lane & 15);
+  }
+  const int a_row_base = wm * TM + (lane & 15);
+  const int k_lane = (lane >> 4) * 8;
+
+  const int64_t nk64 = (K + 63) / 64;
+  const int64_t nk32 = (K + 31) / 32;
+  const int64_t steps_per_tile = p.tile / 32;
+  float scv[NJ];
+
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+
+  for (int64_t kt = 0; kt < nk64; ++kt) {
+    const int cur = (int)(kt & 1);
+    if (kt + 1 < nk64) load_stage((kt + 1) * 64);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int64_t g = kt * 2 + ks;
+      if (g < nk32) {
+        const bool first = (g % steps_per_tile) == 0;
+        const bool last = ((g + 1) % steps_per_tile) == 0 || g == nk32 - 1;
+        if (first) {
+          const int64_t kb = (g * 32) / p.tile;
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) scv[j] = scol[j] ? scol[j][kb] : 0.0f;
+        }
+        bf16x8_t af[NSPLIT][FM];
+#pragma unroll
+        for (int sp = 0; sp < NSPLIT; ++sp)
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+            af[sp][i] = *(const bf16x8_t*)&sA[cur][sp][a_row_base + i * 16][ks * 32 + k_lane];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const bf16x8_t bfr = *(const bf16x8_t*)&sB[cur][bl_row[j]][ks * 32 + k_lane];
+#pragma unroll
+          for (int i = 0; i < FM; ++i) {
+            f32x4_t c = first ? f32x4_t{0.f, 0.f, 0.f, 0.f} : part[i][j];
+#pragma unroll
+            for (int sp = 0; sp < NSPLIT; ++sp)
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[sp][i], bfr, c, 0, 0, 0);
+            part[i][j] = c;
+          }
+        }
+        if (last) {
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(scv[j], part[i][j][r], acc[i][j][r]);
+        }
+      }
+    }
+    if (kt + 1 < nk64) store_stage(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue ------------------------------------------------------------
+  // 16x16 MFMA output: lane holds column (lane & 15), rows (lane >> 4) * 4 + r.
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int lr = wm * TM + i * 16 + (lane >> 4) * 4 + r;
+      if (lr >= rows_here) continue;
+      const int64_t orow = row0 + lr;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int64_t col = n0 + wn * TNO + j * 16 + (lane & 15);
+        if (col >= N) continue;
+        float v;
+        if constexpr (SWIGLU) {
+          float g = acc[i][j][r], u = acc[i][j + FN][r];
+          if constexpr (OUT_BF16) {
+            g = bf2f(f2bf(g));
+            u = bf2f(f2bf(u));
+          }
+          v = silu_f(g) * u;
+        } else {
+          v = acc[i][j][r];
+        }
+        if constexpr (OUT_BF16) {
+          ((uint16_t*)p.y)[orow * p.ldy + col] = (uint16_t)f2bf(v);
+        } else {
+          ((float*)p.y)[orow * p.ldy + col] = v;
+        }
+      }
+    }
+  }
+}
+
+// Launch configurations.
+//   big:   128 rows x (64 SwiGLU outputs | 128 outputs), 4 waves as 2x2
+//   small:  32 rows x (64 SwiGLU outputs | 64 outputs),  4 waves as 1x4
+struct CfgBig {
+  static constexpr int BM = 128, WM = 2, WN = 2, BNO_SWIGLU = 64, BNO_PLAIN = 128;
+};
+struct CfgSmall {
+  static constexpr int BM = 32, WM = 1, WN = 4, BNO_SWIGLU = 64, BNO_PLAIN = 64;
+};
+
+template <class CF, bool SWIGLU, int NSPLIT, bool OUT_BF16, bool VEC>
+int launch_gemm(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
+  constexpr int BNO = SWIGLU ? CF::BNO_SWIGLU : CF::BNO_PLAIN;
+  const int64_t n_tiles = (a.N + BNO - 1) / BNO;
+  if (m_tiles <= 0 || n_tiles <= 0) return SMAUL_OK;
+  if (m_tiles > 65535 || n_tiles > 65535) return fail(SMAUL_ERR_UNSUPPORTED, "gemm grid too large");
+  dim3 grid((unsigned)n_tiles, (unsigned)m_tiles);
+  hipLaunchKernelGGL((fp8_gemm_kernel<CF::BM, BNO, CF::WM, CF::WN, SWIGLU, NSPLIT, OUT_BF16, VEC>),
+                     grid, dim3(CF::WM * CF::WN * 64), 0, stream, a);
+  return check_launch("fp8_gemm_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// router: logits, softmax, top-k (torch CPU order), renormalisation
+// ---------------------------------------------------------------------------
+// Lanes are (token, expert) pairs: LPT = next power of two >= E lanes per
+// token, 64 / LPT tokens per wave; each lane forms one full dot product in
+// ascending k.  One thread per token then runs softmax and the selection.
+constexpr int ROUTER_THREADS = 256;
+
+template <bool XBF16>
+__global__ void __launch_bounds__(ROUTER_THREADS)
+router_kernel(const void* __restrict__ x, const float* __restrict__ gw, const float* __restrict__ gb,
+              float* __restrict__ prob, int64_t* __restrict__ topi, float* __restrict__ topw,
+              int64_t T, int d, int E, int k, int lpt_log2) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int lpt = 1 << lpt_log2;
+  const int tpw = 64 >> lpt_log2;                 // tokens per wave
+  const int tpb = tpw * (ROUTER_THREADS / 64);    // tokens per block
+  float* slog = (float*)smem;                     // [tpb][E]
+  smaul_topk::Pair* spair = (smaul_topk::Pair*)(slog + tpb * E);  // [tpb][E]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int tl = wave * tpw + (lane >> lpt_log2);
+  const int ex = lane & (lpt - 1);
+  const int64_t t = (int64_t)blockIdx.x * tpb + tl;
+
+  if (t < T && ex < E) {
+    const float* wr = gw + (int64_t)ex * d;
+    float acc = 0.0f;
+    if constexpr (XBF16) {
+      const uint16_t* xr = (const uint16_t*)x + t * d;
+      int kk = 0;
+      if ((d & 7) == 0) {
+        for (; kk < d; kk += 8) {
+          const uint4 xv = *(const uint4*)(xr + kk);
+          const float4 w0 = *(const float4*)(wr + kk);
+          const float4 w1 = *(const float4*)(wr + kk + 4);
+          acc = __builtin_fmaf(bf2f(xv.x & 0xffff), w0.x, acc);
+          acc = __builtin_fmaf(bf2f(xv.x >> 16), w0.y, acc);
+          acc = __builtin_fmaf(bf2f(xv.y & 0xffff), w0.z, acc);
+          acc = __builtin_fmaf(bf2f(xv.y >> 16), w0.w, acc);
+          acc = __builtin_fmaf(bf2f(xv.z & 0xffff), w1.x, acc);
+          acc = __builtin_fmaf(bf2f(xv.z >> 16), w1.y, acc);
+          acc = __builtin_fmaf(bf2f(xv.w & 0xffff), w1.z, acc);
+          acc = __builtin_fmaf(bf2f(xv.w >> 16), w1.w, acc);
+        }
+      }
+      for (; kk < d; ++kk) acc = __builtin_fmaf(bf2f(xr[kk]), wr[kk], acc);
+    } else {
+      const float* xr = (const float*)x + t * d;
+      int kk = 0;
+      if ((d & 3) == 0) {
+        for (; kk < d; kk += 4) {
+          const float4 xv = *(const float4*)(xr + kk);
+          const float4 w0 = *(const float4*)(wr + kk);
+          acc = __builtin_fmaf(xv.x, w0.x, acc);
+          acc = __builtin_fmaf(xv.y, w0.y, acc);
+          acc = __builtin_fmaf(xv.z, w0.z, acc);
+          acc = __builtin_fmaf(xv.w, w0.w, acc);
+        }
+      }
+      for (; kk < d; ++kk) acc = __builtin_fmaf(xr[kk], wr[kk], acc);
+    }
+    if (gb) acc = acc + gb[ex];
+    slog[tl * E + ex] = acc;
+  }
+  __syncthreads();
+  if (tid < tpb) {
+    const int64_t tt = (int64_t)blockIdx.x * tpb + tid;
+    if (tt < T) {
+      const float* lg = slog + tid * E;
+      smaul_topk::Pair* q = spair + tid * E;
+      // softmax: max, exp(l - max), sum, multiply by 1/sum
+      float mx = lg[0];  // NaN propagates, as in torch's max reduction
+      for (int i = 1; i < E; ++i) mx = (lg[i] > mx || lg[i] != lg[i]) ? lg[i] : mx;
+      float sum = 0.0f;
+      for (int i = 0; i < E; ++i) {
+        const float ev = expf(lg[i] - mx);
+        q[i].v = ev;
+        sum = sum + ev;
+      }
+      const float inv = 1.0f / sum;
+      for (int i = 0; i < E; ++i) {
+        const float pv = q[i].v * inv;
+        q[i].v = pv;
+        q[i].i = i;
+        prob[tt * E + i] = pv;
+      }
+      smaul_topk::topk(q, E, k);
+      float denom = 0.0f;
+      for (int j = 0; j < k; ++j) denom = denom + q[j].v;
+      const bool tiny = denom < 1e-6f;
+      const float dcl = fmaxf(denom, 1e-9f);
+      for (int j = 0; j < k; ++j) {
+        topi[tt * k + j] = q[j].i;
+        topw[tt * k + j] = tiny ? 1.0f / (float)k : q[j].v / dcl;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dispatch (one workgroup): counts, offsets, tile table, ranked permutation
+// ---------------------------------------------------------------------------
+constexpr int DISPATCH_THREADS = 1024;
+constexpr int MAX_E = 64;
+
+__global__ void __launch_bounds__(DISPATCH_THREADS)
+dispatch_kernel(const int64_t* __restrict__ topi, const float* __restrict__ topw,
+                int32_t* __restrict__ counts, int32_t* __restrict__ seg_off,
+                int32_t* __restrict__ tile_off, int32_t* __restrict__ perm_row,
+                float* __restrict__ perm_w, int32_t* __restrict__ inv, int64_t T, int E, int k,
+                int block_m) {
+  __shared__ int s_cnt[MAX_E];
+  __shared__ int s_base[MAX_E];
+  __shared__ int s_wc[MAX_E][DISPATCH_THREADS / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int NW = DISPATCH_THREADS / 64;
+  if (tid < MAX_E) s_cnt[tid] = 0;
+  __syncthreads();
+  // pass 1: histogram (integer LDS atomics: order does not matter)
+  for (int64_t t = tid; t < T; t += DISPATCH_THREADS) {
+    for (int j = 0; j < k; ++j) {
+      if (topw[t * k + j] > 0.0f) atomicAdd(&s_cnt[(int)topi[t * k + j]], 1);
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int off = 0, toff = 0;
+    for (int ee = 0; ee < E; ++ee) {
+      counts[ee] = s_cnt[ee];
+      seg_off[ee] = off;
+      tile_off[ee] = toff;
+      s_base[ee] = off;
+      off += s_cnt[ee];
+      toff += (s_cnt[ee] + block_m - 1) / block_m;
+    }
+    seg_off[E] = off;
+    tile_off[E] = toff;
+  }
+  __syncthreads();
+  // pass 2: ranks in ascending token order, one round of 1024 tokens at a time
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t r0 = 0; r0 < T; r0 += DISPATCH_THREADS) {
+    const int64_t t = r0 + tid;
+    const bool valid = t < T;
+    int ej[8], rk[8];
+    bool on[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ej[j] = -1;
+      rk[j] = 0;
+      on[j] = false;
+    }
+    uint64_t sel = 0;
+    if (valid) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j < k) {
+          const float w = topw[t * k + j];
+          ej[j] = (int)topi[t * k + j];
+          on[j] = w > 0.0f;
+          if (on[j]) sel |= 1ull << ej[j];
+          else inv[t * k + j] = -1;
+        }
+      }
+    }
+    for (int ee = 0; ee < E; ++ee) {
+      const bool has = (sel >> ee) & 1ull;
+      const uint64_t b = __ballot(has);
+      if (lane == 0) s_wc[ee][wave] = __popcll(b);
+      if (has) {
+        const int rank = __popcll(b & lt_mask);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (on[j] && ej[j] == ee) rk[j] = rank;
+      }
+    }
+    __syncthreads();
+    if (valid) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j < k && on[j]) {
+          const int ee = ej[j];
+          int pre = 0;
+          for (int ww = 0; ww < wave; ++ww) pre += s_wc[ee][ww];
+          const int pos = s_base[ee] + pre + rk[j];
+          perm_row[pos] = (int32_t)t;
+          perm_w[pos] = topw[t * k + j];
+          inv[t * k + j] = pos;
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < E) {
+      int tot = 0;
+      for (int ww = 0; ww < NW; ++ww) tot += s_wc[tid][ww];
+      s_base[tid] += tot;
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// combine: out[t] = cast(sum over ascending expert id of y * w), fp32, no FMA
+// ---------------------------------------------------------------------------
+template <bool BF16>
+__global__ void __launch_bounds__(256)
+combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
+               const float* __restrict__ topw, const int32_t* __restrict__ inv,
+               void* __restrict__ out, int64_t T, int d, int k) {
+  // thread handles 8 consecutive columns of one token
+  const int cpt = d / 8;  // chunks per token (d % 8 == 0 enforced by the host)
+  const int64_t gidx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t t = gidx / cpt;
+  if (t >= T) return;
+  const int c0 = (int)(gidx % cpt) * 8;
+  // gather (expert, row, weight) of dispatched slots, sort by expert id
+  int ex[8];
+  int rw[8];
+  float wt[8];
+  int n = 0;
+  for (int j = 0; j < k; ++j) {
+    const int pos = inv[t * k + j];
+    if (pos < 0) continue;
+    const int ee = (int)topi[t * k + j];
+    int q = n++;
+    while (q > 0 && ex[q - 1] > ee) {
+      ex[q] = ex[q - 1];
+      rw[q] = rw[q - 1];
+      wt[q] = wt[q - 1];
+      --q;
+    }
+    ex[q] = ee;
+    rw[q] = pos;
+    wt[q] = topw[t * k + j];
+  }
+  float acc[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+  for (int s = 0; s < n; ++s) {
+    float yv[8];
+    if constexpr (BF16) {
+      const uint4 v = *(const uint4*)((const uint16_t*)yperm + (int64_t)rw[s] * d + c0);
+      yv[0] = bf2f(v.x & 0xffff); yv[1] = bf2f(v.x >> 16);
+      yv[2] = bf2f(v.y & 0xffff); yv[3] = bf2f(v.y >> 16);
+      yv[4] = bf2f(v.z & 0xffff); yv[5] = bf2f(v.z >> 16);
+      yv[6] = bf2f(v.w & 0xffff); yv[7] = bf2f(v.w >> 16);
+    } else {
+      const float4* src = (const float4*)((const float*)yperm + (int64_t)rw[s] * d + c0);
+      const float4 a = src[0], b = src[1];
+      yv[0] = a.x; yv[1] = a.y; yv[2] = a.z; yv[3] = a.w;
+      yv[4] = b.x; yv[5] = b.y; yv[6] = b.z; yv[7] = b.w;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float pr = yv[q] * wt[s];   // rounded product (library built with -ffp-contract=off)
+      acc[q] = acc[q] + pr;
+    }
+  }
+  if constexpr (BF16) {
+    uint4 o;
+    o.x = f2bf(acc[0]) | (f2bf(acc[1]) << 16);
+    o.y = f2bf(acc[2]) | (f2bf(acc[3]) << 16);
+    o.z = f2bf(acc[4]) | (f2bf(acc[5]) << 16);
+    o.w = f2bf(acc[6]) | (f2bf(acc[7]) << 16);
+    *(uint4*)((uint16_t*)out + t * d + c0) = o;
+  } else {
+    float4* dst = (float4*)((float*)out + t * d + c0);
+    dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host helpers
+// ---------------------------------------------------------------------------
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+bool dtype_ok(int dt) { return dt == SMAUL_DTYPE_F32 || dt == SMAUL_DTYPE_BF16; }
+
+int pick_block_m(int64_t T, int64_t k, int64_t E) {
+  // rows per expert on average; small segments use the 32-row tile
+  const int64_t avg = (T * k + E - 1) / (E > 0 ? E : 1);
+  return avg >= 96 ? CfgBig::BM : CfgSmall::BM;
+}
+
+template <class CF>
+int gemm_dispatch_moe(const GemmArgs& a, bool swiglu, int act_dtype, int64_t m_tiles,
+                      hipStream_t s) {
+  if (swiglu) {
+    if (act_dtype == SMAUL_DTYPE_BF16) return launch_gemm<CF, true, 1, true, true>(a, m_tiles, s);
+    return launch_gemm<CF, true, 2, false, true>(a, m_tiles, s);
+  }
+  if (act_dtype == SMAUL_DTYPE_BF16) return launch_gemm<CF, false, 1, true, true>(a, m_tiles, s);
+  return launch_gemm<CF, false, 2, false, true>(a, m_tiles, s);
+}
+
+int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+int smaul_version(void) { return SMAUL_VERSION; }
+
+const char* smaul_last_error(void) { return g_err; }
+
+int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* s, void* y,
+                     int y_dtype, int64_t rows, int64_t in_f, int64_t out_f, int64_t tile,
+                     hipStream_t stream) {
+  if (tile <= 0 || in_f <= 0 || out_f <= 0 || rows < 0)
+    return fail(SMAUL_ERR_INVALID, "tile/in_f/out_f must be positive, got %lld/%lld/%lld",
+                (long long)tile, (long long)in_f, (long long)out_f);
+  if (!dtype_ok(x_dtype) || y_dtype != SMAUL_DTYPE_F32)
+    return fail(SMAUL_ERR_INVALID, "x dtype must be f32|bf16 and y dtype f32");
+  if (tile % 32 != 0)
+    return fail(SMAUL_ERR_UNSUPPORTED, "tile %lld is not a multiple of 32", (long long)tile);
+  if (rows == 0) return SMAUL_OK;
+  if (!x || !w || !s || !y) return fail(SMAUL_ERR_INVALID, "null pointer");
+  GemmArgs a{};
+  a.x = x;
+  a.row_idx = nullptr;
+  a.ldx = in_f;
+  a.w = w;
+  a.s = s;
+  a.w_estride = 0;
+  a.s_estride = 0;
+  a.y = y;
+  a.ldy = out_f;
+  a.K = in_f;
+  a.N = out_f;
+  a.nt = (in_f + tile - 1) / tile;
+  a.tile = tile;
+  a.seg_off = nullptr;
+  a.tile_off = nullptr;
+  a.R = rows;
+  a.E = 1;
+  const bool vec = (in_f % 16 == 0) && aligned16(x) && aligned16(w);
+  const bool small = rows <= 64;
+  const int64_t bm = small ? CfgSmall::BM : CfgBig::BM;
+  const int64_t mt = (rows + bm - 1) / bm;
+  if (x_dtype == SMAUL_DTYPE_BF16) {
+    if (small)
+      return vec ? launch_gemm<CfgSmall, false, 1, false, true>(a, mt, stream)
+                 : launch_gemm<CfgSmall, false, 1, false, false>(a, mt, stream);
+    return vec ? launch_gemm<CfgBig, false, 1, false, true>(a, mt, stream)
+               : launch_gemm<CfgBig, false, 1, false, false>(a, mt, stream);
+  }
+  if (small)
+    return vec ? launch_gemm<CfgSmall, false, 2, false, true>(a, mt, stream)
+               : launch_gemm<CfgSmall, false, 2, false, false>(a, mt, stream);
+  return vec ? launch_gemm<CfgBig, false, 2, false, true>(a, mt, stream)
+             : launch_gemm<CfgBig, false, 2, false, false>(a, mt, stream);
+}
+
+int smaul_moe_router(const void* x, int x_dtype, const float* gate_w, const float* gate_b,
+                     float* prob, int64_t* topi, float* topw, int64_t T, int64_t d, int64_t E,
+                     int64_t k, hipStream_t stream) {
+  if (T < 0 || d <= 0 || E < 1 || E > MAX_E || k < 1 || k > E)
+    return fail(SMAUL_ERR_INVALID, "router: need T>=0, d>0, 1<=k<=E<=64 (T=%lld d=%lld E=%lld k=%lld)",
+                (long long)T, (long long)d, (long long)E, (long long)k);
+  if (!dtype_ok(x_dtype)) return fail(SMAUL_ERR_INVALID, "router: bad x dtype");
+  if (T == 0) return SMAUL_OK;
+  if (!x || !gate_w || !prob || !topi || !topw) return fail(SMAUL_ERR_INVALID, "router: null pointer");
+  if (!aligned16(x) || !aligned16(gate_w))
+    return fail(SMAUL_ERR_INVALID, "router: x and gate_w must be 16-byte aligned");
+  int lpt_log2 = 0;
+  while ((1 << lpt_log2) < E) ++lpt_log2;
+  const int tpb = (64 >> lpt_log2) * (ROUTER_THREADS / 64);
+  const int64_t blocks = (T + tpb - 1) / tpb;
+  const size_t shm = (size_t)tpb * E * (sizeof(float) + sizeof(smaul_topk::Pair));
+  if (x_dtype == SMAUL_DTYPE_BF16)
+    hipLaunchKernelGGL(router_kernel<true>, dim3((unsigned)blocks), dim3(ROUTER_THREADS), shm, stream,
+                       x, gate_w, gate_b, prob, topi, topw, T, (int)d, (int)E, (int)k, lpt_log2);
+  else
+    hipLaunchKernelGGL(router_kernel<false>, dim3((unsigned)blocks), dim3(ROUTER_THREADS), shm, stream,
+                       x, gate_w, gate_b, prob, topi, topw, T, (int)d, (int)E, (int)k, lpt_log2);
+  return check_launch("router_kernel");
+}
+
+int smaul_moe_dispatch(const int64_t* topi, const float* topw, int32_t* counts, int32_t* seg_off,
+                       int32_t* tile_off, int32_t* perm_row, float* perm_w, int32_t* inv, int64_t T,
+                       int64_t E, int64_t k, int64_t block_m, hipStream_t stream) {
+  if (T < 0 || E < 1 || E > MAX_E || k < 1 || k > E || k > 8)
+    return fail(SMAUL_ERR_INVALID, "dispatch: need T>=0, 1<=k<=min(E,8), E<=64");
+  if (T * k > 2147483647LL) return fail(SMAUL_ERR_UNSUPPORTED, "dispatch: T*k exceeds int32");
+  if (!(block_m == 16 || block_m == 32 || block_m == 64 || block_m == 128 || block_m == 256))
+    return fail(SMAUL_ERR_INVALID, "dispatch: block_m must be 16..256 (power of two)");
+  if (!topi || !topw || !counts || !seg_off || !tile_off || !perm_row || !perm_w || !inv)
+    return fail(SMAUL_ERR_INVALID, "dispatch: null pointer");
+  hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DISPATCH_THREADS), 0, stream, topi, topw, counts,
+                     seg_off, tile_off, perm_row, perm_w, inv, T, (int)E, (int)k, (int)block_m);
+  return check_launch("dispatch_kernel");
+}
+
+int smaul_moe_block_m(int64_t T, int64_t k, int64_t E) { return pick_block_m(T, k, E); }
+
+static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* perm_row,
+                    const uint8_t* const* w1, const float* const* s1, const uint8_t* const* w2,
+                    const float* const* s2, void* out, const int32_t* seg_off,
+                    const int32_t* tile_off, int64_t max_tiles, int64_t E, int64_t K, int64_t N,
+                    int64_t tile, int64_t block_m, hipStream_t stream) {
+  if (!dtype_ok(act_dtype)) return fail(SMAUL_ERR_INVALID, "moe gemm: bad dtype");
+  if (E < 1 || E > MAX_E || K <= 0 || N <= 0 || tile <= 0 || max_tiles < 0)
+    return fail(SMAUL_ERR_INVALID, "moe gemm: bad sizes");
+  if (tile % 32 != 0) return fail(SMAUL_ERR_UNSUPPORTED, "moe gemm: tile must be a multiple of 32");
+  if (K % 16 != 0 || !aligned16(act))
+    return fail(SMAUL_ERR_UNSUPPORTED, "moe gemm: K must be a multiple of 16 and activations 16-byte aligned");
+  if (!(block_m == CfgBig::BM || block_m == CfgSmall::BM))
+    return fail(SMAUL_ERR_INVALID, "moe gemm: block_m must come from smaul_moe_block_m");
+  if (!act || !w1 || !s1 || !out || !seg_off || !tile_off || (swiglu && (!w2 || !s2)))
+    return fail(SMAUL_ERR_INVALID, "moe gemm: null pointer");
+  if (max_tiles == 0) return SMAUL_OK;
+  GemmArgs a{};
+  a.x = act;
+  a.row_idx = perm_row;
+  a.ldx = K;
+  a.wp = w1;
+  a.sp = s1;
+  a.wp2 = w2;
+  a.sp2 = s2;
+  a.y = out;
+  a.ldy = N;
+  a.K = K;
+  a.N = N;
+  a.nt = (K + tile - 1) / tile;
+  a.tile = tile;
+  a.seg_off = seg_off;
+  a.tile_off = tile_off;
+  a.E = (int)E;
+  if (block_m == CfgBig::BM) return gemm_dispatch_moe<CfgBig>(a, swiglu, act_dtype, max_tiles, stream);
+  return gemm_dispatch_moe<CfgSmall>(a, swiglu, act_dtype, max_tiles, stream);
+}
+
+int smaul_moe_gate_up(const void* x, int act_dtype, const int32_t* perm_row,
+                      const uint8_t* const* gate_w, const float* const* gate_s,
+                      const uint8_t* const* up_w, const float* const* up_s, void* hdn,
+                      const int32_t* seg_off, const int32_t* tile_off, int64_t max_tiles, int64_t E,
+                      int64_t d, int64_t h, int64_t tile, int64_t block_m, hipStream_t stream) {
+  if (!perm_row) return fail(SMAUL_ERR_INVALID, "gate_up: null perm_row");
+  return moe_gemm(true, x, act_dtype, perm_row, gate_w, gate_s, up_w, up_s, hdn, seg_off, tile_off,
+                  max_tiles, E, d, h, tile, block_m, stream);
+}
+
+int smaul_moe_down(const void* hdn, int act_dtype, const uint8_t* const* down_w,
+                   const float* const* down_s, void* yperm, const int32_t* seg_off,
+                   const int32_t* tile_off, int64_t max_tiles, int64_t E, int64_t d, int64_t h,
+                   int64_t tile, int64_t block_m, hipStream_t stream) {
+  return moe_gemm(false, hdn, act_dtype, nullptr, down_w, down_s, nullptr, nullptr, yperm, seg_off,
+                  tile_off, max_tiles, E, h, d, tile, block_m, stream);
+}
+
+int smaul_moe_combine(const void* yperm, int act_dtype, const int64_t* topi, const float* topw,
+                      const int32_t* inv, void* out, int64_t T, int64_t d, int64_t k,
+                      hipStream_t stream) {
+  if (!dtype_ok(act_dtype) || T < 0 || d <= 0 || k < 1 || k > 8)
+    return fail(SMAUL_ERR_INVALID, "combine: bad arguments");
+  if (d % 8 != 0) return fail(SMAUL_ERR_UNSUPPORTED, "combine: d must be a multiple of 8");
+  if (T == 0) return SMAUL_OK;
+  if (!yperm || !topi || !topw || !inv || !out) return fail(SMAUL_ERR_INVALID, "combine: null pointer");
+  if (!aligned16(yperm) || !aligned16(out)) return fail(SMAUL_ERR_INVALID, "combine: unaligned buffers");
+  const int64_t total = T * (d / 8);
+  const int64_t blocks = (total + 255) / 256;
+  if (act_dtype == SMAUL_DTYPE_BF16)
+    hipLaunchKernelGGL(combine_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, yperm, topi,
+                       topw, inv, out, T, (int)d, (int)k);
+  else
+    hipLaunchKernelGGL(combine_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, yperm, topi,
+                       topw, inv, out, T, (int)d, (int)k);
+  return check_launch("combine_kernel");
+}
+
+// Workspace layout (each piece 256-byte aligned):
+//   seg_off[E+1] tile_off[E+1] perm_row[T*k] perm_w[T*k] inv[T*k]
+//   hdn[T*k, h] (act dtype)  yperm[T*k, d] (act dtype)
+int64_t smaul_moe_workspace_size(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
+                                 int act_dtype) {
+  if (T < 0 || d <= 0 || h <= 0 || E < 1 || k < 1 || !dtype_ok(act_dtype)) return -1;
+  const int64_t el = act_dtype == SMAUL_DTYPE_BF16 ? 2 : 4;
+  const int64_t R = T * k;
+  int64_t n = 0;
+  n += align256((E + 1) * 4) * 2;
+  n += align256(R * 4) * 3;
+  n += align256(R * h * el);
+  n += align256(R * d * el);
+  return n;
+}
+
+int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
+                      const uint8_t* const* gate_w8, const float* const* gate_s,
+                      const uint8_t* const* up_w8, const float* const* up_s,
+                      const uint8_t* const* down_w8, const float* const* down_s, void* out,
+                      float* prob, int64_t* topi, float* topw, int32_t* counts, void* workspace,
+                      int64_t workspace_bytes, int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
+                      int64_t tile, hipStream_t stream) {
+  const int64_t need = smaul_moe_workspace_size(T, d, h, E, k, act_dtype);
+  if (need < 0) return fail(SMAUL_ERR_INVALID, "moe_forward: bad sizes");
+  if (workspace_bytes < need)
+    return fail(SMAUL_ERR_INVALID, "moe_forward: workspace %lld < %lld bytes", (long long)workspace_bytes,
+                (long long)need);
+  if (T == 0) return SMAUL_OK;
+  if (((uintptr_t)workspace & 255u) != 0) return fail(SMAUL_ERR_INVALID, "moe_forward: workspace not 256-byte aligned");
+  const int64_t el = act_dtype == SMAUL_DTYPE_BF16 ? 2 : 4;
+  const int64_t R = T * k;
+  char* ws = (char*)workspace;
+  int32_t* seg_off = (int32_t*)ws;
+  ws += align256((E + 1) * 4);
+  int32_t* tile_off = (int32_t*)ws;
+  ws += align256((E + 1) * 4);
+  int32_t* perm_row = (int32_t*)ws;
+  ws += align256(R * 4);
+  float* perm_w = (float*)ws;
+  ws += align256(R * 4);
+  int32_t* inv = (int32_t*)ws;
+  ws += align256(R * 4);
+  void* hdn = ws;
+  ws += align256(R * h * el);
+  void* yperm = ws;
+
+  int rc = smaul_moe_router(x, act_dtype, gate_w, gate_b, prob, topi, topw, T, d, E, k, stream);
+  if (rc) return rc;
+  const int64_t bm = pick_block_m(T, k, E);
+  rc = smaul_moe_dispatch(topi, topw, counts, seg_off, tile_off, perm_row, perm_w, inv, T, E, k, bm, stream);
+  if (rc) return rc;
+  const int64_t max_tiles = (R + bm - 1) / bm + E;
+  rc = smaul_moe_gate_up(x, act_dtype, perm_row, gate_w8, gate_s, up_w8, up_s, hdn, seg_off, tile_off,
+                         max_tiles, E, d, h, tile, bm, stream);
+  if (rc) return rc;
+  rc = smaul_moe_down(hdn, act_dtype, down_w8, down_s, yperm, seg_off, tile_off, max_tiles, E, d, h, tile,
+                      bm, stream);
+  if (rc) return rc;
+  return smaul_moe_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, stream);
+}
+
+int smaul_selftest_topk(const float* vals, int64_t n, int64_t k, int64_t* out_idx) {
+  if (!vals || !out_idx || n < 1 || n > MAX_E || k < 1 || k > n)
+    return fail(SMAUL_ERR_INVALID, "selftest_topk: need 1<=k<=n<=64");
+  smaul_topk::Pair q[MAX_E];
+  for (int i = 0; i < n; ++i) q[i] = smaul_topk::Pair{vals[i], i};
+  smaul_topk::topk(q, (int)n, (int)k);
+  for (int i = 0; i < k; ++i) out_idx[i] = q[i].i;
+  return SMAUL_OK;
+}
+
+}  // extern "C"

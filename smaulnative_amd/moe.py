@@ -1,0 +1,156 @@
+"""``SwiFFN`` and ``SwiFFN_MoE`` with the reference's interface (model.py:282-290, 506-606).
+
+``SwiFFN_MoE.forward(x)`` keeps the reference signature, output dtype and the
+diagnostic attributes read by training logs and retention reports:
+``last_prob``, ``last_topi``, ``last_executed``, ``expert_token_counts``,
+``routing_stats()``, ``reset_routing_stats()``, ``balance_loss(prob)``.
+
+The whole layer (router, dispatch, the expert SwiGLU GEMMs, combine) is one
+call to the backend's ``moe_forward``; the per-expert Python loop with a host
+sync per expert (model.py:574-582) is gone.  ``expert_token_counts`` and
+``last_executed`` are materialised from the device counts only when read, so
+a decode step does not force a device->host sync per layer.
+
+Only the plain architecture's dense SwiGLU experts are on this path; the rawr
+(sparse) experts are not (model.py:528-534).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from smaulnative_amd.compute import get_backend
+from smaulnative_amd.fp8_tile import FP8Linear
+
+
+@dataclass
+class MoEConfig:
+    """The LinearConfig fields (model.py:18-40) the MoE layer reads.
+
+    A reference ``LinearConfig`` instance works in its place (same names).
+    """
+    d_model: int = 512
+    ffn_mult: float = 2.5
+    tile: int = 64
+    num_experts: int = 1
+    num_experts_per_tok: int = 1
+    precision: str = "fp8"
+    architecture: str = "plain"
+
+    def __post_init__(self):
+        for name in ("d_model", "tile", "num_experts", "num_experts_per_tok"):
+            v = getattr(self, name)
+            if not isinstance(v, int) or v <= 0:
+                raise ValueError(f"{name} must be a positive int, got {v!r}")
+        if self.num_experts_per_tok > self.num_experts:
+            raise ValueError(f"num_experts_per_tok ({self.num_experts_per_tok}) > "
+                             f"num_experts ({self.num_experts})")
+
+
+class SwiFFN(nn.Module):
+    """model.py:282-290: down((silu(gate(x).float()) * up(x).float()).to(x.dtype))."""
+
+    def __init__(self, cfg):
+        super().__init__()
+        if cfg.precision != "fp8":
+            raise ValueError("the rocm path implements precision='fp8' experts only")
+        h = int(cfg.d_model * cfg.ffn_mult)
+        self.gate = FP8Linear(cfg.d_model, h, cfg.tile)
+        self.up = FP8Linear(cfg.d_model, h, cfg.tile)
+        self.down = FP8Linear(h, cfg.d_model, cfg.tile)
+
+    def forward(self, x):
+        odt = x.dtype if x.is_floating_point() else torch.float32
+        return self.down((F.silu(self.gate(x).float()) * self.up(x).float()).to(odt))
+
+    def buffers6(self):
+        return (self.gate.w8, self.gate.sc, self.up.w8, self.up.sc, self.down.w8, self.down.sc)
+
+
+class SwiFFN_MoE(nn.Module):
+    """Top-k routed mixture of SwiFFN experts (model.py:506-606)."""
+
+    def __init__(self, cfg, rawr_graph=None):
+        super().__init__()
+        if cfg.num_experts < 1 or cfg.num_experts_per_tok < 1:
+            raise ValueError("num_experts and num_experts_per_tok must be >= 1")
+        if cfg.num_experts_per_tok > cfg.num_experts:
+            raise ValueError(
+                f"num_experts_per_tok ({cfg.num_experts_per_tok}) > num_experts ({cfg.num_experts})")
+        if getattr(cfg, "architecture", "plain") != "plain":
+            raise ValueError("the rocm MoE path implements architecture='plain' (SwiFFN experts) only")
+        self.top_k = cfg.num_experts_per_tok
+        self.num_experts = cfg.num_experts
+        self.architecture = "plain"
+        self.tile = cfg.tile
+        self.experts = nn.ModuleList([SwiFFN(cfg) for _ in range(cfg.num_experts)])
+        self.gate = nn.Linear(cfg.d_model, cfg.num_experts, bias=False)
+        self.last_prob = None
+        self.last_topi = None
+        self._counts_dev = None
+        self._counts_host = [0] * cfg.num_experts
+
+    # -- diagnostics (model.py:538-543,583-584,587-606), materialised lazily --
+    @property
+    def expert_token_counts(self):
+        if self._counts_dev is not None:
+            self._counts_host = [int(c) for c in self._counts_dev.tolist()]
+            self._counts_dev = None
+        return self._counts_host
+
+    @expert_token_counts.setter
+    def expert_token_counts(self, value):
+        self._counts_dev = None
+        self._counts_host = list(value)
+
+    @property
+    def last_executed(self):
+        return [c > 0 for c in self.expert_token_counts]
+
+    @last_executed.setter
+    def last_executed(self, value):
+        # kept for interface compatibility; executed is derived from counts
+        pass
+
+    def balance_loss(self, prob: torch.Tensor) -> torch.Tensor:
+        """Switch-style load-balancing aux loss (model.py:545-555)."""
+        density = prob.mean(0)
+        return (density * density * self.num_experts).sum()
+
+    def forward(self, x):
+        be = get_backend()
+        if not hasattr(be, "moe_forward"):
+            raise RuntimeError(f"compute backend {be.name!r} has no moe_forward entry")
+        if torch.is_grad_enabled() and (x.requires_grad or self.gate.weight.requires_grad) \
+                and self.training:
+            raise NotImplementedError("rocm MoE path is forward-only (training is not implemented)")
+        experts = [ex.buffers6() for ex in self.experts]
+        out, prob, topi, counts = be.moe_forward(x, self.gate.weight, self.gate.bias, experts,
+                                                 self.top_k, self.tile)
+        self.last_prob = prob
+        self.last_topi = topi
+        self._counts_dev = counts
+        return out
+
+    def routing_stats(self) -> dict:
+        counts = list(self.expert_token_counts)
+        total = sum(counts)
+        usage = [(c / total) if total else 0.0 for c in counts]
+        return {
+            "num_experts": self.num_experts,
+            "top_k": self.top_k,
+            "token_counts": counts,
+            "usage_frac": usage,
+            "executed": [c > 0 for c in counts],
+            "inactive_experts": sum(1 for c in counts if c == 0),
+            "max_usage_frac": max(usage) if usage else 0.0,
+        }
+
+    def reset_routing_stats(self) -> None:
+        self.last_prob = None
+        self.last_topi = None
+        self._counts_dev = None
+        self._counts_host = [0] * self.num_experts

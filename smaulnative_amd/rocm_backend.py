@@ -1,0 +1,307 @@
+"""The ``rocm`` compute backend: the reference backend surface on MI355X.
+
+Reference surface (kernel/compute.py:64-322, every call site in the reference):
+``name``, ``configure``, ``has_native`` / ``has_attn_native`` /
+``has_sparse_native``, ``fp8_forward``, ``fp8_backward_input``,
+``fp8_quantize_tiles``, ``attn_forward`` / ``attn_step`` / ``attn_backward``,
+``sparse_grad_v``.  This backend adds ``moe_forward`` (and its stages), the
+entry the MoE layer calls; the reference has no MoE hook because its routing
+is plain torch code inside SwiFFN_MoE.forward (model.py:557-585).
+
+Behaviour differences from the reference CPU backend, all deliberate:
+- nothing falls back: where the reference warns once and runs a torch
+  fallback (compute.py:134,137-143), this backend raises;
+- inputs must be HIP device tensors; work is enqueued on the current stream
+  and nothing synchronises;
+- ``fp8_forward`` also accepts bf16 ``x`` (fed to bf16 MFMA unchanged);
+  fp32 ``x`` is split into two bf16 terms inside the kernel;
+- training entry points (backward, quantizer, attention, sparse) are not part
+  of this path and raise ``NotImplementedError`` -- except
+  ``fp8_quantize_tiles``, whose contract lets it return ``None`` so the caller
+  runs the torch quantizer (compute.py:246-263, fp8_tile.py:96-113).
+"""
+from __future__ import annotations
+
+import os
+import threading
+from typing import Sequence
+
+import torch
+
+from smaulnative_amd import _lib
+
+_ACT = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
+
+
+def _stream_handle(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _need_device(name: str, *tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(f"{name}: rocm backend needs HIP device tensors, got {t.device}")
+    dev = tensors[0].device
+    for t in tensors[1:]:
+        if t is not None and t.device != dev:
+            raise RuntimeError(f"{name}: tensors are on different devices ({dev} vs {t.device})")
+
+
+class RocmBackend:
+    """MI355X backend over libsmaul_rocm.so (hand-written HIP for gfx950)."""
+
+    name = "rocm"
+
+    def __init__(self):
+        self._lock = threading.Lock()
+        self._ptr_cache: dict = {}
+
+    # ---- compute.py:77-103 ------------------------------------------------
+    def configure(self, threads=None):
+        """Host thread count for torch's CPU-side work; same rules as the reference."""
+        if threads is None:
+            env = os.environ.get("SMAUL_CPU_THREADS")
+            if env:
+                try:
+                    threads = int(float(env))
+                except (TypeError, ValueError):
+                    raise ValueError(f"SMAUL_CPU_THREADS must be an integer, got {env!r}")
+            else:
+                threads = max(1, (os.cpu_count() or 2) // 2)
+        try:
+            threads = int(threads)
+        except (TypeError, ValueError):
+            raise ValueError(f"threads must be an integer, got {threads!r}")
+        threads = max(1, threads)
+        os.environ["OMP_NUM_THREADS"] = str(threads)
+        os.environ["MKL_NUM_THREADS"] = str(threads)
+        torch.set_num_threads(threads)
+        try:
+            torch.set_num_interop_threads(1)
+        except RuntimeError:
+            pass
+        return threads
+
+    @property
+    def has_native(self):
+        try:
+            _lib.load()
+            return True
+        except _lib.LibraryMissing:
+            return False
+
+    @property
+    def has_attn_native(self):
+        return False
+
+    @property
+    def has_sparse_native(self):
+        return False
+
+    # ---- FP8 linear (compute.py:125-135, fp8_cpu.cpp:100-141) ---------------
+    def fp8_forward(self, x, w, s, in_f, out_f, tile):
+        """y[rows, out_f] fp32 = x[rows, in_f] . decode(w, s)^T on the HIP device."""
+        if tile <= 0 or in_f <= 0 or out_f <= 0:
+            raise ValueError(f"tile/in_f/out_f must be positive, got {tile}/{in_f}/{out_f}")
+        lib = _lib.load()
+        _need_device("fp8_forward", x, w, s)
+        if x.dtype not in _ACT:
+            raise RuntimeError(f"fp8_forward: x must be float32 or bfloat16, got {x.dtype}")
+        if w.dtype != torch.uint8:
+            raise RuntimeError(f"fp8_forward: w must be uint8, got {w.dtype}")
+        if x.dim() != 2 or x.shape[1] != in_f:
+            raise RuntimeError(f"fp8_forward: x must be [rows, in_f={in_f}], got {tuple(x.shape)}")
+        nt = (in_f + tile - 1) // tile
+        if w.numel() != out_f * in_f or s.numel() != out_f * nt:
+            raise RuntimeError(f"fp8_forward: size mismatch w={w.numel()} s={s.numel()} expected "
+                               f"{out_f * in_f} and {out_f * nt}")
+        if not ((w.dim() == 2 and tuple(w.shape) == (out_f, in_f)) or w.dim() == 1):
+            raise RuntimeError("fp8_forward: w must be [out_f, in_f] or flattened [out_f*in_f]")
+        if not ((s.dim() == 2 and tuple(s.shape) == (out_f, nt)) or s.dim() == 1):
+            raise RuntimeError("fp8_forward: s must be [out_f, nt] or flattened")
+        xc = x if x.is_contiguous() else x.contiguous()
+        wc = w.reshape(-1).contiguous()
+        sc = s.reshape(-1)
+        sc = (sc if sc.dtype == torch.float32 else sc.float()).contiguous()
+        rows = xc.shape[0]
+        y = torch.empty(rows, out_f, dtype=torch.float32, device=x.device)
+        if rows == 0:
+            return y
+        with torch.cuda.device(x.device):
+            rc = lib.smaul_fp8_linear(xc.data_ptr(), _ACT[xc.dtype], wc.data_ptr(), sc.data_ptr(),
+                                      y.data_ptr(), _lib.DTYPE_F32, rows, in_f, out_f, tile,
+                                      _stream_handle(x.device))
+        _lib.check(rc, "fp8_forward")
+        return y
+
+    def fp8_backward_input(self, g, w, s, in_f, out_f, tile):
+        raise NotImplementedError("rocm backend: fp8_backward_input (training) is not implemented")
+
+    def fp8_quantize_tiles(self, w32, tile):
+        """No device quantizer: returning None makes the caller run the torch path."""
+        return None
+
+    def attn_forward(self, Q, K, V, eps, need_den, need_state=False):
+        raise NotImplementedError("rocm backend: linear attention is not implemented")
+
+    def attn_step(self, S, z, q, k, v, eps):
+        raise NotImplementedError("rocm backend: linear attention is not implemented")
+
+    def attn_backward(self, dY, Q, K, V, Y, DEN, eps):
+        raise NotImplementedError("rocm backend: linear attention is not implemented")
+
+    def sparse_grad_v(self, dout, x, cols, values, budget=1 << 22):
+        raise NotImplementedError("rocm backend: sparse_grad_v is not implemented")
+
+    # ---- MoE (model.py:557-585) -------------------------------------------
+    def _expert_table(self, experts: Sequence[Sequence[torch.Tensor]], device, d, h, tile):
+        """Device int64 [6, E] table of the experts' buffer addresses.
+
+        Cached on the buffers' addresses and versions, so a requant or a
+        ``copy_`` into ``w8``/``sc`` (which bumps ``_version``) rebuilds it.
+        Non-fp32 scales (a model cast to bf16) are widened once and kept alive
+        by the cache entry.
+        """
+        key_parts = []
+        for ex in experts:
+            if len(ex) != 6:
+                raise ValueError("each expert is (gate_w8, gate_sc, up_w8, up_sc, down_w8, down_sc)")
+            for t in ex:
+                key_parts.append((t.data_ptr(), t._version, t.dtype))
+        key = (str(device), d, h, tile, tuple(key_parts))
+        hit = self._ptr_cache.get(key)
+        if hit is not None:
+            return hit[0]
+        nt_d = (d + tile - 1) // tile
+        nt_h = (h + tile - 1) // tile
+        keep = []
+        rows = [[] for _ in range(6)]
+        for e, (gw, gs, uw, us, dw, ds) in enumerate(experts):
+            for idx, (t, shape, is_code) in enumerate(((gw, (h, d), True), (gs, (h, nt_d), False),
+                                                       (uw, (h, d), True), (us, (h, nt_d), False),
+                                                       (dw, (d, h), True), (ds, (d, nt_h), False))):
+                _need_device("moe_forward", t)
+                if t.device != device:
+                    raise RuntimeError(f"moe_forward: expert {e} buffer on {t.device}, x on {device}")
+                if tuple(t.shape) != shape:
+                    raise RuntimeError(f"moe_forward: expert {e} buffer {idx} has shape {tuple(t.shape)}, "
+                                       f"expected {shape}")
+                if is_code:
+                    if t.dtype != torch.uint8:
+                        raise RuntimeError(f"moe_forward: expert {e} codes must be uint8")
+                    if not t.is_contiguous():
+                        raise RuntimeError(f"moe_forward: expert {e} codes must be contiguous")
+                    if t.data_ptr() % 16:
+                        raise RuntimeError(f"moe_forward: expert {e} codes must be 16-byte aligned")
+                    u = t
+                else:
+                    u = t if (t.dtype == torch.float32 and t.is_contiguous()) else t.float().contiguous()
+                    keep.append(u)
+                rows[idx].append(u.data_ptr())
+        table = torch.tensor(rows, dtype=torch.int64).to(device)
+        with self._lock:
+            if len(self._ptr_cache) > 64:
+                self._ptr_cache.clear()
+            self._ptr_cache[key] = (table, keep)
+        return table
+
+    def moe_router(self, x2, gate_w, gate_b, top_k):
+        """Router stage alone: (prob [T,E] fp32, topi [T,k] int64, topw [T,k] fp32)."""
+        lib = _lib.load()
+        T, d = x2.shape
+        E = gate_w.shape[0]
+        prob = torch.empty(T, E, dtype=torch.float32, device=x2.device)
+        topi = torch.empty(T, top_k, dtype=torch.int64, device=x2.device)
+        topw = torch.empty(T, top_k, dtype=torch.float32, device=x2.device)
+        gw = gate_w.detach().float().contiguous()
+        gb = None if gate_b is None else gate_b.detach().float().contiguous()
+        with torch.cuda.device(x2.device):
+            rc = lib.smaul_moe_router(x2.data_ptr(), _ACT[x2.dtype], gw.data_ptr(),
+                                      None if gb is None else gb.data_ptr(), prob.data_ptr(),
+                                      topi.data_ptr(), topw.data_ptr(), T, d, E, top_k,
+                                      _stream_handle(x2.device))
+        _lib.check(rc, "moe_router")
+        return prob, topi, topw
+
+    def moe_dispatch(self, topi, topw, num_experts, block_m=None):
+        """Dispatch stage alone: dict of counts/seg_off/tile_off/perm_row/perm_w/inv."""
+        lib = _lib.load()
+        T, k = topi.shape
+        E = int(num_experts)
+        if block_m is None:
+            block_m = lib.smaul_moe_block_m(T, k, E)
+        dev = topi.device
+        i32 = dict(dtype=torch.int32, device=dev)
+        out = {
+            "counts": torch.empty(E, **i32),
+            "seg_off": torch.empty(E + 1, **i32),
+            "tile_off": torch.empty(E + 1, **i32),
+            "perm_row": torch.empty(max(1, T * k), **i32),
+            "perm_w": torch.empty(max(1, T * k), dtype=torch.float32, device=dev),
+            "inv": torch.empty(max(1, T * k), **i32),
+        }
+        with torch.cuda.device(dev):
+            rc = lib.smaul_moe_dispatch(topi.contiguous().data_ptr(), topw.contiguous().data_ptr(),
+                                        out["counts"].data_ptr(), out["seg_off"].data_ptr(),
+                                        out["tile_off"].data_ptr(), out["perm_row"].data_ptr(),
+                                        out["perm_w"].data_ptr(), out["inv"].data_ptr(), T, E, k,
+                                        block_m, _stream_handle(dev))
+        _lib.check(rc, "moe_dispatch")
+        out["block_m"] = block_m
+        return out
+
+    def moe_forward(self, x, gate_w, gate_b, experts, top_k, tile):
+        """SwiFFN_MoE.forward on the device.
+
+        x: [..., d] bf16 or fp32; gate_w fp32 [E, d]; gate_b [E] or None;
+        experts: E tuples (gate_w8, gate_sc, up_w8, up_sc, down_w8, down_sc).
+        Returns (out [..., d] x.dtype, prob [..., E] fp32, topi [..., k] int64,
+        counts [E] int32 on the device).
+        """
+        lib = _lib.load()
+        _need_device("moe_forward", x, gate_w)
+        if x.dtype not in _ACT:
+            raise RuntimeError(f"moe_forward: x must be float32 or bfloat16, got {x.dtype}")
+        d = x.shape[-1]
+        E = len(experts)
+        if gate_w.dim() != 2 or tuple(gate_w.shape) != (E, d):
+            raise RuntimeError(f"moe_forward: gate weight must be [{E}, {d}], got {tuple(gate_w.shape)}")
+        if not 1 <= top_k <= E:
+            raise ValueError(f"top_k must be in [1, {E}], got {top_k}")
+        if tile <= 0:
+            raise ValueError(f"tile must be > 0, got {tile}")
+        h = experts[0][0].shape[0]
+        x2 = x.reshape(-1, d)
+        x2 = x2 if x2.is_contiguous() else x2.contiguous()
+        T = x2.shape[0]
+        dev = x.device
+        table = self._expert_table(experts, dev, d, h, tile)
+        gw = gate_w.detach()
+        gw = gw if (gw.dtype == torch.float32 and gw.is_contiguous()) else gw.float().contiguous()
+        gb = None
+        if gate_b is not None:
+            gb = gate_b.detach()
+            gb = gb if (gb.dtype == torch.float32 and gb.is_contiguous()) else gb.float().contiguous()
+        act = _ACT[x.dtype]
+        out = torch.empty_like(x2)
+        prob = torch.empty(T, E, dtype=torch.float32, device=dev)
+        topi = torch.empty(T, top_k, dtype=torch.int64, device=dev)
+        topw = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+        counts = torch.zeros(E, dtype=torch.int32, device=dev)
+        if T > 0:
+            ws_bytes = lib.smaul_moe_workspace_size(T, d, h, E, top_k, act)
+            if ws_bytes < 0:
+                raise ValueError("moe_forward: invalid sizes")
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            tp = table.data_ptr()
+            row = E * 8
+            with torch.cuda.device(dev):
+                rc = lib.smaul_moe_forward(
+                    x2.data_ptr(), act, gw.data_ptr(), None if gb is None else gb.data_ptr(),
+                    tp, tp + row, tp + 2 * row, tp + 3 * row, tp + 4 * row, tp + 5 * row,
+                    out.data_ptr(), prob.data_ptr(), topi.data_ptr(), topw.data_ptr(),
+                    counts.data_ptr(), ws.data_ptr(), ws_bytes, T, d, h, E, top_k, tile,
+                    _stream_handle(dev))
+            _lib.check(rc, "moe_forward")
+        lead = x.shape[:-1]
+        return (out.reshape(*lead, d), prob.reshape(*lead, E), topi.reshape(*lead, top_k), counts)

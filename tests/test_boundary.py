@@ -1,0 +1,130 @@
+"""CPU checks of the drop-in boundary: the C-ABI library and the Python backend surface.
+
+No compute call reaches a GPU here; these cover the library's exports, the
+host-side top-k order, argument validation and the no-fallback rule.
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from smaulnative_amd import _lib
+from smaulnative_amd.compute import get_backend, register_backend, registered
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "smaul_rocm.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(smaul_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    names = declared_symbols()
+    assert len(names) >= 10
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding covers the same set
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_library_version_and_error_channel():
+    lib = _lib.load()
+    assert lib.smaul_version() >= 100
+    assert isinstance(_lib.last_error(), str)
+
+
+def test_library_validates_without_touching_the_gpu():
+    lib = _lib.load()
+    # non-positive sizes are rejected before any launch
+    rc = lib.smaul_fp8_linear(None, 0, None, None, None, 0, 4, 0, 8, 64, None)
+    assert rc == _lib.SMAUL_ERR_INVALID and "positive" in _lib.last_error()
+    rc = lib.smaul_fp8_linear(None, 0, None, None, None, 0, 4, 64, 8, 48, None)
+    assert rc == _lib.SMAUL_ERR_UNSUPPORTED
+    rc = lib.smaul_moe_router(None, 1, None, None, None, None, None, 8, 64, 65, 2, None)
+    assert rc == _lib.SMAUL_ERR_INVALID
+    assert lib.smaul_moe_workspace_size(16384, 1024, 2560, 8, 2, 1) > 2 * 32768 * 2560
+
+
+def _host_topk(vals, k):
+    lib = _lib.load()
+    v = np.ascontiguousarray(vals, dtype=np.float32)
+    out = np.zeros(k, dtype=np.int64)
+    assert lib.smaul_selftest_topk(v.ctypes.data, v.size, k, out.ctypes.data) == 0
+    return out
+
+
+def test_router_topk_order_matches_torch_on_ties():
+    gen = torch.Generator().manual_seed(0)
+    for trial in range(3000):
+        n = int(torch.randint(1, 65, (1,), generator=gen))
+        k = int(torch.randint(1, n + 1, (1,), generator=gen))
+        if trial % 5 == 0:
+            n, k = 64, 1  # torch's partial_sort branch (k * 64 <= n)
+        mode = trial % 4
+        if mode == 0:
+            v = torch.randint(0, 3, (n,), generator=gen).float()
+        elif mode == 1:
+            v = torch.full((n,), 0.125)
+        elif mode == 2:
+            v = torch.rand(n, generator=gen)
+        else:
+            v = torch.randint(0, 4, (n,), generator=gen).float()
+            v[torch.rand(n, generator=gen) < 0.1] = float("nan")
+        ref = torch.topk(v, k, -1)[1].numpy()
+        assert np.array_equal(_host_topk(v.numpy(), k), ref), (n, k, v.tolist())
+
+
+def test_registry_contract():
+    be = get_backend()
+    assert be.name == "rocm" and "rocm" in registered()
+    with pytest.raises(ValueError, match="unknown compute backend"):
+        get_backend("cpu-fake")
+
+    class Other:
+        name = "other-test"
+    register_backend(Other())
+    assert get_backend("other-test").name == "other-test"
+
+
+def test_backend_surface_and_no_fallback():
+    be = get_backend("rocm")
+    for attr in ("configure", "fp8_forward", "fp8_backward_input", "fp8_quantize_tiles",
+                 "attn_forward", "attn_step", "attn_backward", "sparse_grad_v", "moe_forward"):
+        assert callable(getattr(be, attr)), attr
+    assert be.has_native is True
+    assert be.has_attn_native is False and be.has_sparse_native is False
+    assert be.configure(2) == 2
+    w = torch.zeros(8, 64, dtype=torch.uint8)
+    s = torch.ones(8, 1)
+    with pytest.raises(ValueError):
+        be.fp8_forward(torch.zeros(2, 64), w, s, 64, 8, 0)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        be.fp8_forward(torch.zeros(2, 64), w, s, 64, 8, 64)  # CPU tensors: raise, never fall back
+    with pytest.raises(NotImplementedError):
+        be.fp8_backward_input(torch.zeros(2, 8), w, s, 64, 8, 64)
+    assert be.fp8_quantize_tiles(torch.zeros(8, 64), 64) is None
+
+
+def test_fp8linear_and_moe_modules_on_cpu():
+    from smaulnative_amd import FP8Linear, MoEConfig, SwiFFN_MoE
+    m = FP8Linear(100, 40, 64)
+    assert m.w8.dtype == torch.uint8 and tuple(m.w8.shape) == (40, 100)
+    assert tuple(m.sc.shape) == (40, 2) and m.sc.dtype == torch.float32
+    with pytest.raises(RuntimeError, match="HIP device"):
+        m(torch.randn(3, 100))
+    with pytest.raises(ValueError):
+        SwiFFN_MoE(MoEConfig(d_model=64, num_experts=2, num_experts_per_tok=3))
+    moe = SwiFFN_MoE(MoEConfig(d_model=64, num_experts=4, num_experts_per_tok=2))
+    assert len(moe.experts) == 4 and moe.experts[0].gate.out_f == 160
+    assert moe.routing_stats()["token_counts"] == [0, 0, 0, 0]
+    with torch.no_grad(), pytest.raises(RuntimeError, match="HIP device"):
+        moe(torch.randn(1, 4, 64))
+    aux = moe.balance_loss(torch.full((8, 4), 0.25))
+    assert abs(float(aux) - 1.0) < 1e-6

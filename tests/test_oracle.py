@@ -1,0 +1,210 @@
+"""Pins the CPU oracle before anything is checked against it.
+
+Every function of oracle/ is checked here against (a) the golden vectors in
+tests/golden/ written from the reference itself (tests/golden/make_golden.py),
+(b) the reference's own fp8_cpu.cpp built under oracle/_ref where present, and
+(c) what the mathematics fixes (closed form of the codebook, brute-force
+x @ decode(W).T).  A planted mistake in the GEMM's rounding order is shown to
+fail the golden check, so the golden check can tell the two orders apart.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "golden_fp8_moe.npz")
+
+
+@pytest.fixture(scope="module")
+def g():
+    return np.load(GOLD)
+
+
+def _t(a):
+    return torch.from_numpy(np.array(a))
+
+
+def _bf(a):
+    return torch.from_numpy(np.array(a)).view(torch.bfloat16)
+
+
+# --------------------------------------------------------------------------
+# codebook
+# --------------------------------------------------------------------------
+def _closed_form(c):
+    e, m = (c >> 3) & 15, c & 7
+    s = -1.0 if c & 128 else 1.0
+    if e == 15 and m == 7:
+        return s * 448.0
+    if e == 0:
+        return s * m * 2.0 ** -9
+    return s * (1 + m / 8.0) * 2.0 ** (e - 7)
+
+
+def test_lut_closed_form_and_golden(g):
+    lut = oracle.e4m3_lut()
+    assert [float(v) for v in lut] == [_closed_form(c) for c in range(256)]
+    assert np.array_equal(lut.view(np.uint32), g["lut"].view(np.uint32))
+    assert np.array_equal(oracle.c_lut().view(np.uint32), g["lut"].view(np.uint32))
+    # reference conventions: 0x7E/0x7F = 448, 0xFE/0xFF = -448, 0x80 = -0
+    assert lut[0x7E] == lut[0x7F] == 448.0 and lut[0xFE] == lut[0xFF] == -448.0
+    assert lut[0x80] == 0.0 and np.signbit(lut[0x80])
+    # every value is exact in bf16 (3-bit mantissa, exponents 2^-9..2^8)
+    as_bf = torch.from_numpy(lut).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(as_bf, lut)
+
+
+def test_quant_tables_match_reference(g):
+    _, order, _, bounds = oracle.quant_tables()
+    assert np.array_equal(order.numpy(), g["order"])
+    assert np.array_equal(bounds.numpy().view(np.uint32), g["bounds"].view(np.uint32))
+
+
+# --------------------------------------------------------------------------
+# quantizer (oracle restatement and the product's own weight-prep quantizer)
+# --------------------------------------------------------------------------
+QCASES = ["uniform", "tiny", "huge", "zeros", "half_zero", "codebook", "midpoints", "saturating",
+          "subnormal", "odd_shape", "padded_tile", "nonfinite"]
+
+
+@pytest.mark.parametrize("tile", [32, 64, 128])
+@pytest.mark.parametrize("name", QCASES)
+def test_quantize_matches_golden(g, name, tile):
+    import warnings
+    w = _t(g[f"q_{name}_w"])
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        codes, sc = oracle.quantize_tiles(w.clone(), tile)
+        from smaulnative_amd.fp8_tile import quantize_tiles as prod_quantize
+        pc, ps = prod_quantize(w.clone(), tile)
+    assert np.array_equal(codes.numpy(), g[f"q_{name}_t{tile}_codes"])
+    assert np.array_equal(sc.numpy().view(np.uint32), g[f"q_{name}_t{tile}_sc"].view(np.uint32))
+    assert torch.equal(pc, codes) and torch.equal(ps, sc)
+
+
+# --------------------------------------------------------------------------
+# fp8 GEMM (C restatement of fp8_cpu.cpp)
+# --------------------------------------------------------------------------
+def test_fp8_forward_bit_exact_with_golden(g):
+    for i, (rows, in_f, out_f, tile) in enumerate(g["gemm_shapes"].tolist()):
+        x, w, s = _t(g[f"gemm{i}_x"]), _t(g[f"gemm{i}_w"]), _t(g[f"gemm{i}_s"])
+        y = oracle.fp8_forward(x, w, s, in_f, out_f, tile)
+        assert np.array_equal(y.numpy().view(np.uint32), g[f"gemm{i}_y"].view(np.uint32)), (rows, in_f, out_f)
+
+
+def test_fp8_forward_matches_bruteforce():
+    # test_linear_fp8.py:170-183 shapes: forward vs x @ decode(W).T, rel < 1e-5
+    for in_f, out_f, rows in [(128, 64, 9), (100, 70, 5), (65, 65, 33), (512, 256, 64)]:
+        torch.manual_seed(0)
+        w, s = oracle.quantize_tiles(torch.randn(out_f, in_f) * 0.05, 64)
+        x = torch.randn(rows, in_f)
+        y = oracle.fp8_forward(x, w, s, in_f, out_f, 64)
+        ref = x.double() @ oracle.decode_full(w, s, 64).double().T
+        rel = float((y.double() - ref).abs().max() / ref.abs().max())
+        assert rel < 1e-5, (in_f, out_f, rows, rel)
+
+
+def test_fp8_forward_threads_do_not_change_bits():
+    torch.manual_seed(3)
+    w, s = oracle.quantize_tiles(torch.randn(200, 192) * 0.02, 64)
+    x = torch.randn(77, 192)
+    a = oracle.fp8_forward(x, w, s, 192, 200, 64, threads=1)
+    b = oracle.fp8_forward(x, w, s, 192, 200, 64, threads=8)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.skipif(oracle.ref_module() is None, reason="oracle/_ref (reference build) not present")
+@pytest.mark.parametrize("rows,in_f,out_f,tile", [(33, 100, 65, 64), (64, 128, 128, 64), (5, 70, 100, 32),
+                                                  (96, 256, 192, 128), (64, 64, 64, 16), (130, 640, 96, 64)])
+def test_fp8_forward_bit_exact_with_reference_build(rows, in_f, out_f, tile):
+    torch.manual_seed(rows + in_f)
+    x = torch.randn(rows, in_f)
+    w, s = oracle.quantize_tiles(torch.randn(out_f, in_f) * 0.02, tile)
+    assert torch.equal(oracle.fp8_forward(x, w, s, in_f, out_f, tile),
+                       oracle.fp8_forward_ref(x, w, s, in_f, out_f, tile))
+
+
+def _numpy_gemm(x, w, s, tile, fast_order):
+    """A float32 numpy GEMM with one rounding order for every K block."""
+    lut = oracle.e4m3_lut()
+    xs, ws, ss = x.numpy(), w.numpy(), s.numpy()
+    rows, in_f = xs.shape
+    out_f = ws.shape[0]
+    acc = np.zeros((rows, out_f), dtype=np.float32)
+    for k in range(in_f):
+        col = lut[ws[:, k]]
+        sk = ss[:, k // tile]
+        if fast_order:
+            p = xs[:, k:k + 1] * (col * sk)[None, :]
+        else:
+            p = (xs[:, k:k + 1] * col[None, :]) * sk[None, :]
+        acc = (acc + p.astype(np.float32)).astype(np.float32)
+    return acc
+
+
+def test_golden_gemm_distinguishes_rounding_orders(g):
+    # golden shape 1 is 64x128 -> 128: every task is on the reference's fast
+    # path, x*(lut*s).  The planted mistake (x*lut)*s must NOT reproduce it.
+    i = 1
+    x, w, s = _t(g[f"gemm{i}_x"]), _t(g[f"gemm{i}_w"]), _t(g[f"gemm{i}_s"])
+    good = _numpy_gemm(x, w, s, 64, fast_order=True)
+    bad = _numpy_gemm(x, w, s, 64, fast_order=False)
+    gold = g[f"gemm{i}_y"]
+    assert np.array_equal(good.view(np.uint32), gold.view(np.uint32))
+    assert not np.array_equal(bad.view(np.uint32), gold.view(np.uint32))
+
+
+# --------------------------------------------------------------------------
+# MoE forward (router, top-k ties, w>0 mask, combine order, dtype rounding)
+# --------------------------------------------------------------------------
+MOE_CASES = ["moe_e4k2_f32", "moe_e4k2_bf16", "moe_e8k3_bf16", "moe_e8k2_bf16", "moe_tie_uniform",
+             "moe_tie_underflow", "moe_zero_weight"]
+
+
+def load_moe_case(g, tag):
+    d, E, k, tile, h = g[f"{tag}_meta"].tolist()
+    is_bf16 = int(g[f"{tag}_dtype"][0]) == 1
+    x = _bf(g[f"{tag}_x"]) if is_bf16 else _t(g[f"{tag}_x"])
+    experts = []
+    for e in range(E):
+        parts = []
+        for nm in ("gate", "up", "down"):
+            parts += [_t(g[f"{tag}_e{e}_{nm}_w"]), _t(g[f"{tag}_e{e}_{nm}_s"])]
+        experts.append(oracle.ExpertWeights(*parts))
+    out = _bf(g[f"{tag}_out"]) if is_bf16 else _t(g[f"{tag}_out"])
+    return dict(d=d, E=E, k=k, tile=tile, h=h, x=x, gate_w=_t(g[f"{tag}_gate_w"]), experts=experts,
+                out=out, prob=_t(g[f"{tag}_prob"]), topi=_t(g[f"{tag}_topi"]),
+                counts=g[f"{tag}_counts"].tolist(), executed=[bool(v) for v in g[f"{tag}_executed"]])
+
+
+@pytest.mark.parametrize("tag", MOE_CASES)
+def test_moe_oracle_matches_golden(g, tag):
+    c = load_moe_case(g, tag)
+    r = oracle.moe_forward(c["x"], c["gate_w"], None, c["experts"], c["k"], c["tile"])
+    assert torch.equal(r.topi, c["topi"]), tag
+    assert r.counts == c["counts"] and r.executed == c["executed"]
+    assert torch.equal(r.prob, c["prob"]), tag
+    assert torch.equal(r.out.view(torch.int16) if r.out.dtype == torch.bfloat16 else r.out,
+                       c["out"].view(torch.int16) if c["out"].dtype == torch.bfloat16 else c["out"]), tag
+
+
+def test_moe_oracle_perm_is_ascending_and_complete(g):
+    c = load_moe_case(g, "moe_e8k3_bf16")
+    r = oracle.moe_forward(c["x"], c["gate_w"], None, c["experts"], c["k"], c["tile"])
+    T = c["x"].numel() // c["d"]
+    for e, p in enumerate(r.perm):
+        assert torch.equal(p, torch.sort(p).values)
+        brute = [t for t in range(T) for j in range(c["k"])
+                 if int(r.topi.reshape(T, -1)[t, j]) == e and float(r.topw.reshape(T, -1)[t, j]) > 0]
+        assert p.tolist() == brute
+
+
+def test_zero_weight_slot_is_not_dispatched(g):
+    # k=3 picks an expert whose probability underflowed to 0: it is in topi
+    # but has weight 0, so it is not counted or executed (model.py:576).
+    c = load_moe_case(g, "moe_zero_weight")
+    assert c["topi"].reshape(-1, 3)[0].tolist() == [0, 4, 6]
+    assert c["counts"] == [4, 0, 0, 0, 4, 0, 0, 0]
