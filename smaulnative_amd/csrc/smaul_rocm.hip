@@ -562,8 +562,13 @@ dispatch_kernel(const int64_t* __restrict__ topi, const float* __restrict__ topw
   __syncthreads();
   // pass 1: histogram (integer LDS atomics: order does not matter)
   for (int64_t t = tid; t < T; t += DISPATCH_THREADS) {
+    uint64_t seen = 0;
     for (int j = 0; j < k; ++j) {
-      if (topw[t * k + j] > 0.0f) atomicAdd(&s_cnt[(int)topi[t * k + j]], 1);
+      const int64_t ee = topi[t * k + j];
+      if (topw[t * k + j] > 0.0f && ee >= 0 && ee < E && !((seen >> ee) & 1ull)) {
+        seen |= 1ull << ee;
+        atomicAdd(&s_cnt[(int)ee], 1);
+      }
     }
   }
   __syncthreads();
@@ -599,10 +604,15 @@ dispatch_kernel(const int64_t* __restrict__ topi, const float* __restrict__ topw
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         if (j < k) {
+          // a slot is dispatched when its weight is positive (model.py:576);
+          // out-of-range ids and repeats of an expert already in the row are
+          // not (the router never produces either)
           const float w = topw[t * k + j];
-          ej[j] = (int)topi[t * k + j];
-          on[j] = w > 0.0f;
-          if (on[j]) sel |= 1ull << ej[j];
+          const int64_t ee = topi[t * k + j];
+          const bool ok = w > 0.0f && ee >= 0 && ee < E && !((sel >> ee) & 1ull);
+          ej[j] = ok ? (int)ee : -1;
+          on[j] = ok;
+          if (ok) sel |= 1ull << ee;
           else inv[t * k + j] = -1;
         }
       }

@@ -250,6 +250,59 @@ class RocmBackend:
         out["block_m"] = block_m
         return out
 
+    def moe_stages(self, x2, gate_w, gate_b, experts, top_k, tile, events=None):
+        """The MoE layer as its five stages, each through its own C-ABI entry.
+
+        Same results as ``moe_forward`` (which runs the same kernels from one
+        call).  ``events``, if given, is a list of 6 ``torch.cuda.Event``
+        recorded on the current stream before the router and after each stage
+        (router, dispatch, gate_up, down, combine), for per-kernel timing.
+        Returns (out [T,d], prob, topi, topw, dispatch dict).
+        """
+        lib = _lib.load()
+        T, d = x2.shape
+        E = len(experts)
+        h = experts[0][0].shape[0]
+        dev = x2.device
+        act = _ACT[x2.dtype]
+        table = self._expert_table(experts, dev, d, h, tile)
+        gw = gate_w.detach().float().contiguous()
+        gb = None if gate_b is None else gate_b.detach().float().contiguous()
+        R = T * top_k
+        bm = lib.smaul_moe_block_m(T, top_k, E)
+        max_tiles = (R + bm - 1) // bm + E
+        hdn = torch.empty(max(1, R), h, dtype=x2.dtype, device=dev)
+        yperm = torch.empty(max(1, R), d, dtype=x2.dtype, device=dev)
+        out = torch.empty_like(x2)
+        stream = torch.cuda.current_stream(dev)
+        rec = (lambda i: events[i].record(stream)) if events else (lambda i: None)
+        tp = table.data_ptr()
+        row = E * 8
+        with torch.cuda.device(dev):
+            rec(0)
+            prob, topi, topw = self.moe_router(x2, gw, gb, top_k)
+            rec(1)
+            disp = self.moe_dispatch(topi, topw, E, bm)
+            rec(2)
+            sh = stream.cuda_stream
+            rc = lib.smaul_moe_gate_up(x2.data_ptr(), act, disp["perm_row"].data_ptr(), tp, tp + row,
+                                       tp + 2 * row, tp + 3 * row, hdn.data_ptr(), disp["seg_off"].data_ptr(),
+                                       disp["tile_off"].data_ptr(), max_tiles, E, d, h, tile, bm, sh)
+            _lib.check(rc, "moe_gate_up")
+            rec(3)
+            rc = lib.smaul_moe_down(hdn.data_ptr(), act, tp + 4 * row, tp + 5 * row, yperm.data_ptr(),
+                                    disp["seg_off"].data_ptr(), disp["tile_off"].data_ptr(), max_tiles, E, d,
+                                    h, tile, bm, sh)
+            _lib.check(rc, "moe_down")
+            rec(4)
+            rc = lib.smaul_moe_combine(yperm.data_ptr(), act, topi.data_ptr(), topw.data_ptr(),
+                                       disp["inv"].data_ptr(), out.data_ptr(), T, d, top_k, sh)
+            _lib.check(rc, "moe_combine")
+            rec(5)
+        disp["hdn"] = hdn
+        disp["yperm"] = yperm
+        return out, prob, topi, topw, disp
+
     def moe_forward(self, x, gate_w, gate_b, experts, top_k, tile):
         """SwiFFN_MoE.forward on the device.
 
@@ -287,7 +340,9 @@ class RocmBackend:
         prob = torch.empty(T, E, dtype=torch.float32, device=dev)
         topi = torch.empty(T, top_k, dtype=torch.int64, device=dev)
         topw = torch.empty(T, top_k, dtype=torch.float32, device=dev)
-        counts = torch.zeros(E, dtype=torch.int32, device=dev)
+        # the dispatch kernel writes every count; no fill, so the call can be graph-captured
+        counts = torch.empty(E, dtype=torch.int32, device=dev) if T > 0 else \
+            torch.zeros(E, dtype=torch.int32, device=dev)
         if T > 0:
             ws_bytes = lib.smaul_moe_workspace_size(T, d, h, E, top_k, act)
             if ws_bytes < 0:

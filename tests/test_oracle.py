@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import oracle
+from _cases import load_moe_case
 
 GOLD = os.path.join(os.path.dirname(__file__), "golden", "golden_fp8_moe.npz")
 
@@ -162,22 +163,6 @@ def test_golden_gemm_distinguishes_rounding_orders(g):
 # --------------------------------------------------------------------------
 MOE_CASES = ["moe_e4k2_f32", "moe_e4k2_bf16", "moe_e8k3_bf16", "moe_e8k2_bf16", "moe_tie_uniform",
              "moe_tie_underflow", "moe_zero_weight"]
-
-
-def load_moe_case(g, tag):
-    d, E, k, tile, h = g[f"{tag}_meta"].tolist()
-    is_bf16 = int(g[f"{tag}_dtype"][0]) == 1
-    x = _bf(g[f"{tag}_x"]) if is_bf16 else _t(g[f"{tag}_x"])
-    experts = []
-    for e in range(E):
-        parts = []
-        for nm in ("gate", "up", "down"):
-            parts += [_t(g[f"{tag}_e{e}_{nm}_w"]), _t(g[f"{tag}_e{e}_{nm}_s"])]
-        experts.append(oracle.ExpertWeights(*parts))
-    out = _bf(g[f"{tag}_out"]) if is_bf16 else _t(g[f"{tag}_out"])
-    return dict(d=d, E=E, k=k, tile=tile, h=h, x=x, gate_w=_t(g[f"{tag}_gate_w"]), experts=experts,
-                out=out, prob=_t(g[f"{tag}_prob"]), topi=_t(g[f"{tag}_topi"]),
-                counts=g[f"{tag}_counts"].tolist(), executed=[bool(v) for v in g[f"{tag}_executed"]])
 
 
 @pytest.mark.parametrize("tag", MOE_CASES)
