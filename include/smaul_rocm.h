@@ -38,6 +38,11 @@ enum {
 
 enum { SMAUL_DTYPE_F32 = 0, SMAUL_DTYPE_BF16 = 1 };
 
+/* flags: SMAUL_FLAG_CANONICAL_CODES promises that the code buffers contain no
+ * 0x7F/0xFF bytes (see smaul_fp8_canonicalize), which lets the GEMMs skip
+ * rewriting them on the fly.  Results are identical either way. */
+enum { SMAUL_FLAG_CANONICAL_CODES = 1 };
+
 /* Library version as an integer (major*10000 + minor*100 + patch). */
 int smaul_version(void);
 
@@ -50,12 +55,22 @@ const char* smaul_last_error(void);
  *   kernel/compute.py:125-135 (CpuBackend.fp8_forward) and
  *   kernel/fp8_cpu.cpp:100-141 (native fp8_forward).
  * x: x_dtype [rows, in_f] row-major; w: uint8 [out_f, in_f]; s: fp32
- * [out_f, ceil(in_f/tile)]; y: y_dtype [rows, out_f].  tile must be a
- * positive multiple of 32 (SMAUL_ERR_UNSUPPORTED otherwise).  rows may be 0.
+ * [out_f, ceil(in_f/tile)]; y: y_dtype [rows, out_f].  tile must be 32 or a
+ * multiple of 64 (SMAUL_ERR_UNSUPPORTED otherwise).  rows may be 0.
  */
 int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* s,
                      void* y, int y_dtype, int64_t rows, int64_t in_f, int64_t out_f,
-                     int64_t tile, hipStream_t stream);
+                     int64_t tile, int flags, hipStream_t stream);
+
+/*
+ * Device repack cache of the codes: out = codes with 0x7F -> 0x7E and
+ * 0xFF -> 0xFE (the same values, +-448, in the reference codebook
+ * kernel/fp8_tile.py:43-44; 0x7F/0xFF are NaN in the OCP E4M3FN encoding the
+ * gfx950 converters implement).  No reference counterpart: the stored w8
+ * buffers are never modified, this writes a separate cached copy.  Both
+ * buffers 16-byte aligned.
+ */
+int smaul_fp8_canonicalize(const uint8_t* codes, uint8_t* out, int64_t n, hipStream_t stream);
 
 /*
  * MoE router: logits = x . gate_w^T (+ gate_b), prob = softmax(logits),
@@ -102,19 +117,19 @@ int smaul_moe_dispatch(const int64_t* topi, const float* topw, int32_t* counts,
  * seg_off/tile_off come from smaul_moe_dispatch with block_m = smaul_moe_block_m().
  * max_tiles is an upper bound on tile_off[E] (ceil(T*k/block_m) + E).
  */
-int smaul_moe_block_m(int64_t T, int64_t k, int64_t E);
+int smaul_moe_block_m(int64_t T, int64_t k, int64_t E, int act_dtype);
 
 int smaul_moe_gate_up(const void* x, int act_dtype, const int32_t* perm_row,
                       const uint8_t* const* gate_w, const float* const* gate_s,
                       const uint8_t* const* up_w, const float* const* up_s,
                       void* hdn, const int32_t* seg_off, const int32_t* tile_off,
                       int64_t max_tiles, int64_t E, int64_t d, int64_t h, int64_t tile,
-                      int64_t block_m, hipStream_t stream);
+                      int64_t block_m, int flags, hipStream_t stream);
 
 int smaul_moe_down(const void* hdn, int act_dtype, const uint8_t* const* down_w,
                    const float* const* down_s, void* yperm, const int32_t* seg_off,
                    const int32_t* tile_off, int64_t max_tiles, int64_t E, int64_t d,
-                   int64_t h, int64_t tile, int64_t block_m, hipStream_t stream);
+                   int64_t h, int64_t tile, int64_t block_m, int flags, hipStream_t stream);
 
 /*
  * Combine: out[t] = cast( sum over t's dispatched experts in ascending expert
@@ -143,7 +158,7 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
                       void* out, float* prob, int64_t* topi, float* topw, int32_t* counts,
                       void* workspace, int64_t workspace_bytes,
                       int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile,
-                      hipStream_t stream);
+                      int flags, hipStream_t stream);
 
 /*
  * Host-side self-test of the top-k selection order used by the router (no GPU

@@ -19,6 +19,7 @@ SMAUL_ERR_UNSUPPORTED = 2
 SMAUL_ERR_HIP = 3
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+FLAG_CANONICAL_CODES = 1
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -28,17 +29,18 @@ _I = ctypes.c_int
 SIGNATURES = {
     "smaul_version": (_I, []),
     "smaul_last_error": (ctypes.c_char_p, []),
-    "smaul_fp8_linear": (_I, [_P, _I, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _P]),
+    "smaul_fp8_linear": (_I, [_P, _I, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I, _P]),
+    "smaul_fp8_canonicalize": (_I, [_P, _P, _I64, _P]),
     "smaul_moe_router": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "smaul_moe_dispatch": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
-    "smaul_moe_block_m": (_I, [_I64, _I64, _I64]),
+    "smaul_moe_block_m": (_I, [_I64, _I64, _I64, _I]),
     "smaul_moe_gate_up": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
-                               _I64, _I64, _P]),
-    "smaul_moe_down": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+                               _I64, _I64, _I, _P]),
+    "smaul_moe_down": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P]),
     "smaul_moe_combine": (_I, [_P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "smaul_moe_workspace_size": (_I64, [_I64, _I64, _I64, _I64, _I64, _I]),
     "smaul_moe_forward": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                               _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+                               _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P]),
     "smaul_selftest_topk": (_I, [_P, _I64, _I64, _P]),
 }
 

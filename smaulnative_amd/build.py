@@ -9,6 +9,9 @@ Flags:
   the reference's rounding (model.py:582).
 - ``-Xclang -target-feature -Xclang -packed-fp32-ops``: no packed fp32 VALU
   instructions in generated code.
+- ``-mllvm -amdgpu-mfma-vgpr-form``: MFMA results in ordinary VGPRs.  The
+  GEMM scales every MFMA partial with a VALU fma; with the results in AGPRs
+  each of those would need two extra v_accvgpr moves.
 """
 from __future__ import annotations
 
@@ -26,6 +29,7 @@ HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I" + os.path.join(REPO, "include"), "-I" + os.path.join(HERE, "csrc"),
 ]
 

@@ -77,8 +77,10 @@ __device__ __forceinline__ uint32_t canon4(uint32_t w) {
 }
 
 // 4 E4M3 codes (bytes 0..3 of w) -> 4 bf16 packed in two dwords, exact.
+// CANON: the codes are already canonical (no 0x7F/0xFF bytes).
+template <bool CANON>
 __device__ __forceinline__ void decode4(uint32_t w, uint32_t& lo, uint32_t& hi) {
-  w = canon4(w);
+  if constexpr (!CANON) w = canon4(w);
   bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
   bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
   lo = __builtin_bit_cast(uint32_t, a);
@@ -114,33 +116,43 @@ struct GemmArgs {
   int E;
 };
 
-template <int BM, int BNO, int WM, int WN, bool SWIGLU, int NSPLIT, bool OUT_BF16, bool VEC>
+// KMODE: how scale tiles line up with the 64-wide K stages.
+//   0: tile == 32   (two scale tiles per stage, one MFMA each)
+//   1: tile == 64   (one scale tile per stage)
+//   2: tile == 64*m (a scale tile spans m stages; the partial carries over)
+template <int BM, int BNB, int WM, int WN, bool SWIGLU, int NSPLIT>
 struct GemmCfg {
   static constexpr int NT = WM * WN * 64;
-  static constexpr int NB = SWIGLU ? 2 * BNO : BNO;  // staged weight rows
-  static constexpr int TM = BM / WM;
-  static constexpr int TNO = BNO / WN;
+  static constexpr int BNO = SWIGLU ? BNB / 2 : BNB;   // output columns per workgroup
+  static constexpr int TM = BM / WM;                   // rows per wave
+  static constexpr int TNB = BNB / WN;                 // staged weight rows per wave
+  static constexpr int TNO = SWIGLU ? TNB / 2 : TNB;   // output columns per wave
   static constexpr int FM = TM / 16;
-  static constexpr int FN = TNO / 16;                  // output col tiles per wave
-  static constexpr int NJ = SWIGLU ? 2 * FN : FN;      // weight col tiles per wave
+  static constexpr int NJ = TNB / 16;                  // 16-wide weight tiles per wave
+  static constexpr int FN = TNO / 16;                  // 16-wide output tiles per wave
   static constexpr int LDK = 64 + 8;                   // padded LDS row (bf16 elements)
+  static constexpr int A_PER_ROW = NSPLIT == 1 ? 8 : 16;   // 16-byte chunks per 64-K row
+  static constexpr int A_CH = BM * A_PER_ROW / NT;
+  static constexpr int B_CH = BNB * 4 / NT;
   static_assert(TM % 16 == 0 && TNO % 16 == 0, "wave tile must be a multiple of 16");
-  // staging chunk counts per thread
-  static constexpr int A_CH = NSPLIT == 1 ? (BM * 8) / NT : (BM * 16) / NT;
-  static constexpr int B_CH = (NB * 4) / NT;
-  static_assert(A_CH >= 1 && (NSPLIT == 1 ? BM * 8 : BM * 16) % NT == 0, "A staging split");
-  static_assert(B_CH >= 1 && (NB * 4) % NT == 0, "B staging split");
+  static_assert(A_CH >= 1 && (BM * A_PER_ROW) % NT == 0, "A staging split");
+  static_assert(B_CH >= 1 && (BNB * 4) % NT == 0, "B staging split");
 };
 
-template <int BM, int BNO, int WM, int WN, bool SWIGLU, int NSPLIT, bool OUT_BF16, bool VEC>
+template <int BM, int BNB, int WM, int WN, bool SWIGLU, int NSPLIT, bool OUT_BF16, int KMODE,
+          bool CANON, bool VEC>
 __global__ void __launch_bounds__(WM * WN * 64)
 fp8_gemm_kernel(GemmArgs p) {
-  using C = GemmCfg<BM, BNO, WM, WN, SWIGLU, NSPLIT, OUT_BF16, VEC>;
-  constexpr int NT = C::NT, NB = C::NB, TM = C::TM, TNO = C::TNO, FM = C::FM, FN = C::FN,
-                NJ = C::NJ, LDK = C::LDK;
+  using C = GemmCfg<BM, BNB, WM, WN, SWIGLU, NSPLIT>;
+  constexpr int NT = C::NT, BNO = C::BNO, TM = C::TM, TNO = C::TNO, FM = C::FM, NJ = C::NJ,
+                FN = C::FN, LDK = C::LDK, A_PER_ROW = C::A_PER_ROW, A_CH = C::A_CH,
+                B_CH = C::B_CH;
+  constexpr int SPS = KMODE == 0 ? 2 : 1;   // scale rows per stage
+  constexpr int A_ELEMS = 64 / A_PER_ROW;
 
   __shared__ __attribute__((aligned(16))) uint16_t sA[2][NSPLIT][BM][LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[2][NB][LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[2][BNB][LDK];
+  __shared__ float sS[2][SPS][BNB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -166,72 +178,76 @@ fp8_gemm_kernel(GemmArgs p) {
 
   const uint8_t* W1 = p.wp ? p.wp[e] : p.w + e * p.w_estride;
   const float* S1 = p.sp ? p.sp[e] : p.s + e * p.s_estride;
-  const uint8_t* W2 = nullptr;
-  const float* S2 = nullptr;
+  const uint8_t* W2 = W1;
+  const float* S2 = S1;
   if constexpr (SWIGLU) {
     W2 = p.wp2 ? p.wp2[e] : p.w2 + e * p.w_estride;
     S2 = p.sp2 ? p.sp2[e] : p.s2 + e * p.s_estride;
   }
 
   // ---- per-thread staging assignments --------------------------------------
-  // A: chunk c -> (row, k offset); bf16: 8 chunks of 8 elements per 64-K row,
-  // fp32: 16 chunks of 4 elements.
-  constexpr int A_PER_ROW = NSPLIT == 1 ? 8 : 16;
-  constexpr int A_ELEMS = 64 / A_PER_ROW;
-  const char* arow[C::A_CH];
-  int akoff[C::A_CH], arl[C::A_CH];
+  const char* arow[A_CH];
+  int akoff[A_CH], arl[A_CH];
 #pragma unroll
-  for (int i = 0; i < C::A_CH; ++i) {
+  for (int i = 0; i < A_CH; ++i) {
     const int c = tid + i * NT;
     const int r = c / A_PER_ROW;
     arl[i] = r;
     akoff[i] = (c % A_PER_ROW) * A_ELEMS;
-    if (r < rows_here) {
-      const int64_t lr = row0 + r;
-      const int64_t xr = p.row_idx ? (int64_t)p.row_idx[lr] : lr;
-      arow[i] = (const char*)p.x + xr * p.ldx * (NSPLIT == 1 ? 2 : 4);
-    } else {
-      arow[i] = nullptr;
-    }
+    // Rows past the segment end load a valid row of the segment instead: MFMA
+    // output rows depend only on their own A row, and those rows are never
+    // stored, so the staging loop needs no branch.
+    const int64_t lr = row0 + (r < rows_here ? r : rows_here - 1);
+    const int64_t xr = p.row_idx ? (int64_t)p.row_idx[lr] : lr;
+    arow[i] = (const char*)p.x + xr * p.ldx * (NSPLIT == 1 ? 2 : 4);
   }
-  // B: chunk c -> (staged weight row, k offset), 4 chunks of 16 codes per row.
-  const uint8_t* brow[C::B_CH];
-  int bkoff[C::B_CH], brl[C::B_CH];
+  const uint8_t* brow[B_CH];
+  int bkoff[B_CH], brl[B_CH];
 #pragma unroll
-  for (int i = 0; i < C::B_CH; ++i) {
+  for (int i = 0; i < B_CH; ++i) {
     const int c = tid + i * NT;
     const int r = c >> 2;
     brl[i] = r;
     bkoff[i] = (c & 3) * 16;
-    int64_t col;
-    const uint8_t* base;
-    if (SWIGLU && r >= BNO) {
-      col = n0 + (r - BNO);
-      base = W2;
-    } else {
-      col = n0 + r;
-      base = W1;
-    }
-    brow[i] = col < N ? base + col * K : nullptr;
+    const bool up = SWIGLU && r >= BNO;
+    int64_t col = n0 + (up ? r - BNO : r);
+    if (col >= N) col = N - 1;  // columns past N are computed but never stored
+    brow[i] = (up ? W2 : W1) + col * K;
   }
-
-  // staging registers
-  uint4 ra[C::A_CH];
-  uint4 rb[C::B_CH];
-
-  auto load_stage = [&](int64_t k0) {
+  // scale staging: slot q = tid + i*NT < SPS * BNB owns (sub, column)
+  constexpr int S_CH = (SPS * BNB + NT - 1) / NT;
+  const float* srow[S_CH];
+  int s_sub[S_CH], s_col[S_CH];
+  bool s_own[S_CH];
 #pragma unroll
-    for (int i = 0; i < C::A_CH; ++i) {
+  for (int i = 0; i < S_CH; ++i) {
+    const int q = tid + i * NT;
+    s_own[i] = q < SPS * BNB;
+    s_sub[i] = (q / BNB) % SPS;
+    s_col[i] = q % BNB;
+    const bool up = SWIGLU && s_col[i] >= BNO;
+    int64_t col = n0 + (up ? s_col[i] - BNO : s_col[i]);
+    if (col >= N) col = N - 1;
+    srow[i] = (up ? S2 : S1) + col * nt;
+  }
+  // K % 64 == 0: every stage is full and the loads need no K guard
+  const bool full_k = (K & 63) == 0;
+
+  uint4 ra[A_CH];
+  uint4 rb[B_CH];
+  float rs[S_CH];
+
+  auto load_stage = [&](int64_t kt) {
+    const int64_t k0 = kt * 64;
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
       const int64_t kk = k0 + akoff[i];
       if constexpr (VEC) {
-        if (arow[i] && kk < K) {
-          ra[i] = *(const uint4*)(arow[i] + kk * (NSPLIT == 1 ? 2 : 4));
-        } else {
-          ra[i] = make_uint4(0, 0, 0, 0);
-        }
+        ra[i] = (full_k || kk < K) ? *(const uint4*)(arow[i] + kk * (NSPLIT == 1 ? 2 : 4))
+                                   : make_uint4(0, 0, 0, 0);
       } else {
         uint32_t v[4] = {0, 0, 0, 0};
-        if (arow[i]) {
+        {
           if constexpr (NSPLIT == 1) {
             const uint16_t* src = (const uint16_t*)arow[i];
 #pragma unroll
@@ -248,17 +264,13 @@ fp8_gemm_kernel(GemmArgs p) {
       }
     }
 #pragma unroll
-    for (int i = 0; i < C::B_CH; ++i) {
+    for (int i = 0; i < B_CH; ++i) {
       const int64_t kk = k0 + bkoff[i];
       if constexpr (VEC) {
-        if (brow[i] && kk < K) {
-          rb[i] = *(const uint4*)(brow[i] + kk);
-        } else {
-          rb[i] = make_uint4(0, 0, 0, 0);
-        }
+        rb[i] = (full_k || kk < K) ? *(const uint4*)(brow[i] + kk) : make_uint4(0, 0, 0, 0);
       } else {
         uint32_t v[4] = {0, 0, 0, 0};
-        if (brow[i]) {
+        {
 #pragma unroll
           for (int q = 0; q < 16; ++q)
             if (kk + q < K) v[q >> 2] |= (uint32_t)brow[i][kk + q] << ((q & 3) * 8);
@@ -266,11 +278,19 @@ fp8_gemm_kernel(GemmArgs p) {
         rb[i] = make_uint4(v[0], v[1], v[2], v[3]);
       }
     }
+#pragma unroll
+    for (int i = 0; i < S_CH; ++i) {
+      int64_t kb;
+      if constexpr (KMODE == 0) kb = kt * 2 + s_sub[i];
+      else if constexpr (KMODE == 1) kb = kt;
+      else kb = k0 / p.tile;
+      rs[i] = srow[i][kb < nt ? kb : nt - 1];  // kb == nt only past K (zero data)
+    }
   };
 
   auto store_stage = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < C::A_CH; ++i) {
+    for (int i = 0; i < A_CH; ++i) {
       if constexpr (NSPLIT == 1) {
         *(uint4*)&sA[buf][0][arl[i]][akoff[i]] = ra[i];
       } else {
@@ -285,40 +305,36 @@ fp8_gemm_kernel(GemmArgs p) {
       }
     }
 #pragma unroll
-    for (int i = 0; i < C::B_CH; ++i) {
+    for (int i = 0; i < B_CH; ++i) {
       uint32_t d[8];
-      decode4(rb[i].x, d[0], d[1]);
-      decode4(rb[i].y, d[2], d[3]);
-      decode4(rb[i].z, d[4], d[5]);
-      decode4(rb[i].w, d[6], d[7]);
+      decode4<CANON>(rb[i].x, d[0], d[1]);
+      decode4<CANON>(rb[i].y, d[2], d[3]);
+      decode4<CANON>(rb[i].z, d[4], d[5]);
+      decode4<CANON>(rb[i].w, d[6], d[7]);
       uint4* dst = (uint4*)&sB[buf][brl[i]][bkoff[i]];
       dst[0] = make_uint4(d[0], d[1], d[2], d[3]);
       dst[1] = make_uint4(d[4], d[5], d[6], d[7]);
     }
+#pragma unroll
+    for (int i = 0; i < S_CH; ++i)
+      if (s_own[i]) sS[buf][s_sub[i]][s_col[i]] = rs[i];
   };
 
   // ---- accumulators --------------------------------------------------------
   f32x4_t acc[FM][NJ];
-  f32x4_t part[FM][NJ];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      part[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
-
-  // weight column (global) of col tile j for this lane, and its scale base
-  const float* scol[NJ];
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  [[maybe_unused]] f32x4_t part[KMODE == 2 ? FM : 1][KMODE == 2 ? NJ : 1];
+  if constexpr (KMODE == 2) {
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const bool up = SWIGLU && j >= FN;
-    const int jj = up ? j - FN : j;
-    const int64_t col = n0 + wn * TNO + jj * 16 + (lane & 15);
-    const float* sb = up ? S2 : S1;
-    scol[j] = col < N ? sb + col * nt : nullptr;
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) part[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
-  // LDS row of col tile j inside sB
+
+  // LDS row (inside sB) of weight tile j for this lane
   int bl_row[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
@@ -328,61 +344,78 @@ fp8_gemm_kernel(GemmArgs p) {
   }
   const int a_row_base = wm * TM + (lane & 15);
   const int k_lane = (lane >> 4) * 8;
+  const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
 
-  const int64_t nk64 = (K + 63) / 64;
-  const int64_t nk32 = (K + 31) / 32;
-  const int64_t steps_per_tile = p.tile / 32;
-  float scv[NJ];
+  const int64_t nk = (K + 63) / 64;
 
-  load_stage(0);
-  store_stage(0);
-  __syncthreads();
-
-  for (int64_t kt = 0; kt < nk64; ++kt) {
+  auto compute_stage = [&](int64_t kt) {
     const int cur = (int)(kt & 1);
-    if (kt + 1 < nk64) load_stage((kt + 1) * 64);
+    bf16x8_t af[2][NSPLIT][FM];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int64_t g = kt * 2 + ks;
-      if (g < nk32) {
-        const bool first = (g % steps_per_tile) == 0;
-        const bool last = ((g + 1) % steps_per_tile) == 0 || g == nk32 - 1;
-        if (first) {
-          const int64_t kb = (g * 32) / p.tile;
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) scv[j] = scol[j] ? scol[j][kb] : 0.0f;
-        }
-        bf16x8_t af[NSPLIT][FM];
+      for (int sp = 0; sp < NSPLIT; ++sp)
 #pragma unroll
-        for (int sp = 0; sp < NSPLIT; ++sp)
+        for (int i = 0; i < FM; ++i)
+          af[ks][sp][i] = *(const bf16x8_t*)&sA[cur][sp][a_row_base + i * 16][ks * 32 + k_lane];
+    bool tile_start = true, tile_end = true;
+    if constexpr (KMODE == 2) {
+      tile_start = ((kt * 64) % p.tile) == 0;
+      tile_end = (((kt + 1) * 64) % p.tile) == 0 || kt == nk - 1;
+    }
 #pragma unroll
-          for (int i = 0; i < FM; ++i)
-            af[sp][i] = *(const bf16x8_t*)&sA[cur][sp][a_row_base + i * 16][ks * 32 + k_lane];
+    for (int j = 0; j < NJ; ++j) {
+      const bf16x8_t b0 = *(const bf16x8_t*)&sB[cur][bl_row[j]][k_lane];
+      const bf16x8_t b1 = *(const bf16x8_t*)&sB[cur][bl_row[j]][32 + k_lane];
+      const float sc0 = sS[cur][0][bl_row[j]];
+      const float sc1 = sS[cur][SPS - 1][bl_row[j]];
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const bf16x8_t bfr = *(const bf16x8_t*)&sB[cur][bl_row[j]][ks * 32 + k_lane];
+      for (int i = 0; i < FM; ++i) {
+        if constexpr (KMODE == 0) {
+          f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][0][i], b0, zero4, 0, 0, 0);
+          if constexpr (NSPLIT == 2) q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][1][i], b0, q, 0, 0, 0);
 #pragma unroll
-          for (int i = 0; i < FM; ++i) {
-            f32x4_t c = first ? f32x4_t{0.f, 0.f, 0.f, 0.f} : part[i][j];
+          for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(sc0, q[r], acc[i][j][r]);
+          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][0][i], b1, zero4, 0, 0, 0);
+          if constexpr (NSPLIT == 2) q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][1][i], b1, q, 0, 0, 0);
 #pragma unroll
-            for (int sp = 0; sp < NSPLIT; ++sp)
-              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[sp][i], bfr, c, 0, 0, 0);
-            part[i][j] = c;
+          for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(sc1, q[r], acc[i][j][r]);
+        } else if constexpr (KMODE == 1) {
+          f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][0][i], b0, zero4, 0, 0, 0);
+          if constexpr (NSPLIT == 2) q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][1][i], b0, q, 0, 0, 0);
+          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][0][i], b1, q, 0, 0, 0);
+          if constexpr (NSPLIT == 2) q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][1][i], b1, q, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(sc0, q[r], acc[i][j][r]);
+        } else {
+          f32x4_t q = tile_start ? zero4 : part[i][j];
+          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][0][i], b0, q, 0, 0, 0);
+          if constexpr (NSPLIT == 2) q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][1][i], b0, q, 0, 0, 0);
+          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][0][i], b1, q, 0, 0, 0);
+          if constexpr (NSPLIT == 2) q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][1][i], b1, q, 0, 0, 0);
+          if (tile_end) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(sc0, q[r], acc[i][j][r]);
           }
-        }
-        if (last) {
-#pragma unroll
-          for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-#pragma unroll
-              for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(scv[j], part[i][j][r], acc[i][j][r]);
+          part[i][j] = q;
         }
       }
     }
-    if (kt + 1 < nk64) store_stage(cur ^ 1);
+  };
+
+  // Two LDS buffers: stage kt+1 is fetched into registers while stage kt is
+  // computed, then decoded into the other buffer.  The last stage is peeled so
+  // the loop body has no conditional load/store.
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+  for (int64_t kt = 0; kt + 1 < nk; ++kt) {
+    load_stage(kt + 1);
+    compute_stage(kt);
+    store_stage((int)((kt + 1) & 1));
     __syncthreads();
   }
+  compute_stage(nk - 1);
 
   // ---- epilogue ------------------------------------------------------------
   // 16x16 MFMA output: lane holds column (lane & 15), rows (lane >> 4) * 4 + r.
@@ -418,26 +451,58 @@ fp8_gemm_kernel(GemmArgs p) {
   }
 }
 
-// Launch configurations.
-//   big:   128 rows x (64 SwiGLU outputs | 128 outputs), 4 waves as 2x2
-//   small:  32 rows x (64 SwiGLU outputs | 64 outputs),  4 waves as 1x4
+// Launch configurations: (rows, staged weight rows, wave grid) per workgroup.
+#ifndef SMAUL_BIG_BM
+#define SMAUL_BIG_BM 128
+#endif
+#ifndef SMAUL_BIG_BNB
+#define SMAUL_BIG_BNB 128
+#endif
+#ifndef SMAUL_BIG_WM
+#define SMAUL_BIG_WM 2
+#endif
+#ifndef SMAUL_BIG_WN
+#define SMAUL_BIG_WN 2
+#endif
 struct CfgBig {
-  static constexpr int BM = 128, WM = 2, WN = 2, BNO_SWIGLU = 64, BNO_PLAIN = 128;
+  static constexpr int BM = SMAUL_BIG_BM, BNB = SMAUL_BIG_BNB, WM = SMAUL_BIG_WM, WN = SMAUL_BIG_WN;
+};
+// fp32 activations stage two bf16 planes of A, so they keep a 128-row tile
+struct CfgBigF32 {
+  static constexpr int BM = 128, BNB = 128, WM = 2, WN = 2;
 };
 struct CfgSmall {
-  static constexpr int BM = 32, WM = 1, WN = 4, BNO_SWIGLU = 64, BNO_PLAIN = 64;
+  static constexpr int BM = 32, BNB = 128, WM = 1, WN = 4;
 };
 
-template <class CF, bool SWIGLU, int NSPLIT, bool OUT_BF16, bool VEC>
-int launch_gemm(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
-  constexpr int BNO = SWIGLU ? CF::BNO_SWIGLU : CF::BNO_PLAIN;
+int kmode_of(int64_t tile) {
+  if (tile == 32) return 0;
+  if (tile == 64) return 1;
+  if (tile > 64 && tile % 64 == 0) return 2;
+  return -1;
+}
+
+template <class CF, bool SWIGLU, int NSPLIT, bool OUT_BF16, int KMODE, bool CANON, bool VEC>
+int launch_gemm_k(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
+  constexpr int BNO = SWIGLU ? CF::BNB / 2 : CF::BNB;
   const int64_t n_tiles = (a.N + BNO - 1) / BNO;
   if (m_tiles <= 0 || n_tiles <= 0) return SMAUL_OK;
   if (m_tiles > 65535 || n_tiles > 65535) return fail(SMAUL_ERR_UNSUPPORTED, "gemm grid too large");
   dim3 grid((unsigned)n_tiles, (unsigned)m_tiles);
-  hipLaunchKernelGGL((fp8_gemm_kernel<CF::BM, BNO, CF::WM, CF::WN, SWIGLU, NSPLIT, OUT_BF16, VEC>),
-                     grid, dim3(CF::WM * CF::WN * 64), 0, stream, a);
+  hipLaunchKernelGGL(
+      (fp8_gemm_kernel<CF::BM, CF::BNB, CF::WM, CF::WN, SWIGLU, NSPLIT, OUT_BF16, KMODE, CANON, VEC>),
+      grid, dim3(CF::WM * CF::WN * 64), 0, stream, a);
   return check_launch("fp8_gemm_kernel");
+}
+
+template <class CF, bool SWIGLU, int NSPLIT, bool OUT_BF16, bool CANON, bool VEC>
+int launch_gemm(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
+  switch (kmode_of(a.tile)) {
+    case 0: return launch_gemm_k<CF, SWIGLU, NSPLIT, OUT_BF16, 0, CANON, VEC>(a, m_tiles, stream);
+    case 1: return launch_gemm_k<CF, SWIGLU, NSPLIT, OUT_BF16, 1, CANON, VEC>(a, m_tiles, stream);
+    case 2: return launch_gemm_k<CF, SWIGLU, NSPLIT, OUT_BF16, 2, CANON, VEC>(a, m_tiles, stream);
+    default: return fail(SMAUL_ERR_UNSUPPORTED, "tile %lld: need 32 or a multiple of 64", (long long)a.tile);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -725,26 +790,62 @@ combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
 }
 
 // ---------------------------------------------------------------------------
+// code canonicalisation (device repack cache): 0x7F -> 0x7E, 0xFF -> 0xFE
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+canonicalize_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ out, int64_t n) {
+  const int64_t nv = n / 16;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += stride) {
+    uint4 v = ((const uint4*)in)[i];
+    v.x = canon4(v.x);
+    v.y = canon4(v.y);
+    v.z = canon4(v.z);
+    v.w = canon4(v.w);
+    ((uint4*)out)[i] = v;
+  }
+  if (blockIdx.x == 0 && threadIdx.x < (n & 15)) {
+    const int64_t j = nv * 16 + threadIdx.x;
+    const uint8_t c = in[j];
+    out[j] = ((c & 0x7f) == 0x7f) ? (uint8_t)(c - 1) : c;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host helpers
 // ---------------------------------------------------------------------------
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 bool dtype_ok(int dt) { return dt == SMAUL_DTYPE_F32 || dt == SMAUL_DTYPE_BF16; }
 
-int pick_block_m(int64_t T, int64_t k, int64_t E) {
+int pick_block_m(int64_t T, int64_t k, int64_t E, int act_dtype) {
   // rows per expert on average; small segments use the 32-row tile
   const int64_t avg = (T * k + E - 1) / (E > 0 ? E : 1);
-  return avg >= 96 ? CfgBig::BM : CfgSmall::BM;
+  if (avg < 96) return CfgSmall::BM;
+  return act_dtype == SMAUL_DTYPE_BF16 ? CfgBig::BM : CfgBigF32::BM;
 }
 
-template <class CF>
-int gemm_dispatch_moe(const GemmArgs& a, bool swiglu, int act_dtype, int64_t m_tiles,
-                      hipStream_t s) {
+template <class CF, class CF32, bool CANON>
+int gemm_dispatch_moe_c(const GemmArgs& a, bool swiglu, int act_dtype, int64_t m_tiles, hipStream_t s) {
   if (swiglu) {
-    if (act_dtype == SMAUL_DTYPE_BF16) return launch_gemm<CF, true, 1, true, true>(a, m_tiles, s);
-    return launch_gemm<CF, true, 2, false, true>(a, m_tiles, s);
+    if (act_dtype == SMAUL_DTYPE_BF16) return launch_gemm<CF, true, 1, true, CANON, true>(a, m_tiles, s);
+    return launch_gemm<CF32, true, 2, false, CANON, true>(a, m_tiles, s);
   }
-  if (act_dtype == SMAUL_DTYPE_BF16) return launch_gemm<CF, false, 1, true, true>(a, m_tiles, s);
-  return launch_gemm<CF, false, 2, false, true>(a, m_tiles, s);
+  if (act_dtype == SMAUL_DTYPE_BF16) return launch_gemm<CF, false, 1, true, CANON, true>(a, m_tiles, s);
+  return launch_gemm<CF32, false, 2, false, CANON, true>(a, m_tiles, s);
+}
+
+template <class CF, class CF32>
+int gemm_dispatch_moe(const GemmArgs& a, bool swiglu, int act_dtype, int64_t m_tiles, bool canon,
+                      hipStream_t s) {
+  return canon ? gemm_dispatch_moe_c<CF, CF32, true>(a, swiglu, act_dtype, m_tiles, s)
+               : gemm_dispatch_moe_c<CF, CF32, false>(a, swiglu, act_dtype, m_tiles, s);
+}
+
+template <class CF, int NSPLIT>
+int gemm_dispatch_dense(const GemmArgs& a, bool vec, bool canon, int64_t m_tiles, hipStream_t s) {
+  if (!vec) return launch_gemm<CF, false, NSPLIT, false, false, false>(a, m_tiles, s);
+  return canon ? launch_gemm<CF, false, NSPLIT, false, true, true>(a, m_tiles, s)
+               : launch_gemm<CF, false, NSPLIT, false, false, true>(a, m_tiles, s);
 }
 
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
@@ -761,15 +862,15 @@ int smaul_version(void) { return SMAUL_VERSION; }
 const char* smaul_last_error(void) { return g_err; }
 
 int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* s, void* y,
-                     int y_dtype, int64_t rows, int64_t in_f, int64_t out_f, int64_t tile,
+                     int y_dtype, int64_t rows, int64_t in_f, int64_t out_f, int64_t tile, int flags,
                      hipStream_t stream) {
   if (tile <= 0 || in_f <= 0 || out_f <= 0 || rows < 0)
     return fail(SMAUL_ERR_INVALID, "tile/in_f/out_f must be positive, got %lld/%lld/%lld",
                 (long long)tile, (long long)in_f, (long long)out_f);
   if (!dtype_ok(x_dtype) || y_dtype != SMAUL_DTYPE_F32)
     return fail(SMAUL_ERR_INVALID, "x dtype must be f32|bf16 and y dtype f32");
-  if (tile % 32 != 0)
-    return fail(SMAUL_ERR_UNSUPPORTED, "tile %lld is not a multiple of 32", (long long)tile);
+  if (kmode_of(tile) < 0)
+    return fail(SMAUL_ERR_UNSUPPORTED, "tile %lld: need 32 or a multiple of 64", (long long)tile);
   if (rows == 0) return SMAUL_OK;
   if (!x || !w || !s || !y) return fail(SMAUL_ERR_INVALID, "null pointer");
   GemmArgs a{};
@@ -791,21 +892,18 @@ int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* 
   a.R = rows;
   a.E = 1;
   const bool vec = (in_f % 16 == 0) && aligned16(x) && aligned16(w);
+  const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
   const bool small = rows <= 64;
-  const int64_t bm = small ? CfgSmall::BM : CfgBig::BM;
-  const int64_t mt = (rows + bm - 1) / bm;
   if (x_dtype == SMAUL_DTYPE_BF16) {
-    if (small)
-      return vec ? launch_gemm<CfgSmall, false, 1, false, true>(a, mt, stream)
-                 : launch_gemm<CfgSmall, false, 1, false, false>(a, mt, stream);
-    return vec ? launch_gemm<CfgBig, false, 1, false, true>(a, mt, stream)
-               : launch_gemm<CfgBig, false, 1, false, false>(a, mt, stream);
+    const int64_t bm = small ? CfgSmall::BM : CfgBig::BM;
+    const int64_t mt = (rows + bm - 1) / bm;
+    return small ? gemm_dispatch_dense<CfgSmall, 1>(a, vec, canon, mt, stream)
+                 : gemm_dispatch_dense<CfgBig, 1>(a, vec, canon, mt, stream);
   }
-  if (small)
-    return vec ? launch_gemm<CfgSmall, false, 2, false, true>(a, mt, stream)
-               : launch_gemm<CfgSmall, false, 2, false, false>(a, mt, stream);
-  return vec ? launch_gemm<CfgBig, false, 2, false, true>(a, mt, stream)
-             : launch_gemm<CfgBig, false, 2, false, false>(a, mt, stream);
+  const int64_t bm = small ? CfgSmall::BM : CfgBigF32::BM;
+  const int64_t mt = (rows + bm - 1) / bm;
+  return small ? gemm_dispatch_dense<CfgSmall, 2>(a, vec, canon, mt, stream)
+               : gemm_dispatch_dense<CfgBigF32, 2>(a, vec, canon, mt, stream);
 }
 
 int smaul_moe_router(const void* x, int x_dtype, const float* gate_w, const float* gate_b,
@@ -848,20 +946,23 @@ int smaul_moe_dispatch(const int64_t* topi, const float* topw, int32_t* counts, 
   return check_launch("dispatch_kernel");
 }
 
-int smaul_moe_block_m(int64_t T, int64_t k, int64_t E) { return pick_block_m(T, k, E); }
+int smaul_moe_block_m(int64_t T, int64_t k, int64_t E, int act_dtype) {
+  return pick_block_m(T, k, E, act_dtype);
+}
 
 static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* perm_row,
                     const uint8_t* const* w1, const float* const* s1, const uint8_t* const* w2,
                     const float* const* s2, void* out, const int32_t* seg_off,
                     const int32_t* tile_off, int64_t max_tiles, int64_t E, int64_t K, int64_t N,
-                    int64_t tile, int64_t block_m, hipStream_t stream) {
+                    int64_t tile, int64_t block_m, int flags, hipStream_t stream) {
   if (!dtype_ok(act_dtype)) return fail(SMAUL_ERR_INVALID, "moe gemm: bad dtype");
   if (E < 1 || E > MAX_E || K <= 0 || N <= 0 || tile <= 0 || max_tiles < 0)
     return fail(SMAUL_ERR_INVALID, "moe gemm: bad sizes");
-  if (tile % 32 != 0) return fail(SMAUL_ERR_UNSUPPORTED, "moe gemm: tile must be a multiple of 32");
+  if (kmode_of(tile) < 0) return fail(SMAUL_ERR_UNSUPPORTED, "moe gemm: tile must be 32 or a multiple of 64");
   if (K % 16 != 0 || !aligned16(act))
     return fail(SMAUL_ERR_UNSUPPORTED, "moe gemm: K must be a multiple of 16 and activations 16-byte aligned");
-  if (!(block_m == CfgBig::BM || block_m == CfgSmall::BM))
+  const int64_t big_bm = act_dtype == SMAUL_DTYPE_BF16 ? CfgBig::BM : CfgBigF32::BM;
+  if (!(block_m == big_bm || block_m == CfgSmall::BM))
     return fail(SMAUL_ERR_INVALID, "moe gemm: block_m must come from smaul_moe_block_m");
   if (!act || !w1 || !s1 || !out || !seg_off || !tile_off || (swiglu && (!w2 || !s2)))
     return fail(SMAUL_ERR_INVALID, "moe gemm: null pointer");
@@ -883,26 +984,29 @@ static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* 
   a.seg_off = seg_off;
   a.tile_off = tile_off;
   a.E = (int)E;
-  if (block_m == CfgBig::BM) return gemm_dispatch_moe<CfgBig>(a, swiglu, act_dtype, max_tiles, stream);
-  return gemm_dispatch_moe<CfgSmall>(a, swiglu, act_dtype, max_tiles, stream);
+  const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
+  if (block_m == big_bm)
+    return gemm_dispatch_moe<CfgBig, CfgBigF32>(a, swiglu, act_dtype, max_tiles, canon, stream);
+  return gemm_dispatch_moe<CfgSmall, CfgSmall>(a, swiglu, act_dtype, max_tiles, canon, stream);
 }
 
 int smaul_moe_gate_up(const void* x, int act_dtype, const int32_t* perm_row,
                       const uint8_t* const* gate_w, const float* const* gate_s,
                       const uint8_t* const* up_w, const float* const* up_s, void* hdn,
                       const int32_t* seg_off, const int32_t* tile_off, int64_t max_tiles, int64_t E,
-                      int64_t d, int64_t h, int64_t tile, int64_t block_m, hipStream_t stream) {
+                      int64_t d, int64_t h, int64_t tile, int64_t block_m, int flags,
+                      hipStream_t stream) {
   if (!perm_row) return fail(SMAUL_ERR_INVALID, "gate_up: null perm_row");
   return moe_gemm(true, x, act_dtype, perm_row, gate_w, gate_s, up_w, up_s, hdn, seg_off, tile_off,
-                  max_tiles, E, d, h, tile, block_m, stream);
+                  max_tiles, E, d, h, tile, block_m, flags, stream);
 }
 
 int smaul_moe_down(const void* hdn, int act_dtype, const uint8_t* const* down_w,
                    const float* const* down_s, void* yperm, const int32_t* seg_off,
                    const int32_t* tile_off, int64_t max_tiles, int64_t E, int64_t d, int64_t h,
-                   int64_t tile, int64_t block_m, hipStream_t stream) {
+                   int64_t tile, int64_t block_m, int flags, hipStream_t stream) {
   return moe_gemm(false, hdn, act_dtype, nullptr, down_w, down_s, nullptr, nullptr, yperm, seg_off,
-                  tile_off, max_tiles, E, h, d, tile, block_m, stream);
+                  tile_off, max_tiles, E, h, d, tile, block_m, flags, stream);
 }
 
 int smaul_moe_combine(const void* yperm, int act_dtype, const int64_t* topi, const float* topw,
@@ -947,7 +1051,7 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
                       const uint8_t* const* down_w8, const float* const* down_s, void* out,
                       float* prob, int64_t* topi, float* topw, int32_t* counts, void* workspace,
                       int64_t workspace_bytes, int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
-                      int64_t tile, hipStream_t stream) {
+                      int64_t tile, int flags, hipStream_t stream) {
   const int64_t need = smaul_moe_workspace_size(T, d, h, E, k, act_dtype);
   if (need < 0) return fail(SMAUL_ERR_INVALID, "moe_forward: bad sizes");
   if (workspace_bytes < need)
@@ -974,17 +1078,30 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
 
   int rc = smaul_moe_router(x, act_dtype, gate_w, gate_b, prob, topi, topw, T, d, E, k, stream);
   if (rc) return rc;
-  const int64_t bm = pick_block_m(T, k, E);
+  const int64_t bm = pick_block_m(T, k, E, act_dtype);
   rc = smaul_moe_dispatch(topi, topw, counts, seg_off, tile_off, perm_row, perm_w, inv, T, E, k, bm, stream);
   if (rc) return rc;
   const int64_t max_tiles = (R + bm - 1) / bm + E;
   rc = smaul_moe_gate_up(x, act_dtype, perm_row, gate_w8, gate_s, up_w8, up_s, hdn, seg_off, tile_off,
-                         max_tiles, E, d, h, tile, bm, stream);
+                         max_tiles, E, d, h, tile, bm, flags, stream);
   if (rc) return rc;
   rc = smaul_moe_down(hdn, act_dtype, down_w8, down_s, yperm, seg_off, tile_off, max_tiles, E, d, h, tile,
-                      bm, stream);
+                      bm, flags, stream);
   if (rc) return rc;
   return smaul_moe_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, stream);
+}
+
+int smaul_fp8_canonicalize(const uint8_t* codes, uint8_t* out, int64_t n, hipStream_t stream) {
+  if (n < 0) return fail(SMAUL_ERR_INVALID, "canonicalize: n < 0");
+  if (n == 0) return SMAUL_OK;
+  if (!codes || !out) return fail(SMAUL_ERR_INVALID, "canonicalize: null pointer");
+  if (!aligned16(codes) || !aligned16(out)) return fail(SMAUL_ERR_INVALID, "canonicalize: buffers must be 16-byte aligned");
+  const int64_t nv = n / 16;
+  int64_t blocks = (nv + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(canonicalize_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, codes, out, n);
+  return check_launch("canonicalize_kernel");
 }
 
 int smaul_selftest_topk(const float* vals, int64_t n, int64_t k, int64_t* out_idx) {

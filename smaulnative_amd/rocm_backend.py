@@ -129,7 +129,7 @@ class RocmBackend:
             return y
         with torch.cuda.device(x.device):
             rc = lib.smaul_fp8_linear(xc.data_ptr(), _ACT[xc.dtype], wc.data_ptr(), sc.data_ptr(),
-                                      y.data_ptr(), _lib.DTYPE_F32, rows, in_f, out_f, tile,
+                                      y.data_ptr(), _lib.DTYPE_F32, rows, in_f, out_f, tile, 0,
                                       _stream_handle(x.device))
         _lib.check(rc, "fp8_forward")
         return y
@@ -155,55 +155,85 @@ class RocmBackend:
 
     # ---- MoE (model.py:557-585) -------------------------------------------
     def _expert_table(self, experts: Sequence[Sequence[torch.Tensor]], device, d, h, tile):
-        """Device int64 [6, E] table of the experts' buffer addresses.
+        """Device int64 [6, E] table of the experts' buffer addresses (a repack cache).
 
-        Cached on the buffers' addresses and versions, so a requant or a
-        ``copy_`` into ``w8``/``sc`` (which bumps ``_version``) rebuilds it.
-        Non-fp32 scales (a model cast to bf16) are widened once and kept alive
-        by the cache entry.
+        Rows: gate codes, gate scales, up codes, up scales, down codes, down
+        scales.  The code rows point at *canonical copies* of the ``w8``
+        buffers (0x7F/0xFF rewritten to 0x7E/0xFE, the same +-448 values) so
+        the GEMMs can use the hardware E4M3 converter directly; the stored
+        ``w8`` buffers are never modified.  Non-fp32 scales (a model cast to
+        bf16) are widened into cached copies.
+
+        The cache is keyed on the buffers' addresses.  When a buffer's
+        ``_version`` changes (requant, ``copy_``), the copies are refreshed in
+        place on the current stream, so the table -- and any HIP graph that
+        captured it -- keeps pointing at valid, current data.  Entries whose
+        source buffers have been freed are dropped.
         """
-        key_parts = []
+        import weakref
+        lib = _lib.load()
+        flat = []
         for ex in experts:
             if len(ex) != 6:
                 raise ValueError("each expert is (gate_w8, gate_sc, up_w8, up_sc, down_w8, down_sc)")
-            for t in ex:
-                key_parts.append((t.data_ptr(), t._version, t.dtype))
-        key = (str(device), d, h, tile, tuple(key_parts))
-        hit = self._ptr_cache.get(key)
-        if hit is not None:
-            return hit[0]
+            flat.extend(ex)
+        key = (str(device), d, h, tile, tuple(t.data_ptr() for t in flat))
+        versions = tuple(t._version for t in flat)
+        ent = self._ptr_cache.get(key)
+        if ent is not None and all(r() is not None for r in ent["refs"]):
+            if ent["versions"] != versions:
+                self._refresh(ent, flat, lib, device)
+                ent["versions"] = versions
+            return ent["table"]
         nt_d = (d + tile - 1) // tile
         nt_h = (h + tile - 1) // tile
-        keep = []
-        rows = [[] for _ in range(6)]
-        for e, (gw, gs, uw, us, dw, ds) in enumerate(experts):
-            for idx, (t, shape, is_code) in enumerate(((gw, (h, d), True), (gs, (h, nt_d), False),
-                                                       (uw, (h, d), True), (us, (h, nt_d), False),
-                                                       (dw, (d, h), True), (ds, (d, nt_h), False))):
-                _need_device("moe_forward", t)
-                if t.device != device:
-                    raise RuntimeError(f"moe_forward: expert {e} buffer on {t.device}, x on {device}")
-                if tuple(t.shape) != shape:
-                    raise RuntimeError(f"moe_forward: expert {e} buffer {idx} has shape {tuple(t.shape)}, "
-                                       f"expected {shape}")
-                if is_code:
-                    if t.dtype != torch.uint8:
-                        raise RuntimeError(f"moe_forward: expert {e} codes must be uint8")
-                    if not t.is_contiguous():
-                        raise RuntimeError(f"moe_forward: expert {e} codes must be contiguous")
-                    if t.data_ptr() % 16:
-                        raise RuntimeError(f"moe_forward: expert {e} codes must be 16-byte aligned")
-                    u = t
-                else:
-                    u = t if (t.dtype == torch.float32 and t.is_contiguous()) else t.float().contiguous()
-                    keep.append(u)
-                rows[idx].append(u.data_ptr())
-        table = torch.tensor(rows, dtype=torch.int64).to(device)
+        shapes = [(h, d), (h, nt_d), (h, d), (h, nt_d), (d, h), (d, nt_h)]
+        for n, t in enumerate(flat):
+            e, idx = divmod(n, 6)
+            if not t.is_cuda or t.device != device:
+                raise RuntimeError(f"moe_forward: expert {e} buffer {idx} on {t.device}, x on {device}")
+            if tuple(t.shape) != shapes[idx]:
+                raise RuntimeError(f"moe_forward: expert {e} buffer {idx} has shape {tuple(t.shape)}, "
+                                   f"expected {shapes[idx]}")
+            if idx % 2 == 0 and t.dtype != torch.uint8:
+                raise RuntimeError(f"moe_forward: expert {e} codes must be uint8, got {t.dtype}")
+        copies = [torch.empty(t.numel(), dtype=torch.uint8, device=device) if i % 2 == 0 else None
+                  for i, t in enumerate(flat)]
+        ent = {"copies": copies, "refs": [weakref.ref(t) for t in flat], "versions": versions}
+        self._refresh(ent, flat, lib, device)
+        E = len(experts)
+        rows = [[0] * E for _ in range(6)]
+        for n in range(len(flat)):
+            e, idx = divmod(n, 6)
+            rows[idx][e] = ent["copies"][n].data_ptr()
+        ent["table"] = torch.tensor(rows, dtype=torch.int64).to(device)
         with self._lock:
-            if len(self._ptr_cache) > 64:
-                self._ptr_cache.clear()
-            self._ptr_cache[key] = (table, keep)
-        return table
+            dead = [k for k, v in self._ptr_cache.items() if any(r() is None for r in v["refs"])]
+            for k in dead:
+                del self._ptr_cache[k]
+            self._ptr_cache[key] = ent
+        return ent["table"]
+
+    @staticmethod
+    def _refresh(ent, flat, lib, device):
+        """(Re)write the cached canonical codes and fp32 scales from the source buffers."""
+        stream = _stream_handle(device)
+        for n, t in enumerate(flat):
+            if n % 2 == 0:
+                src = t if t.is_contiguous() else t.contiguous()
+                dst = ent["copies"][n]
+                with torch.cuda.device(device):
+                    rc = lib.smaul_fp8_canonicalize(src.data_ptr(), dst.data_ptr(), src.numel(), stream)
+                _lib.check(rc, "fp8_canonicalize")
+            else:
+                if t.dtype == torch.float32 and t.is_contiguous():
+                    ent["copies"][n] = t
+                else:
+                    w = t.float().contiguous()
+                    if ent["copies"][n] is None or ent["copies"][n] is t:
+                        ent["copies"][n] = w
+                    else:
+                        ent["copies"][n].copy_(w.reshape(ent["copies"][n].shape))
 
     def moe_router(self, x2, gate_w, gate_b, top_k):
         """Router stage alone: (prob [T,E] fp32, topi [T,k] int64, topw [T,k] fp32)."""
@@ -229,7 +259,7 @@ class RocmBackend:
         T, k = topi.shape
         E = int(num_experts)
         if block_m is None:
-            block_m = lib.smaul_moe_block_m(T, k, E)
+            block_m = lib.smaul_moe_block_m(T, k, E, _lib.DTYPE_BF16)
         dev = topi.device
         i32 = dict(dtype=torch.int32, device=dev)
         out = {
@@ -269,7 +299,7 @@ class RocmBackend:
         gw = gate_w.detach().float().contiguous()
         gb = None if gate_b is None else gate_b.detach().float().contiguous()
         R = T * top_k
-        bm = lib.smaul_moe_block_m(T, top_k, E)
+        bm = lib.smaul_moe_block_m(T, top_k, E, act)
         max_tiles = (R + bm - 1) // bm + E
         hdn = torch.empty(max(1, R), h, dtype=x2.dtype, device=dev)
         yperm = torch.empty(max(1, R), d, dtype=x2.dtype, device=dev)
@@ -287,12 +317,13 @@ class RocmBackend:
             sh = stream.cuda_stream
             rc = lib.smaul_moe_gate_up(x2.data_ptr(), act, disp["perm_row"].data_ptr(), tp, tp + row,
                                        tp + 2 * row, tp + 3 * row, hdn.data_ptr(), disp["seg_off"].data_ptr(),
-                                       disp["tile_off"].data_ptr(), max_tiles, E, d, h, tile, bm, sh)
+                                       disp["tile_off"].data_ptr(), max_tiles, E, d, h, tile, bm,
+                                       _lib.FLAG_CANONICAL_CODES, sh)
             _lib.check(rc, "moe_gate_up")
             rec(3)
             rc = lib.smaul_moe_down(hdn.data_ptr(), act, tp + 4 * row, tp + 5 * row, yperm.data_ptr(),
                                     disp["seg_off"].data_ptr(), disp["tile_off"].data_ptr(), max_tiles, E, d,
-                                    h, tile, bm, sh)
+                                    h, tile, bm, _lib.FLAG_CANONICAL_CODES, sh)
             _lib.check(rc, "moe_down")
             rec(4)
             rc = lib.smaul_moe_combine(yperm.data_ptr(), act, topi.data_ptr(), topw.data_ptr(),
@@ -356,7 +387,7 @@ class RocmBackend:
                     tp, tp + row, tp + 2 * row, tp + 3 * row, tp + 4 * row, tp + 5 * row,
                     out.data_ptr(), prob.data_ptr(), topi.data_ptr(), topw.data_ptr(),
                     counts.data_ptr(), ws.data_ptr(), ws_bytes, T, d, h, E, top_k, tile,
-                    _stream_handle(dev))
+                    _lib.FLAG_CANONICAL_CODES, _stream_handle(dev))
             _lib.check(rc, "moe_forward")
         lead = x.shape[:-1]
         return (out.reshape(*lead, d), prob.reshape(*lead, E), topi.reshape(*lead, top_k), counts)

@@ -43,9 +43,9 @@ def test_library_version_and_error_channel():
 def test_library_validates_without_touching_the_gpu():
     lib = _lib.load()
     # non-positive sizes are rejected before any launch
-    rc = lib.smaul_fp8_linear(None, 0, None, None, None, 0, 4, 0, 8, 64, None)
+    rc = lib.smaul_fp8_linear(None, 0, None, None, None, 0, 4, 0, 8, 64, 0, None)
     assert rc == _lib.SMAUL_ERR_INVALID and "positive" in _lib.last_error()
-    rc = lib.smaul_fp8_linear(None, 0, None, None, None, 0, 4, 64, 8, 48, None)
+    rc = lib.smaul_fp8_linear(None, 0, None, None, None, 0, 4, 64, 8, 48, 0, None)
     assert rc == _lib.SMAUL_ERR_UNSUPPORTED
     rc = lib.smaul_moe_router(None, 1, None, None, None, None, None, 8, 64, 65, 2, None)
     assert rc == _lib.SMAUL_ERR_INVALID
