@@ -87,7 +87,13 @@ __device__ __forceinline__ void decode4(uint32_t w, uint32_t& lo, uint32_t& hi) 
   hi = __builtin_bit_cast(uint32_t, b);
 }
 
-__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
+// silu(v) = v / (1 + e^-v) with the hardware exp2 and reciprocal (about two
+// ulp in fp32).  Every caller rounds the result to the activation dtype or
+// compares it at a tolerance far above that.
+__device__ __forceinline__ float silu_f(float v) {
+  const float e = __builtin_amdgcn_exp2f(-v * 1.4426950408889634f);
+  return v * __builtin_amdgcn_rcpf(1.0f + e);
+}
 
 // ---------------------------------------------------------------------------
 // grouped / dense FP8 GEMM
@@ -139,11 +145,18 @@ struct GemmCfg {
   static_assert(B_CH >= 1 && (BNB * 4) % NT == 0, "B staging split");
 };
 
-template <int BM, int BNB, int WM, int WN, bool SWIGLU, int NSPLIT, bool OUT_BF16, int KMODE,
-          bool CANON, bool VEC>
+#ifndef SMAUL_GROUP_M
+#define SMAUL_GROUP_M 8
+#endif
+constexpr int GROUP_M = SMAUL_GROUP_M;
+
+template <int BM, int BNB, int WM, int WN, int MT, bool REMAP, bool SWIGLU, int NSPLIT, bool OUT_BF16,
+          int KMODE, bool CANON, bool VEC>
 __global__ void __launch_bounds__(WM * WN * 64)
 fp8_gemm_kernel(GemmArgs p) {
   using C = GemmCfg<BM, BNB, WM, WN, SWIGLU, NSPLIT>;
+  static_assert(MT == 16 || MT == 32, "MFMA tile is 16x16x32 or 32x32x16");
+  static_assert(C::TM % MT == 0 && C::TNO % MT == 0, "wave tile must be a multiple of the MFMA tile");
   constexpr int NT = C::NT, BNO = C::BNO, TM = C::TM, TNO = C::TNO, FM = C::FM, NJ = C::NJ,
                 FN = C::FN, LDK = C::LDK, A_PER_ROW = C::A_PER_ROW, A_CH = C::A_CH,
                 B_CH = C::B_CH;
@@ -159,8 +172,32 @@ fp8_gemm_kernel(GemmArgs p) {
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  // ---- which expert / rows does this workgroup own -------------------------
-  const int mt = blockIdx.y;
+  // ---- which tile does this workgroup own ----------------------------------
+  // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
+  // L2).  Remap the linear id so each XCD walks a contiguous band of tiles,
+  // then order that band in groups of GROUP_M row tiles x all column tiles,
+  // column-major inside a group: the concurrently running workgroups of an
+  // XCD share a few A row tiles and a few weight column tiles.
+  int mt, nt_idx;
+  {
+    const int n_tiles = gridDim.x, m_tiles = gridDim.y;
+    const int total = n_tiles * m_tiles;
+    int lin = blockIdx.y * n_tiles + blockIdx.x;
+    if constexpr (REMAP) {
+      constexpr int NXCD = 8;
+      const int full = (total / NXCD) * NXCD;
+      if (lin < full) lin = (lin % NXCD) * (full / NXCD) + lin / NXCD;
+      const int group = GROUP_M * n_tiles;
+      const int g = lin / group, within = lin % group;
+      const int m_first = g * GROUP_M;
+      const int gm = min(GROUP_M, m_tiles - m_first);
+      mt = m_first + within % gm;
+      nt_idx = within / gm;
+    } else {
+      mt = lin / n_tiles;
+      nt_idx = lin % n_tiles;
+    }
+  }
   int e = 0, row0, rows_here;
   if (p.seg_off) {
     const int total = p.tile_off[p.E];
@@ -173,7 +210,7 @@ fp8_gemm_kernel(GemmArgs p) {
     rows_here = (int)min<int64_t>(BM, p.R - row0);
   }
   if (rows_here <= 0) return;
-  const int n0 = blockIdx.x * BNO;
+  const int n0 = nt_idx * BNO;
   const int64_t K = p.K, N = p.N, nt = p.nt;
 
   const uint8_t* W1 = p.wp ? p.wp[e] : p.w + e * p.w_estride;
@@ -321,83 +358,105 @@ fp8_gemm_kernel(GemmArgs p) {
   };
 
   // ---- accumulators --------------------------------------------------------
-  f32x4_t acc[FM][NJ];
+  // MT x MT output tiles: FMT row tiles x NJT weight tiles per wave; an MT=16
+  // tile holds 4 fp32 per lane, an MT=32 tile 16.
+  constexpr int FMT = TM / MT, NJT = (C::TNB) / MT, FNT = TNO / MT, NACC = MT * MT / 64;
+  typedef float accv_t __attribute__((ext_vector_type(NACC)));
+  accv_t acc[FMT][NJT];
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < FMT; ++i)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  [[maybe_unused]] f32x4_t part[KMODE == 2 ? FM : 1][KMODE == 2 ? NJ : 1];
+    for (int j = 0; j < NJT; ++j)
+#pragma unroll
+      for (int r = 0; r < NACC; ++r) acc[i][j][r] = 0.0f;
+  [[maybe_unused]] accv_t part[KMODE == 2 ? FMT : 1][KMODE == 2 ? NJT : 1];
   if constexpr (KMODE == 2) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FMT; ++i)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) part[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < NJT; ++j)
+#pragma unroll
+        for (int r = 0; r < NACC; ++r) part[i][j][r] = 0.0f;
   }
 
   // LDS row (inside sB) of weight tile j for this lane
-  int bl_row[NJ];
+  int bl_row[NJT];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const bool up = SWIGLU && j >= FN;
-    const int jj = up ? j - FN : j;
-    bl_row[j] = (up ? BNO : 0) + wn * TNO + jj * 16 + (lane & 15);
+  for (int j = 0; j < NJT; ++j) {
+    const bool up = SWIGLU && j >= FNT;
+    const int jj = up ? j - FNT : j;
+    bl_row[j] = (up ? BNO : 0) + wn * TNO + jj * MT + (lane & (MT - 1));
   }
-  const int a_row_base = wm * TM + (lane & 15);
-  const int k_lane = (lane >> 4) * 8;
-  const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+  const int a_row_base = wm * TM + (lane & (MT - 1));
+  // k offset of this lane inside one MFMA k-step (8 bf16 per lane)
+  const int k_lane = MT == 16 ? (lane >> 4) * 8 : (lane >> 5) * 8;
+  constexpr int KSTEP = MT == 16 ? 32 : 16;     // K per MFMA
+  constexpr int NKS = 64 / KSTEP;               // MFMA k-steps per stage
+  constexpr int KS_PER_TILE32 = 32 / KSTEP;     // k-steps per 32-wide scale tile (KMODE 0)
+  accv_t zacc;
+#pragma unroll
+  for (int r = 0; r < NACC; ++r) zacc[r] = 0.0f;
+
+  auto mfma = [&](const bf16x8_t& a, const bf16x8_t& b, const accv_t& c) -> accv_t {
+    if constexpr (MT == 16) return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  };
 
   const int64_t nk = (K + 63) / 64;
 
   auto compute_stage = [&](int64_t kt) {
     const int cur = (int)(kt & 1);
-    bf16x8_t af[2][NSPLIT][FM];
+    bf16x8_t af[NKS][NSPLIT][FMT];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
       for (int sp = 0; sp < NSPLIT; ++sp)
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
-          af[ks][sp][i] = *(const bf16x8_t*)&sA[cur][sp][a_row_base + i * 16][ks * 32 + k_lane];
+        for (int i = 0; i < FMT; ++i)
+          af[ks][sp][i] = *(const bf16x8_t*)&sA[cur][sp][a_row_base + i * MT][ks * KSTEP + k_lane];
     bool tile_start = true, tile_end = true;
     if constexpr (KMODE == 2) {
       tile_start = ((kt * 64) % p.tile) == 0;
       tile_end = (((kt + 1) * 64) % p.tile) == 0 || kt == nk - 1;
     }
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const bf16x8_t b0 = *(const bf16x8_t*)&sB[cur][bl_row[j]][k_lane];
-      const bf16x8_t b1 = *(const bf16x8_t*)&sB[cur][bl_row[j]][32 + k_lane];
+    for (int j = 0; j < NJT; ++j) {
+      bf16x8_t bf[NKS];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) bf[ks] = *(const bf16x8_t*)&sB[cur][bl_row[j]][ks * KSTEP + k_lane];
       const float sc0 = sS[cur][0][bl_row[j]];
       const float sc1 = sS[cur][SPS - 1][bl_row[j]];
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
+      for (int i = 0; i < FMT; ++i) {
         if constexpr (KMODE == 0) {
-          f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][0][i], b0, zero4, 0, 0, 0);
-          if constexpr (NSPLIT == 2) q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][1][i], b0, q, 0, 0, 0);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(sc0, q[r], acc[i][j][r]);
-          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][0][i], b1, zero4, 0, 0, 0);
-          if constexpr (NSPLIT == 2) q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][1][i], b1, q, 0, 0, 0);
+          for (int half = 0; half < 2; ++half) {
+            accv_t q = zacc;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(sc1, q[r], acc[i][j][r]);
-        } else if constexpr (KMODE == 1) {
-          f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][0][i], b0, zero4, 0, 0, 0);
-          if constexpr (NSPLIT == 2) q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][1][i], b0, q, 0, 0, 0);
-          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][0][i], b1, q, 0, 0, 0);
-          if constexpr (NSPLIT == 2) q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][1][i], b1, q, 0, 0, 0);
+            for (int ks = half * KS_PER_TILE32; ks < (half + 1) * KS_PER_TILE32; ++ks)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(sc0, q[r], acc[i][j][r]);
-        } else {
-          f32x4_t q = tile_start ? zero4 : part[i][j];
-          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][0][i], b0, q, 0, 0, 0);
-          if constexpr (NSPLIT == 2) q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][1][i], b0, q, 0, 0, 0);
-          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][0][i], b1, q, 0, 0, 0);
-          if constexpr (NSPLIT == 2) q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][1][i], b1, q, 0, 0, 0);
-          if (tile_end) {
+              for (int sp = 0; sp < NSPLIT; ++sp) q = mfma(af[ks][sp][i], bf[ks], q);
+            const float sc = half ? sc1 : sc0;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(sc0, q[r], acc[i][j][r]);
+            for (int r = 0; r < NACC; ++r) acc[i][j][r] = __builtin_fmaf(sc, q[r], acc[i][j][r]);
           }
-          part[i][j] = q;
+        } else {
+          accv_t q = zacc;
+          if constexpr (KMODE == 2) q = tile_start ? zacc : part[i][j];
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+            for (int sp = 0; sp < NSPLIT; ++sp) q = mfma(af[ks][sp][i], bf[ks], q);
+          if constexpr (KMODE == 1) {
+#pragma unroll
+            for (int r = 0; r < NACC; ++r) acc[i][j][r] = __builtin_fmaf(sc0, q[r], acc[i][j][r]);
+          } else {
+            if (tile_end) {
+#pragma unroll
+              for (int r = 0; r < NACC; ++r) acc[i][j][r] = __builtin_fmaf(sc0, q[r], acc[i][j][r]);
+            }
+            part[i][j] = q;
+          }
         }
       }
     }
@@ -411,28 +470,35 @@ fp8_gemm_kernel(GemmArgs p) {
   __syncthreads();
   for (int64_t kt = 0; kt + 1 < nk; ++kt) {
     load_stage(kt + 1);
+    // Scheduling fences: keep the next stage's global loads ahead of this
+    // stage's MFMAs and its LDS stores (which wait for those loads) after
+    // them, so the load latency overlaps a whole stage of compute.
+    __builtin_amdgcn_sched_barrier(0);
     compute_stage(kt);
+    __builtin_amdgcn_sched_barrier(0);
     store_stage((int)((kt + 1) & 1));
     __syncthreads();
   }
   compute_stage(nk - 1);
 
   // ---- epilogue ------------------------------------------------------------
-  // 16x16 MFMA output: lane holds column (lane & 15), rows (lane >> 4) * 4 + r.
+  // MFMA output layout: lane holds column (lane % MT) of its tile; for MT=16
+  // rows (lane/16)*4 + r, for MT=32 rows (r/4)*8 + (lane/32)*4 + r%4.
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
+  for (int i = 0; i < FMT; ++i) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int lr = wm * TM + i * 16 + (lane >> 4) * 4 + r;
+    for (int r = 0; r < NACC; ++r) {
+      const int rin = MT == 16 ? (lane >> 4) * 4 + r : (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      const int lr = wm * TM + i * MT + rin;
       if (lr >= rows_here) continue;
       const int64_t orow = row0 + lr;
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int64_t col = n0 + wn * TNO + j * 16 + (lane & 15);
+      for (int j = 0; j < FNT; ++j) {
+        const int64_t col = n0 + wn * TNO + j * MT + (lane & (MT - 1));
         if (col >= N) continue;
         float v;
         if constexpr (SWIGLU) {
-          float g = acc[i][j][r], u = acc[i][j + FN][r];
+          float g = acc[i][j][r], u = acc[i][j + FNT][r];
           if constexpr (OUT_BF16) {
             g = bf2f(f2bf(g));
             u = bf2f(f2bf(u));
@@ -464,15 +530,25 @@ fp8_gemm_kernel(GemmArgs p) {
 #ifndef SMAUL_BIG_WN
 #define SMAUL_BIG_WN 2
 #endif
+#ifndef SMAUL_BIG_MT
+#define SMAUL_BIG_MT 32
+#endif
+#ifndef SMAUL_REMAP
+#define SMAUL_REMAP 1
+#endif
 struct CfgBig {
   static constexpr int BM = SMAUL_BIG_BM, BNB = SMAUL_BIG_BNB, WM = SMAUL_BIG_WM, WN = SMAUL_BIG_WN;
+  static constexpr int MT = SMAUL_BIG_MT;
+  static constexpr bool REMAP = SMAUL_REMAP;
 };
 // fp32 activations stage two bf16 planes of A, so they keep a 128-row tile
 struct CfgBigF32 {
-  static constexpr int BM = 128, BNB = 128, WM = 2, WN = 2;
+  static constexpr int BM = 128, BNB = 128, WM = 2, WN = 2, MT = 16;
+  static constexpr bool REMAP = SMAUL_REMAP;
 };
 struct CfgSmall {
-  static constexpr int BM = 32, BNB = 128, WM = 1, WN = 4;
+  static constexpr int BM = 32, BNB = 128, WM = 1, WN = 4, MT = 16;
+  static constexpr bool REMAP = false;
 };
 
 int kmode_of(int64_t tile) {
@@ -490,7 +566,8 @@ int launch_gemm_k(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
   if (m_tiles > 65535 || n_tiles > 65535) return fail(SMAUL_ERR_UNSUPPORTED, "gemm grid too large");
   dim3 grid((unsigned)n_tiles, (unsigned)m_tiles);
   hipLaunchKernelGGL(
-      (fp8_gemm_kernel<CF::BM, CF::BNB, CF::WM, CF::WN, SWIGLU, NSPLIT, OUT_BF16, KMODE, CANON, VEC>),
+      (fp8_gemm_kernel<CF::BM, CF::BNB, CF::WM, CF::WN, CF::MT, CF::REMAP, SWIGLU, NSPLIT, OUT_BF16, KMODE,
+                       CANON, VEC>),
       grid, dim3(CF::WM * CF::WN * 64), 0, stream, a);
   return check_launch("fp8_gemm_kernel");
 }
