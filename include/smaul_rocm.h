@@ -79,7 +79,7 @@ int smaul_fp8_canonicalize(const uint8_t* codes, uint8_t* out, int64_t n, hipStr
  * Replaces model.py:558-570 (SwiFFN_MoE.forward router, softmax, topk, renorm).
  * x: x_dtype [T, d]; gate_w fp32 [E, d]; gate_b fp32 [E] or NULL.
  * Outputs: prob fp32 [T, E]; topi int64 [T, k]; topw fp32 [T, k].
- * 1 <= k <= E <= 64.
+ * 1 <= k <= min(E, 8), E <= 64, d a multiple of 8.
  */
 int smaul_moe_router(const void* x, int x_dtype, const float* gate_w, const float* gate_b,
                      float* prob, int64_t* topi, float* topw,
@@ -89,7 +89,7 @@ int smaul_moe_router(const void* x, int x_dtype, const float* gate_w, const floa
  * Deterministic dispatch: for each expert e, the tokens t with a positive
  * routing weight for e, in ascending t (the boolean-mask gather order of
  * model.py:574-581).  Replaces the per-expert mask/gather loop there.
- * Inputs: topi int64 [T, k], topw fp32 [T, k].
+ * Inputs: topi int64 [T, k] (distinct experts per row), topw fp32 [T, k].
  * Outputs (int32 unless noted):
  *   counts  [E]       tokens per expert (model.py:577 `n`)
  *   seg_off [E+1]     first logical row of each expert's segment
@@ -97,12 +97,15 @@ int smaul_moe_router(const void* x, int x_dtype, const float* gate_w, const floa
  *   perm_row[T*k]     logical row -> token index (first seg_off[E] valid)
  *   perm_w  fp32 [T*k] logical row -> routing weight
  *   inv     [T*k]     token slot (t*k + j) -> logical row, -1 if not dispatched
- * block_m must be 16, 32, 64, 128 or 256.
+ * block_m must be 16, 32, 64, 128 or 256.  `workspace` holds
+ * smaul_moe_dispatch_workspace_size(T, E) bytes (per-block counts/offsets).
  */
+int64_t smaul_moe_dispatch_workspace_size(int64_t T, int64_t E);
+
 int smaul_moe_dispatch(const int64_t* topi, const float* topw, int32_t* counts,
                        int32_t* seg_off, int32_t* tile_off, int32_t* perm_row, float* perm_w,
                        int32_t* inv, int64_t T, int64_t E, int64_t k, int64_t block_m,
-                       hipStream_t stream);
+                       void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * Grouped expert GEMMs over the dispatched segments (SwiFFN, model.py:289-290).
@@ -116,8 +119,12 @@ int smaul_moe_dispatch(const int64_t* topi, const float* topw, int32_t* counts,
  * smaul_moe_down: yperm[r, :] = cast(hdn[r] . Wd^T); yperm: act_dtype [T*k, d].
  * seg_off/tile_off come from smaul_moe_dispatch with block_m = smaul_moe_block_m().
  * max_tiles is an upper bound on tile_off[E] (ceil(T*k/block_m) + E).
+ * block_m 16 (chosen for T <= 64, bf16, tile 64, d and h multiples of 128)
+ * selects the decode-regime kernels, which stream each expert's weights once
+ * for all of its rows.
  */
-int smaul_moe_block_m(int64_t T, int64_t k, int64_t E, int act_dtype);
+int smaul_moe_block_m(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile,
+                      int act_dtype);
 
 int smaul_moe_gate_up(const void* x, int act_dtype, const int32_t* perm_row,
                       const uint8_t* const* gate_w, const float* const* gate_s,

@@ -32,8 +32,9 @@ SIGNATURES = {
     "smaul_fp8_linear": (_I, [_P, _I, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I, _P]),
     "smaul_fp8_canonicalize": (_I, [_P, _P, _I64, _P]),
     "smaul_moe_router": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
-    "smaul_moe_dispatch": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
-    "smaul_moe_block_m": (_I, [_I64, _I64, _I64, _I]),
+    "smaul_moe_dispatch_workspace_size": (_I64, [_I64, _I64]),
+    "smaul_moe_dispatch": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
+    "smaul_moe_block_m": (_I, [_I64, _I64, _I64, _I64, _I64, _I64, _I]),
     "smaul_moe_gate_up": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                _I64, _I64, _I, _P]),
     "smaul_moe_down": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P]),

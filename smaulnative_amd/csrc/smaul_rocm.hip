@@ -87,6 +87,20 @@ __device__ __forceinline__ void decode4(uint32_t w, uint32_t& lo, uint32_t& hi) 
   hi = __builtin_bit_cast(uint32_t, b);
 }
 
+// Loads through explicit global-address-space pointers.  Pointers read from
+// memory (per-expert weight tables, gathered rows) are otherwise generic, and
+// a generic (flat) load counts against both the vector-memory and the LDS
+// wait counters, so the compiler drains every outstanding load before the
+// next LDS access.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4_t* g_u4p;
+typedef const __attribute__((address_space(1))) float* g_fp;
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+  const u32x4_t v = *(g_u4p)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float ldgf(const float* p) { return *(g_fp)p; }
+
 // silu(v) = v / (1 + e^-v) with the hardware exp2 and reciprocal (about two
 // ulp in fp32).  Every caller rounds the result to the activation dtype or
 // compares it at a tolerance far above that.
@@ -280,8 +294,7 @@ fp8_gemm_kernel(GemmArgs p) {
     for (int i = 0; i < A_CH; ++i) {
       const int64_t kk = k0 + akoff[i];
       if constexpr (VEC) {
-        ra[i] = (full_k || kk < K) ? *(const uint4*)(arow[i] + kk * (NSPLIT == 1 ? 2 : 4))
-                                   : make_uint4(0, 0, 0, 0);
+        ra[i] = (full_k || kk < K) ? ldg16(arow[i] + kk * (NSPLIT == 1 ? 2 : 4)) : make_uint4(0, 0, 0, 0);
       } else {
         uint32_t v[4] = {0, 0, 0, 0};
         {
@@ -304,7 +317,7 @@ fp8_gemm_kernel(GemmArgs p) {
     for (int i = 0; i < B_CH; ++i) {
       const int64_t kk = k0 + bkoff[i];
       if constexpr (VEC) {
-        rb[i] = (full_k || kk < K) ? *(const uint4*)(brow[i] + kk) : make_uint4(0, 0, 0, 0);
+        rb[i] = (full_k || kk < K) ? ldg16(brow[i] + kk) : make_uint4(0, 0, 0, 0);
       } else {
         uint32_t v[4] = {0, 0, 0, 0};
         {
@@ -321,7 +334,7 @@ fp8_gemm_kernel(GemmArgs p) {
       if constexpr (KMODE == 0) kb = kt * 2 + s_sub[i];
       else if constexpr (KMODE == 1) kb = kt;
       else kb = k0 / p.tile;
-      rs[i] = srow[i][kb < nt ? kb : nt - 1];  // kb == nt only past K (zero data)
+      rs[i] = ldgf(srow[i] + (kb < nt ? kb : nt - 1));  // kb == nt only past K (zero data)
     }
   };
 
@@ -583,215 +596,588 @@ int launch_gemm(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
+// decode-regime grouped GEMM (at most 64 rows per expert)
+// ---------------------------------------------------------------------------
+// One wave owns one expert and one 16-wide output column tile (for SwiGLU the
+// gate and the up tile of the same columns) over the whole K, for all of the
+// expert's rows (1..4 row tiles of 16).  Weight codes stream from HBM straight
+// into registers: lane l reads 16 consecutive codes of column (l & 15) at
+// k = (l >> 4) * 16 inside each 64-wide K block, DB blocks ahead of use, and
+// the A fragments are read with the same k mapping, so every MFMA still sums
+// exactly the products of one 64-wide scale tile.  No LDS, no barriers: the
+// wave's only job is to keep enough loads in flight to stream its weights.
+template <bool SWIGLU, bool OUT_BF16, bool CANON, int NRT, int DB>
+__device__ __forceinline__ void decode_wave(const GemmArgs& p, int e, int row0, int nrows, int64_t col,
+                                            bool col_ok, int lane) {
+  const int64_t K = p.K, nkb = K >> 6, nt = p.nt;
+  const uint8_t* W1 = p.wp[e] + col * K;
+  const float* S1 = p.sp[e] + col * nt;
+  const uint8_t* W2 = SWIGLU ? p.wp2[e] + col * K : W1;
+  const float* S2 = SWIGLU ? p.sp2[e] + col * nt : S1;
+  const int kq = (lane >> 4) * 16;
+  const uint16_t* arow[NRT];
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt) {
+    int r = rt * 16 + (lane & 15);
+    if (r >= nrows) r = nrows - 1;  // rows past the segment: computed, never stored
+    const int64_t lr = row0 + r;
+    const int64_t xr = p.row_idx ? (int64_t)p.row_idx[lr] : lr;
+    arow[rt] = (const uint16_t*)p.x + xr * p.ldx;
+  }
+  f32x4_t acc1[NRT], acc2[NRT];
+  const f32x4_t z4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt) acc1[rt] = acc2[rt] = z4;
+  // Prefetch ring of DB 64-wide K blocks: weight codes, scales and the A
+  // fragments all travel in it, in the order they are consumed, so each
+  // block's wait (vmcnt retires in order) never waits for a later block.
+  uint4 b1[DB], b2[DB], a0[DB][NRT], a1[DB][NRT];
+  float s1[DB], s2[DB];
+  auto fetch = [&](int slot, int64_t kb) {
+    b1[slot] = ldg16(W1 + kb * 64 + kq);
+    s1[slot] = ldgf(S1 + kb);
+    if constexpr (SWIGLU) {
+      b2[slot] = ldg16(W2 + kb * 64 + kq);
+      s2[slot] = ldgf(S2 + kb);
+    }
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+      a0[slot][rt] = ldg16(arow[rt] + kb * 64 + kq);
+      a1[slot][rt] = ldg16(arow[rt] + kb * 64 + kq + 8);
+    }
+  };
+  // consume slot i (block kb); optionally refill it with block kb + DB
+  auto step = [&](int i, bool refill, int64_t next) {
+    uint32_t d[8];
+    decode4<CANON>(b1[i].x, d[0], d[1]);
+    decode4<CANON>(b1[i].y, d[2], d[3]);
+    decode4<CANON>(b1[i].z, d[4], d[5]);
+    decode4<CANON>(b1[i].w, d[6], d[7]);
+    const bf16x8_t g0 = __builtin_bit_cast(bf16x8_t, make_uint4(d[0], d[1], d[2], d[3]));
+    const bf16x8_t g1 = __builtin_bit_cast(bf16x8_t, make_uint4(d[4], d[5], d[6], d[7]));
+    const float sg = s1[i];
+    bf16x8_t u0, u1;
+    float su = 0.0f;
+    if constexpr (SWIGLU) {
+      decode4<CANON>(b2[i].x, d[0], d[1]);
+      decode4<CANON>(b2[i].y, d[2], d[3]);
+      decode4<CANON>(b2[i].z, d[4], d[5]);
+      decode4<CANON>(b2[i].w, d[6], d[7]);
+      u0 = __builtin_bit_cast(bf16x8_t, make_uint4(d[0], d[1], d[2], d[3]));
+      u1 = __builtin_bit_cast(bf16x8_t, make_uint4(d[4], d[5], d[6], d[7]));
+      su = s2[i];
+    }
+    bf16x8_t x0[NRT], x1[NRT];
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+      x0[rt] = __builtin_bit_cast(bf16x8_t, a0[i][rt]);
+      x1[rt] = __builtin_bit_cast(bf16x8_t, a1[i][rt]);
+    }
+    if (refill) fetch(i, next);
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+      f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0[rt], g0, z4, 0, 0, 0);
+      q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1[rt], g1, q, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc1[rt][r] = __builtin_fmaf(sg, q[r], acc1[rt][r]);
+      if constexpr (SWIGLU) {
+        f32x4_t w = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0[rt], u0, z4, 0, 0, 0);
+        w = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1[rt], u1, w, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc2[rt][r] = __builtin_fmaf(su, w[r], acc2[rt][r]);
+      }
+    }
+  };
+  // nkb is a multiple of DB (the launcher picks DB): full rounds with
+  // refills, then a last round without, so no step is conditional.
+#pragma unroll
+  for (int i = 0; i < DB; ++i) fetch(i, i);
+  const int64_t rounds = nkb / DB;
+  for (int64_t r = 0; r + 1 < rounds; ++r) {
+#pragma unroll
+    for (int i = 0; i < DB; ++i) step(i, true, (r + 1) * DB + i);
+  }
+#pragma unroll
+  for (int i = 0; i < DB; ++i) step(i, false, 0);
+  if (!col_ok) return;
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int lr = rt * 16 + (lane >> 4) * 4 + r;
+      if (lr >= nrows) continue;
+      float v;
+      if constexpr (SWIGLU) {
+        float g = acc1[rt][r], u = acc2[rt][r];
+        if constexpr (OUT_BF16) {
+          g = bf2f(f2bf(g));
+          u = bf2f(f2bf(u));
+        }
+        v = silu_f(g) * u;
+      } else {
+        v = acc1[rt][r];
+      }
+      const int64_t orow = row0 + lr;
+      if constexpr (OUT_BF16) ((uint16_t*)p.y)[orow * p.ldy + col] = (uint16_t)f2bf(v);
+      else ((float*)p.y)[orow * p.ldy + col] = v;
+    }
+}
+
+constexpr int DECODE_WAVES = 4;
+
+template <bool SWIGLU, bool OUT_BF16, bool CANON, int DB>
+__global__ void __launch_bounds__(DECODE_WAVES * 64)
+decode_gemm_kernel(GemmArgs p, int col_tiles) {
+  const int lane = threadIdx.x & 63;
+  const int wid = blockIdx.x * DECODE_WAVES + (threadIdx.x >> 6);
+  const int e = wid / col_tiles, ct = wid % col_tiles;
+  if (e >= p.E) return;
+  const int seg0 = p.seg_off[e];
+  const int seg_rows = p.seg_off[e + 1] - seg0;
+  const int64_t c = (int64_t)ct * 16 + (lane & 15);
+  const bool col_ok = c < p.N;
+  const int64_t col = col_ok ? c : p.N - 1;
+  // up to 64 rows per pass (the decode regime has at most 64); more rows
+  // re-stream the weights once per 64
+  for (int rb = 0; rb < seg_rows; rb += 64) {
+    const int row0 = seg0 + rb;
+    const int nrows = min(64, seg_rows - rb);
+    // prefetch depth shrinks as the A fragments per block grow (DB divides
+    // the block count: the launcher guarantees nkb % DB == 0 and DB even)
+    switch ((nrows + 15) >> 4) {
+      case 1: decode_wave<SWIGLU, OUT_BF16, CANON, 1, DB>(p, e, row0, nrows, col, col_ok, lane); break;
+      case 2: decode_wave<SWIGLU, OUT_BF16, CANON, 2, (DB >= 4 ? DB / 2 : DB)>(p, e, row0, nrows, col, col_ok, lane); break;
+      case 3: decode_wave<SWIGLU, OUT_BF16, CANON, 3, (DB >= 4 ? DB / 4 * 2 / 2 : DB)>(p, e, row0, nrows, col, col_ok, lane); break;
+      default: decode_wave<SWIGLU, OUT_BF16, CANON, 4, (DB >= 4 ? DB / 4 * 2 / 2 : DB)>(p, e, row0, nrows, col, col_ok, lane); break;
+    }
+  }
+}
+
+template <bool SWIGLU, bool CANON, int DB>
+int launch_decode_db(const GemmArgs& a, hipStream_t stream) {
+  const int col_tiles = (int)((a.N + 15) / 16);
+  const int64_t waves = (int64_t)a.E * col_tiles;
+  const int64_t blocks = (waves + DECODE_WAVES - 1) / DECODE_WAVES;
+  hipLaunchKernelGGL((decode_gemm_kernel<SWIGLU, true, CANON, DB>), dim3((unsigned)blocks),
+                     dim3(DECODE_WAVES * 64), 0, stream, a, col_tiles);
+  return check_launch("decode_gemm_kernel");
+}
+
+// ring depth: the largest of 8 / 4 / 2 dividing the K block count (K % 128 == 0)
+template <bool SWIGLU, bool CANON>
+int launch_decode(const GemmArgs& a, hipStream_t stream) {
+  const int64_t nkb = a.K / 64;
+  if (nkb % 8 == 0) return launch_decode_db<SWIGLU, CANON, 8>(a, stream);
+  if (nkb % 4 == 0) return launch_decode_db<SWIGLU, CANON, 4>(a, stream);
+  return launch_decode_db<SWIGLU, CANON, 2>(a, stream);
+}
+
+// ---------------------------------------------------------------------------
 // router: logits, softmax, top-k (torch CPU order), renormalisation
 // ---------------------------------------------------------------------------
-// Lanes are (token, expert) pairs: LPT = next power of two >= E lanes per
-// token, 64 / LPT tokens per wave; each lane forms one full dot product in
-// ascending k.  One thread per token then runs softmax and the selection.
-constexpr int ROUTER_THREADS = 256;
+// A workgroup of 16 waves owns a block of TB*16 tokens (64 when E <= 16, else
+// 16).  The router weight is staged in LDS (in column chunks of at most 32 KB);
+// inside a wave the 64 lanes split the model dimension into 8-wide groups
+// (coalesced 16-byte loads of x), each lane keeps TB tokens x EMAX experts of
+// partial dot products, and a butterfly over the lanes completes them.  One
+// thread per token then runs softmax, the top-k selection and the
+// renormalisation, and the block's per-expert dispatch counts are written for
+// the dispatch scan.  With a single block (T <= 64, the decode regime) the
+// same workgroup also performs the dispatch.
+constexpr int ROUTE_THREADS = 1024;
+constexpr int ROUTE_WAVES = ROUTE_THREADS / 64;
+constexpr int MAX_E = 64;
+constexpr int ROUTE_WFLOATS = 8192;  // router-weight chunk staged in LDS (32 KB)
 
-template <bool XBF16>
-__global__ void __launch_bounds__(ROUTER_THREADS)
+struct RouteOut {
+  float* prob;
+  int64_t* topi;
+  float* topw;
+  int32_t* blockcnt;   // [nb][E], or nullptr
+  // fused dispatch (single block only); nullptr otherwise
+  int32_t* counts;
+  int32_t* seg_off;
+  int32_t* tile_off;
+  int32_t* perm_row;
+  float* perm_w;
+  int32_t* inv;
+  int block_m;
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// a slot is dispatched when its weight is positive (model.py:576); ids out of
+// range and repeats of an expert already in the row are not (the router
+// never produces either)
+__device__ __forceinline__ uint64_t selection_of(const int* ti, const float* tw, int E, int k) {
+  uint64_t sel = 0;
+  for (int j = 0; j < k; ++j) {
+    const int ee = ti[j];
+    if (tw[j] > 0.0f && ee >= 0 && ee < E && !((sel >> ee) & 1ull)) sel |= 1ull << ee;
+  }
+  return sel;
+}
+
+template <bool XBF16, int TB, int EMAX>
+__global__ void __launch_bounds__(ROUTE_THREADS)
 router_kernel(const void* __restrict__ x, const float* __restrict__ gw, const float* __restrict__ gb,
-              float* __restrict__ prob, int64_t* __restrict__ topi, float* __restrict__ topw,
-              int64_t T, int d, int E, int k, int lpt_log2) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int lpt = 1 << lpt_log2;
-  const int tpw = 64 >> lpt_log2;                 // tokens per wave
-  const int tpb = tpw * (ROUTER_THREADS / 64);    // tokens per block
-  float* slog = (float*)smem;                     // [tpb][E]
-  smaul_topk::Pair* spair = (smaul_topk::Pair*)(slog + tpb * E);  // [tpb][E]
+              RouteOut o, int64_t T, int d, int E, int k) {
+  constexpr int TPB = TB * ROUTE_WAVES;
+  __shared__ __attribute__((aligned(16))) float sW[ROUTE_WFLOATS];
+  __shared__ float slog[TPB][EMAX];
+  __shared__ smaul_topk::Pair spair[TPB][EMAX];
+  __shared__ int s_ti[TPB][8];
+  __shared__ float s_tw[TPB][8];
+  __shared__ int s_cnt[EMAX];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * TPB;
+  if (tid < EMAX) s_cnt[tid] = 0;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int tl = wave * tpw + (lane >> lpt_log2);
-  const int ex = lane & (lpt - 1);
-  const int64_t t = (int64_t)blockIdx.x * tpb + tl;
-
-  if (t < T && ex < E) {
-    const float* wr = gw + (int64_t)ex * d;
-    float acc = 0.0f;
-    if constexpr (XBF16) {
-      const uint16_t* xr = (const uint16_t*)x + t * d;
-      int kk = 0;
-      if ((d & 7) == 0) {
-        for (; kk < d; kk += 8) {
-          const uint4 xv = *(const uint4*)(xr + kk);
-          const float4 w0 = *(const float4*)(wr + kk);
-          const float4 w1 = *(const float4*)(wr + kk + 4);
-          acc = __builtin_fmaf(bf2f(xv.x & 0xffff), w0.x, acc);
-          acc = __builtin_fmaf(bf2f(xv.x >> 16), w0.y, acc);
-          acc = __builtin_fmaf(bf2f(xv.y & 0xffff), w0.z, acc);
-          acc = __builtin_fmaf(bf2f(xv.y >> 16), w0.w, acc);
-          acc = __builtin_fmaf(bf2f(xv.z & 0xffff), w1.x, acc);
-          acc = __builtin_fmaf(bf2f(xv.z >> 16), w1.y, acc);
-          acc = __builtin_fmaf(bf2f(xv.w & 0xffff), w1.z, acc);
-          acc = __builtin_fmaf(bf2f(xv.w >> 16), w1.w, acc);
-        }
-      }
-      for (; kk < d; ++kk) acc = __builtin_fmaf(bf2f(xr[kk]), wr[kk], acc);
-    } else {
-      const float* xr = (const float*)x + t * d;
-      int kk = 0;
-      if ((d & 3) == 0) {
-        for (; kk < d; kk += 4) {
-          const float4 xv = *(const float4*)(xr + kk);
-          const float4 w0 = *(const float4*)(wr + kk);
-          acc = __builtin_fmaf(xv.x, w0.x, acc);
-          acc = __builtin_fmaf(xv.y, w0.y, acc);
-          acc = __builtin_fmaf(xv.z, w0.z, acc);
-          acc = __builtin_fmaf(xv.w, w0.w, acc);
-        }
-      }
-      for (; kk < d; ++kk) acc = __builtin_fmaf(xr[kk], wr[kk], acc);
+  // ---- logits: this wave's TB tokens ---------------------------------------
+  // Weight rows e >= E are staged as zeros, so the loops below carry no
+  // expert guard and unroll fully.
+  const int64_t tw0 = t0 + wave * TB;
+  float acc[TB * EMAX];
+#pragma unroll
+  for (int i = 0; i < TB * EMAX; ++i) acc[i] = 0.0f;
+  const int dc = min(d, ROUTE_WFLOATS / EMAX);  // chunk of model columns (d % 8 == 0)
+  for (int c0 = 0; c0 < d; c0 += dc) {
+    const int cw = min(dc, d - c0);
+    __syncthreads();
+    for (int i = tid; i < EMAX * (cw >> 2); i += ROUTE_THREADS) {
+      const int e = i / (cw >> 2), q = i % (cw >> 2);
+      float4 w = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (e < E) w = *(const float4*)(gw + (int64_t)e * d + c0 + q * 4);
+      *(float4*)&sW[e * cw + q * 4] = w;
     }
-    if (gb) acc = acc + gb[ex];
-    slog[tl * E + ex] = acc;
+    __syncthreads();
+    for (int g = lane; g < (cw >> 3); g += 64) {
+      float xv[TB][8];
+#pragma unroll
+      for (int a = 0; a < TB; ++a) {
+        const int64_t t = tw0 + a < T ? tw0 + a : T - 1;  // rows past T are computed, never written
+        if constexpr (XBF16) {
+          const uint4 v = ldg16((const uint16_t*)x + t * d + c0 + g * 8);
+          xv[a][0] = bf2f(v.x & 0xffff); xv[a][1] = bf2f(v.x >> 16);
+          xv[a][2] = bf2f(v.y & 0xffff); xv[a][3] = bf2f(v.y >> 16);
+          xv[a][4] = bf2f(v.z & 0xffff); xv[a][5] = bf2f(v.z >> 16);
+          xv[a][6] = bf2f(v.w & 0xffff); xv[a][7] = bf2f(v.w >> 16);
+        } else {
+          const uint4 v0 = ldg16((const float*)x + t * d + c0 + g * 8);
+          const uint4 v1 = ldg16((const float*)x + t * d + c0 + g * 8 + 4);
+          xv[a][0] = __uint_as_float(v0.x); xv[a][1] = __uint_as_float(v0.y);
+          xv[a][2] = __uint_as_float(v0.z); xv[a][3] = __uint_as_float(v0.w);
+          xv[a][4] = __uint_as_float(v1.x); xv[a][5] = __uint_as_float(v1.y);
+          xv[a][6] = __uint_as_float(v1.z); xv[a][7] = __uint_as_float(v1.w);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e) {
+        const float4 w0 = *(const float4*)&sW[e * cw + g * 8];
+        const float4 w1 = *(const float4*)&sW[e * cw + g * 8 + 4];
+        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int a = 0; a < TB; ++a)
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[a * EMAX + e] = __builtin_fmaf(xv[a][q], wv[q], acc[a * EMAX + e]);
+      }
+    }
+  }
+  // Halving butterfly over the 64 lanes: at each step a lane keeps half of
+  // its values and adds the partner's copy of them, so the TB*EMAX sums need
+  // TB*EMAX-1 exchanges in all (instead of 6 per value) and the exchanges of
+  // a step are independent.  Afterwards lane l holds the full sum of value
+  // index vidx(l).
+  {
+    constexpr int N = TB * EMAX;
+    static_assert(N == 32 || N == 64, "router reduction expects 32 or 64 partial sums per lane");
+    int vidx = 0;
+#pragma unroll
+    for (int step = 0; step < 6; ++step) {
+      const int m = 32 >> step;
+      const int n = N >> step;
+      const bool up = (lane & m) != 0;
+      if (n >= 2) {
+        const int half = n >> 1;
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) {
+          if (i < half) {
+            const float give = up ? acc[i] : acc[i + half];
+            const float keep = up ? acc[i + half] : acc[i];
+            acc[i] = keep + __shfl_xor(give, m, 64);
+          }
+        }
+        if (up) vidx += half;
+      } else {
+        acc[0] += __shfl_xor(acc[0], m, 64);
+      }
+    }
+    const int a = vidx / EMAX, e = vidx % EMAX;
+    const bool writer = N == 64 || (lane & 1) == 0;
+    if (writer && e < E) slog[wave * TB + a][e] = gb ? acc[0] + gb[e] : acc[0];
   }
   __syncthreads();
-  if (tid < tpb) {
-    const int64_t tt = (int64_t)blockIdx.x * tpb + tid;
-    if (tt < T) {
-      const float* lg = slog + tid * E;
-      smaul_topk::Pair* q = spair + tid * E;
-      // softmax: max, exp(l - max), sum, multiply by 1/sum
-      float mx = lg[0];  // NaN propagates, as in torch's max reduction
-      for (int i = 1; i < E; ++i) mx = (lg[i] > mx || lg[i] != lg[i]) ? lg[i] : mx;
+
+  // ---- per token: softmax, top-k, renormalisation (model.py:558-570) --------
+  if (tid < TPB) {
+    const int64_t t = t0 + tid;
+    if (t < T) {
+      float v[EMAX];
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e) v[e] = e < E ? slog[tid][e] : 0.0f;
+      float mx = v[0];  // NaN propagates, as in torch's max reduction
+#pragma unroll
+      for (int e = 1; e < EMAX; ++e)
+        if (e < E) mx = (v[e] > mx || v[e] != v[e]) ? v[e] : mx;
       float sum = 0.0f;
-      for (int i = 0; i < E; ++i) {
-        const float ev = expf(lg[i] - mx);
-        q[i].v = ev;
-        sum = sum + ev;
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e)
+        if (e < E) {
+          v[e] = expf(v[e] - mx);
+          sum = sum + v[e];
+        }
+      const float rs = 1.0f / sum;
+      bool ties = false;
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e)
+        if (e < E) {
+          v[e] = v[e] * rs;
+          o.prob[t * E + e] = v[e];
+          ties |= v[e] != v[e];
+        }
+      // Top-k.  With all-distinct values the selection is unique: the k
+      // largest in descending order, found in registers.  Equal values (or
+      // NaN) go through the exact restatement of torch's selection steps.
+      int ti[8];
+      float tv[8];
+      if constexpr (EMAX <= 16) {
+#pragma unroll
+        for (int a = 0; a < EMAX; ++a)
+#pragma unroll
+          for (int b = a + 1; b < EMAX; ++b)
+            if (b < E) ties |= v[a] == v[b];
+      } else {
+        ties = true;
       }
-      const float inv = 1.0f / sum;
-      for (int i = 0; i < E; ++i) {
-        const float pv = q[i].v * inv;
-        q[i].v = pv;
-        q[i].i = i;
-        prob[tt * E + i] = pv;
+      if (!ties) {
+        uint64_t used = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (j < k) {
+            int bi = -1;
+            float bv = 0.0f;
+#pragma unroll
+            for (int e = 0; e < EMAX; ++e)
+              if (e < E && !((used >> e) & 1ull) && (bi < 0 || v[e] > bv)) {
+                bi = e;
+                bv = v[e];
+              }
+            used |= 1ull << bi;
+            ti[j] = bi;
+            tv[j] = bv;
+          }
+        }
+      } else {
+        smaul_topk::Pair* q = spair[tid];
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e)
+          if (e < E) q[e] = smaul_topk::Pair{v[e], e};
+        smaul_topk::topk_small(q, E, k);  // k <= 8
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (j < k) {
+            ti[j] = q[j].i;
+            tv[j] = q[j].v;
+          }
       }
-      smaul_topk::topk(q, E, k);
       float denom = 0.0f;
-      for (int j = 0; j < k; ++j) denom = denom + q[j].v;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < k) denom = denom + tv[j];
       const bool tiny = denom < 1e-6f;
       const float dcl = fmaxf(denom, 1e-9f);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < k) {
+          tv[j] = tiny ? 1.0f / (float)k : tv[j] / dcl;
+          o.topi[t * k + j] = ti[j];
+          o.topw[t * k + j] = tv[j];
+          s_ti[tid][j] = ti[j];
+          s_tw[tid][j] = tv[j];
+        }
+      const uint64_t sel = selection_of(ti, tv, E, k);
+      for (int e = 0; e < E; ++e)
+        if ((sel >> e) & 1ull) atomicAdd(&s_cnt[e], 1);
+    }
+  }
+  __syncthreads();
+  if (o.blockcnt && tid < E) o.blockcnt[(int64_t)blockIdx.x * E + tid] = s_cnt[tid];
+
+  // ---- fused dispatch for a single block (T <= TPB <= 64) -------------------
+  if (o.counts && gridDim.x == 1 && wave == 0) {
+    const int64_t t = lane;
+    const bool valid = t < T && lane < TPB;
+    const uint64_t sel = valid ? selection_of(s_ti[lane], s_tw[lane], E, k) : 0ull;
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    int off = 0, toff = 0;
+    for (int e = 0; e < E; ++e) {
+      const uint64_t b = __ballot((sel >> e) & 1ull);
+      const int n = __popcll(b);
+      if (lane == 0) {
+        o.counts[e] = n;
+        o.seg_off[e] = off;
+        o.tile_off[e] = toff;
+      }
+      if ((sel >> e) & 1ull) {
+        const int pos = off + __popcll(b & lt);
+        o.perm_row[pos] = (int32_t)t;
+        for (int j = 0; j < k; ++j)
+          if (s_ti[lane][j] == e && s_tw[lane][j] > 0.0f) {
+            o.perm_w[pos] = s_tw[lane][j];
+            o.inv[t * k + j] = pos;
+            break;
+          }
+      }
+      off += n;
+      toff += (n + o.block_m - 1) / o.block_m;
+    }
+    if (lane == 0) {
+      o.seg_off[E] = off;
+      o.tile_off[E] = toff;
+    }
+    if (valid) {
+      uint64_t seen = 0;
       for (int j = 0; j < k; ++j) {
-        topi[tt * k + j] = q[j].i;
-        topw[tt * k + j] = tiny ? 1.0f / (float)k : q[j].v / dcl;
+        const int ee = s_ti[lane][j];
+        const bool ok = s_tw[lane][j] > 0.0f && ee >= 0 && ee < E && !((seen >> ee) & 1ull);
+        if (ok) seen |= 1ull << ee;
+        else o.inv[t * k + j] = -1;
       }
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// dispatch (one workgroup): counts, offsets, tile table, ranked permutation
+// dispatch for many blocks: counts per block, scan over blocks, ranked scatter
 // ---------------------------------------------------------------------------
-constexpr int DISPATCH_THREADS = 1024;
-constexpr int MAX_E = 64;
+// Per-expert order is ascending token index (the boolean-mask gather order of
+// model.py:574-581): blocks are consecutive token ranges, a block's tokens are
+// ranked by ballot in token order, and each block starts at the exclusive
+// scan of the earlier blocks' counts.
+constexpr int DISPATCH_TPB = 64;
 
-__global__ void __launch_bounds__(DISPATCH_THREADS)
-dispatch_kernel(const int64_t* __restrict__ topi, const float* __restrict__ topw,
-                int32_t* __restrict__ counts, int32_t* __restrict__ seg_off,
-                int32_t* __restrict__ tile_off, int32_t* __restrict__ perm_row,
-                float* __restrict__ perm_w, int32_t* __restrict__ inv, int64_t T, int E, int k,
-                int block_m) {
-  __shared__ int s_cnt[MAX_E];
-  __shared__ int s_base[MAX_E];
-  __shared__ int s_wc[MAX_E][DISPATCH_THREADS / 64];
+__device__ __forceinline__ uint64_t token_selection(const int64_t* topi, const float* topw, int64_t t,
+                                                    int E, int k) {
+  int ti[8];
+  float tw[8];
+  for (int j = 0; j < k; ++j) {
+    const int64_t v = topi[t * k + j];
+    ti[j] = (v >= 0 && v < E) ? (int)v : -1;
+    tw[j] = topw[t * k + j];
+  }
+  return selection_of(ti, tw, E, k);
+}
+
+__global__ void __launch_bounds__(64)
+block_count_kernel(const int64_t* __restrict__ topi, const float* __restrict__ topw,
+                   int32_t* __restrict__ blockcnt, int64_t T, int E, int k, int tpb) {
+  const int lane = threadIdx.x;
+  const int64_t t = (int64_t)blockIdx.x * tpb + lane;
+  const uint64_t sel = (lane < tpb && t < T) ? token_selection(topi, topw, t, E, k) : 0ull;
+  for (int e = 0; e < E; ++e) {
+    const int n = __popcll(__ballot((sel >> e) & 1ull));
+    if (lane == 0) blockcnt[(int64_t)blockIdx.x * E + e] = n;
+  }
+}
+
+// One wave per expert: a running exclusive scan of the per-block counts in
+// chunks of 64 blocks (shuffle prefix sums), then one thread turns the totals
+// into segment and tile offsets.  blockoff is relative to the segment start.
+constexpr int SCAN_THREADS = 1024;
+
+__global__ void __launch_bounds__(SCAN_THREADS)
+dispatch_scan_kernel(const int32_t* __restrict__ blockcnt, int32_t* __restrict__ blockoff,
+                     int32_t* __restrict__ counts, int32_t* __restrict__ seg_off,
+                     int32_t* __restrict__ tile_off, int64_t nb, int E, int block_m) {
+  __shared__ int s_tot[MAX_E];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  constexpr int NW = DISPATCH_THREADS / 64;
-  if (tid < MAX_E) s_cnt[tid] = 0;
-  __syncthreads();
-  // pass 1: histogram (integer LDS atomics: order does not matter)
-  for (int64_t t = tid; t < T; t += DISPATCH_THREADS) {
-    uint64_t seen = 0;
-    for (int j = 0; j < k; ++j) {
-      const int64_t ee = topi[t * k + j];
-      if (topw[t * k + j] > 0.0f && ee >= 0 && ee < E && !((seen >> ee) & 1ull)) {
-        seen |= 1ull << ee;
-        atomicAdd(&s_cnt[(int)ee], 1);
+  for (int e = wave; e < E; e += SCAN_THREADS / 64) {
+    int running = 0;
+    for (int64_t b0 = 0; b0 < nb; b0 += 64) {
+      const int64_t b = b0 + lane;
+      const int v = b < nb ? blockcnt[b * E + e] : 0;
+      int inc = v;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += u;
       }
+      if (b < nb) blockoff[b * E + e] = running + inc - v;
+      running += __shfl(inc, 63, 64);
     }
+    if (lane == 0) s_tot[e] = running;
   }
   __syncthreads();
   if (tid == 0) {
-    int off = 0, toff = 0;
-    for (int ee = 0; ee < E; ++ee) {
-      counts[ee] = s_cnt[ee];
-      seg_off[ee] = off;
-      tile_off[ee] = toff;
-      s_base[ee] = off;
-      off += s_cnt[ee];
-      toff += (s_cnt[ee] + block_m - 1) / block_m;
+    int base = 0, tbase = 0;
+    for (int e = 0; e < E; ++e) {
+      counts[e] = s_tot[e];
+      seg_off[e] = base;
+      tile_off[e] = tbase;
+      base += s_tot[e];
+      tbase += (s_tot[e] + block_m - 1) / block_m;
     }
-    seg_off[E] = off;
-    tile_off[E] = toff;
+    seg_off[E] = base;
+    tile_off[E] = tbase;
   }
-  __syncthreads();
-  // pass 2: ranks in ascending token order, one round of 1024 tokens at a time
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int64_t r0 = 0; r0 < T; r0 += DISPATCH_THREADS) {
-    const int64_t t = r0 + tid;
-    const bool valid = t < T;
-    int ej[8], rk[8];
-    bool on[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      ej[j] = -1;
-      rk[j] = 0;
-      on[j] = false;
+}
+
+__global__ void __launch_bounds__(64)
+dispatch_scatter_kernel(const int64_t* __restrict__ topi, const float* __restrict__ topw,
+                        const int32_t* __restrict__ blockoff, const int32_t* __restrict__ seg_off,
+                        int32_t* __restrict__ perm_row, float* __restrict__ perm_w, int32_t* __restrict__ inv,
+                        int64_t T, int E, int k, int tpb) {
+  const int lane = threadIdx.x;
+  const int64_t t = (int64_t)blockIdx.x * tpb + lane;
+  const bool valid = lane < tpb && t < T;
+  int ti[8];
+  float tw[8];
+  uint64_t sel = 0;
+  if (valid) {
+    for (int j = 0; j < k; ++j) {
+      const int64_t v = topi[t * k + j];
+      ti[j] = (v >= 0 && v < E) ? (int)v : -1;
+      tw[j] = topw[t * k + j];
     }
-    uint64_t sel = 0;
-    if (valid) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (j < k) {
-          // a slot is dispatched when its weight is positive (model.py:576);
-          // out-of-range ids and repeats of an expert already in the row are
-          // not (the router never produces either)
-          const float w = topw[t * k + j];
-          const int64_t ee = topi[t * k + j];
-          const bool ok = w > 0.0f && ee >= 0 && ee < E && !((sel >> ee) & 1ull);
-          ej[j] = ok ? (int)ee : -1;
-          on[j] = ok;
-          if (ok) sel |= 1ull << ee;
-          else inv[t * k + j] = -1;
-        }
-      }
-    }
-    for (int ee = 0; ee < E; ++ee) {
-      const bool has = (sel >> ee) & 1ull;
-      const uint64_t b = __ballot(has);
-      if (lane == 0) s_wc[ee][wave] = __popcll(b);
-      if (has) {
-        const int rank = __popcll(b & lt_mask);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (on[j] && ej[j] == ee) rk[j] = rank;
-      }
-    }
-    __syncthreads();
-    if (valid) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (j < k && on[j]) {
-          const int ee = ej[j];
-          int pre = 0;
-          for (int ww = 0; ww < wave; ++ww) pre += s_wc[ee][ww];
-          const int pos = s_base[ee] + pre + rk[j];
-          perm_row[pos] = (int32_t)t;
-          perm_w[pos] = topw[t * k + j];
+    sel = selection_of(ti, tw, E, k);
+  }
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const int32_t* off = blockoff + (int64_t)blockIdx.x * E;
+  for (int e = 0; e < E; ++e) {
+    const uint64_t b = __ballot((sel >> e) & 1ull);
+    if ((sel >> e) & 1ull) {
+      const int pos = seg_off[e] + off[e] + __popcll(b & lt);
+      perm_row[pos] = (int32_t)t;
+      for (int j = 0; j < k; ++j)
+        if (ti[j] == e && tw[j] > 0.0f) {
+          perm_w[pos] = tw[j];
           inv[t * k + j] = pos;
+          break;
         }
-      }
     }
-    __syncthreads();
-    if (tid < E) {
-      int tot = 0;
-      for (int ww = 0; ww < NW; ++ww) tot += s_wc[tid][ww];
-      s_base[tid] += tot;
+  }
+  if (valid) {
+    uint64_t seen = 0;
+    for (int j = 0; j < k; ++j) {
+      const int ee = ti[j];
+      const bool ok = tw[j] > 0.0f && ee >= 0 && ee < E && !((seen >> ee) & 1ull);
+      if (ok) seen |= 1ull << ee;
+      else inv[t * k + j] = -1;
     }
-    __syncthreads();
   }
 }
 
@@ -894,7 +1280,14 @@ canonicalize_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ out, i
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 bool dtype_ok(int dt) { return dt == SMAUL_DTYPE_F32 || dt == SMAUL_DTYPE_BF16; }
 
-int pick_block_m(int64_t T, int64_t k, int64_t E, int act_dtype) {
+// block_m 16 selects the decode-regime kernels (at most 64 rows per expert:
+// every token appears at most once per expert, so T <= 64 guarantees it).
+constexpr int DECODE_BM = 16;
+
+bool decode_shape_ok(int64_t d, int64_t h, int64_t tile) { return tile == 64 && d % 128 == 0 && h % 128 == 0; }
+
+int pick_block_m(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile, int act_dtype) {
+  if (T <= 64 && act_dtype == SMAUL_DTYPE_BF16 && decode_shape_ok(d, h, tile)) return DECODE_BM;
   // rows per expert on average; small segments use the 32-row tile
   const int64_t avg = (T * k + E - 1) / (E > 0 ? E : 1);
   if (avg < 96) return CfgSmall::BM;
@@ -983,34 +1376,86 @@ int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* 
                : gemm_dispatch_dense<CfgBigF32, 2>(a, vec, canon, mt, stream);
 }
 
+// router launch shape for E experts: (tokens per wave, expert register width)
+static int route_tpb(int64_t E) { return E <= 16 ? 4 * ROUTE_WAVES : ROUTE_WAVES; }
+
+static int launch_router(const void* x, int x_dtype, const float* gate_w, const float* gate_b,
+                         const RouteOut& o, int64_t T, int64_t d, int64_t E, int64_t k,
+                         hipStream_t stream) {
+  const int64_t tpb = route_tpb(E);
+  const int64_t nb = (T + tpb - 1) / tpb;
+  if (nb > 2147483647LL) return fail(SMAUL_ERR_UNSUPPORTED, "router: too many tokens");
+  const dim3 grid((unsigned)nb), block(ROUTE_THREADS);
+  const bool bf = x_dtype == SMAUL_DTYPE_BF16;
+#define SMAUL_ROUTE(TB, EMAX)                                                                       \
+  if (bf)                                                                                           \
+    hipLaunchKernelGGL((router_kernel<true, TB, EMAX>), grid, block, 0, stream, x, gate_w, gate_b, o, \
+                       T, (int)d, (int)E, (int)k);                                                  \
+  else                                                                                              \
+    hipLaunchKernelGGL((router_kernel<false, TB, EMAX>), grid, block, 0, stream, x, gate_w, gate_b, \
+                       o, T, (int)d, (int)E, (int)k);
+  if (E <= 8) {
+    SMAUL_ROUTE(4, 8)
+  } else if (E <= 16) {
+    SMAUL_ROUTE(4, 16)
+  } else {
+    SMAUL_ROUTE(1, 64)
+  }
+#undef SMAUL_ROUTE
+  return check_launch("router_kernel");
+}
+
+static int check_router_args(const void* x, int x_dtype, const float* gate_w, int64_t T, int64_t d,
+                             int64_t E, int64_t k) {
+  if (T < 0 || d <= 0 || E < 1 || E > MAX_E || k < 1 || k > E || k > 8)
+    return fail(SMAUL_ERR_INVALID, "router: need T>=0, d>0, 1<=k<=min(E,8), E<=64 (T=%lld d=%lld E=%lld k=%lld)",
+                (long long)T, (long long)d, (long long)E, (long long)k);
+  if (!dtype_ok(x_dtype)) return fail(SMAUL_ERR_INVALID, "router: bad x dtype");
+  if (d % 8 != 0) return fail(SMAUL_ERR_UNSUPPORTED, "router: d must be a multiple of 8");
+  if (T > 0 && (!x || !gate_w)) return fail(SMAUL_ERR_INVALID, "router: null pointer");
+  if (T > 0 && (!aligned16(x) || !aligned16(gate_w)))
+    return fail(SMAUL_ERR_INVALID, "router: x and gate_w must be 16-byte aligned");
+  return SMAUL_OK;
+}
+
 int smaul_moe_router(const void* x, int x_dtype, const float* gate_w, const float* gate_b,
                      float* prob, int64_t* topi, float* topw, int64_t T, int64_t d, int64_t E,
                      int64_t k, hipStream_t stream) {
-  if (T < 0 || d <= 0 || E < 1 || E > MAX_E || k < 1 || k > E)
-    return fail(SMAUL_ERR_INVALID, "router: need T>=0, d>0, 1<=k<=E<=64 (T=%lld d=%lld E=%lld k=%lld)",
-                (long long)T, (long long)d, (long long)E, (long long)k);
-  if (!dtype_ok(x_dtype)) return fail(SMAUL_ERR_INVALID, "router: bad x dtype");
+  int rc = check_router_args(x, x_dtype, gate_w, T, d, E, k);
+  if (rc) return rc;
   if (T == 0) return SMAUL_OK;
-  if (!x || !gate_w || !prob || !topi || !topw) return fail(SMAUL_ERR_INVALID, "router: null pointer");
-  if (!aligned16(x) || !aligned16(gate_w))
-    return fail(SMAUL_ERR_INVALID, "router: x and gate_w must be 16-byte aligned");
-  int lpt_log2 = 0;
-  while ((1 << lpt_log2) < E) ++lpt_log2;
-  const int tpb = (64 >> lpt_log2) * (ROUTER_THREADS / 64);
-  const int64_t blocks = (T + tpb - 1) / tpb;
-  const size_t shm = (size_t)tpb * E * (sizeof(float) + sizeof(smaul_topk::Pair));
-  if (x_dtype == SMAUL_DTYPE_BF16)
-    hipLaunchKernelGGL(router_kernel<true>, dim3((unsigned)blocks), dim3(ROUTER_THREADS), shm, stream,
-                       x, gate_w, gate_b, prob, topi, topw, T, (int)d, (int)E, (int)k, lpt_log2);
-  else
-    hipLaunchKernelGGL(router_kernel<false>, dim3((unsigned)blocks), dim3(ROUTER_THREADS), shm, stream,
-                       x, gate_w, gate_b, prob, topi, topw, T, (int)d, (int)E, (int)k, lpt_log2);
-  return check_launch("router_kernel");
+  if (!prob || !topi || !topw) return fail(SMAUL_ERR_INVALID, "router: null output pointer");
+  RouteOut o{};
+  o.prob = prob;
+  o.topi = topi;
+  o.topw = topw;
+  return launch_router(x, x_dtype, gate_w, gate_b, o, T, d, E, k, stream);
+}
+
+int64_t smaul_moe_dispatch_workspace_size(int64_t T, int64_t E) {
+  if (T < 0 || E < 1) return -1;
+  const int64_t nb = (T + DISPATCH_TPB - 1) / DISPATCH_TPB;
+  return align256(nb * E * 4) * 2;
+}
+
+static int launch_scan_scatter(const int64_t* topi, const float* topw, int32_t* blockcnt,
+                               int32_t* blockoff, int32_t* counts, int32_t* seg_off, int32_t* tile_off,
+                               int32_t* perm_row, float* perm_w, int32_t* inv, int64_t T, int64_t E,
+                               int64_t k, int64_t block_m, int64_t tpb, hipStream_t stream) {
+  const int64_t nb = (T + tpb - 1) / tpb;
+  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(SCAN_THREADS), 0, stream, blockcnt, blockoff, counts,
+                     seg_off, tile_off, nb, (int)E, (int)block_m);
+  int rc = check_launch("dispatch_scan_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3((unsigned)nb), dim3(64), 0, stream, topi, topw, blockoff,
+                     seg_off, perm_row, perm_w, inv, T, (int)E, (int)k, (int)tpb);
+  return check_launch("dispatch_scatter_kernel");
 }
 
 int smaul_moe_dispatch(const int64_t* topi, const float* topw, int32_t* counts, int32_t* seg_off,
                        int32_t* tile_off, int32_t* perm_row, float* perm_w, int32_t* inv, int64_t T,
-                       int64_t E, int64_t k, int64_t block_m, hipStream_t stream) {
+                       int64_t E, int64_t k, int64_t block_m, void* workspace, int64_t workspace_bytes,
+                       hipStream_t stream) {
   if (T < 0 || E < 1 || E > MAX_E || k < 1 || k > E || k > 8)
     return fail(SMAUL_ERR_INVALID, "dispatch: need T>=0, 1<=k<=min(E,8), E<=64");
   if (T * k > 2147483647LL) return fail(SMAUL_ERR_UNSUPPORTED, "dispatch: T*k exceeds int32");
@@ -1018,13 +1463,26 @@ int smaul_moe_dispatch(const int64_t* topi, const float* topw, int32_t* counts, 
     return fail(SMAUL_ERR_INVALID, "dispatch: block_m must be 16..256 (power of two)");
   if (!topi || !topw || !counts || !seg_off || !tile_off || !perm_row || !perm_w || !inv)
     return fail(SMAUL_ERR_INVALID, "dispatch: null pointer");
-  hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DISPATCH_THREADS), 0, stream, topi, topw, counts,
-                     seg_off, tile_off, perm_row, perm_w, inv, T, (int)E, (int)k, (int)block_m);
-  return check_launch("dispatch_kernel");
+  const int64_t need = smaul_moe_dispatch_workspace_size(T, E);
+  if (workspace_bytes < need || (need > 0 && !workspace))
+    return fail(SMAUL_ERR_INVALID, "dispatch: workspace %lld < %lld bytes", (long long)workspace_bytes,
+                (long long)need);
+  const int64_t nb = (T + DISPATCH_TPB - 1) / DISPATCH_TPB;
+  int32_t* blockcnt = (int32_t*)workspace;
+  int32_t* blockoff = (int32_t*)((char*)workspace + align256(nb * E * 4));
+  if (nb > 0) {
+    hipLaunchKernelGGL(block_count_kernel, dim3((unsigned)nb), dim3(64), 0, stream, topi, topw, blockcnt, T,
+                       (int)E, (int)k, DISPATCH_TPB);
+    int rc = check_launch("block_count_kernel");
+    if (rc) return rc;
+  }
+  return launch_scan_scatter(topi, topw, blockcnt, blockoff, counts, seg_off, tile_off, perm_row, perm_w, inv,
+                             T, E, k, block_m, DISPATCH_TPB, stream);
 }
 
-int smaul_moe_block_m(int64_t T, int64_t k, int64_t E, int act_dtype) {
-  return pick_block_m(T, k, E, act_dtype);
+int smaul_moe_block_m(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile,
+                      int act_dtype) {
+  return pick_block_m(T, d, h, E, k, tile, act_dtype);
 }
 
 static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* perm_row,
@@ -1039,7 +1497,8 @@ static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* 
   if (K % 16 != 0 || !aligned16(act))
     return fail(SMAUL_ERR_UNSUPPORTED, "moe gemm: K must be a multiple of 16 and activations 16-byte aligned");
   const int64_t big_bm = act_dtype == SMAUL_DTYPE_BF16 ? CfgBig::BM : CfgBigF32::BM;
-  if (!(block_m == big_bm || block_m == CfgSmall::BM))
+  if (!(block_m == big_bm || block_m == CfgSmall::BM ||
+        (block_m == DECODE_BM && act_dtype == SMAUL_DTYPE_BF16)))
     return fail(SMAUL_ERR_INVALID, "moe gemm: block_m must come from smaul_moe_block_m");
   if (!act || !w1 || !s1 || !out || !seg_off || !tile_off || (swiglu && (!w2 || !s2)))
     return fail(SMAUL_ERR_INVALID, "moe gemm: null pointer");
@@ -1062,6 +1521,14 @@ static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* 
   a.tile_off = tile_off;
   a.E = (int)E;
   const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
+  if (block_m == DECODE_BM) {
+    // decode kernels: K in whole 64-wide blocks, one scale per block, rows per
+    // expert <= 64 (the dispatch rows of T <= 64 tokens)
+    if (tile != 64 || K % 128 != 0)
+      return fail(SMAUL_ERR_INVALID, "moe gemm: block_m %d needs tile 64 and K a multiple of 128", DECODE_BM);
+    if (swiglu) return canon ? launch_decode<true, true>(a, stream) : launch_decode<true, false>(a, stream);
+    return canon ? launch_decode<false, true>(a, stream) : launch_decode<false, false>(a, stream);
+  }
   if (block_m == big_bm)
     return gemm_dispatch_moe<CfgBig, CfgBigF32>(a, swiglu, act_dtype, max_tiles, canon, stream);
   return gemm_dispatch_moe<CfgSmall, CfgSmall>(a, swiglu, act_dtype, max_tiles, canon, stream);
@@ -1108,7 +1575,13 @@ int smaul_moe_combine(const void* yperm, int act_dtype, const int64_t* topi, con
 
 // Workspace layout (each piece 256-byte aligned):
 //   seg_off[E+1] tile_off[E+1] perm_row[T*k] perm_w[T*k] inv[T*k]
+//   blockcnt[nb*E] blockoff[nb*E]  (nb = router token blocks)
 //   hdn[T*k, h] (act dtype)  yperm[T*k, d] (act dtype)
+static int64_t route_blocks(int64_t T, int64_t E) {
+  const int64_t tpb = route_tpb(E);
+  return (T + tpb - 1) / tpb;
+}
+
 int64_t smaul_moe_workspace_size(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
                                  int act_dtype) {
   if (T < 0 || d <= 0 || h <= 0 || E < 1 || k < 1 || !dtype_ok(act_dtype)) return -1;
@@ -1117,6 +1590,7 @@ int64_t smaul_moe_workspace_size(int64_t T, int64_t d, int64_t h, int64_t E, int
   int64_t n = 0;
   n += align256((E + 1) * 4) * 2;
   n += align256(R * 4) * 3;
+  n += align256(route_blocks(T, E) * E * 4) * 2;
   n += align256(R * h * el);
   n += align256(R * d * el);
   return n;
@@ -1134,10 +1608,14 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
   if (workspace_bytes < need)
     return fail(SMAUL_ERR_INVALID, "moe_forward: workspace %lld < %lld bytes", (long long)workspace_bytes,
                 (long long)need);
+  int rc = check_router_args(x, act_dtype, gate_w, T, d, E, k);
+  if (rc) return rc;
   if (T == 0) return SMAUL_OK;
+  if (T * k > 2147483647LL) return fail(SMAUL_ERR_UNSUPPORTED, "moe_forward: T*k exceeds int32");
   if (((uintptr_t)workspace & 255u) != 0) return fail(SMAUL_ERR_INVALID, "moe_forward: workspace not 256-byte aligned");
   const int64_t el = act_dtype == SMAUL_DTYPE_BF16 ? 2 : 4;
   const int64_t R = T * k;
+  const int64_t nb = route_blocks(T, E);
   char* ws = (char*)workspace;
   int32_t* seg_off = (int32_t*)ws;
   ws += align256((E + 1) * 4);
@@ -1149,15 +1627,36 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
   ws += align256(R * 4);
   int32_t* inv = (int32_t*)ws;
   ws += align256(R * 4);
+  int32_t* blockcnt = (int32_t*)ws;
+  ws += align256(nb * E * 4);
+  int32_t* blockoff = (int32_t*)ws;
+  ws += align256(nb * E * 4);
   void* hdn = ws;
   ws += align256(R * h * el);
   void* yperm = ws;
 
-  int rc = smaul_moe_router(x, act_dtype, gate_w, gate_b, prob, topi, topw, T, d, E, k, stream);
+  const int64_t bm = pick_block_m(T, d, h, E, k, tile, act_dtype);
+  RouteOut o{};
+  o.prob = prob;
+  o.topi = topi;
+  o.topw = topw;
+  o.blockcnt = blockcnt;
+  o.block_m = (int)bm;
+  if (nb == 1) {  // one router block: it dispatches too
+    o.counts = counts;
+    o.seg_off = seg_off;
+    o.tile_off = tile_off;
+    o.perm_row = perm_row;
+    o.perm_w = perm_w;
+    o.inv = inv;
+  }
+  rc = launch_router(x, act_dtype, gate_w, gate_b, o, T, d, E, k, stream);
   if (rc) return rc;
-  const int64_t bm = pick_block_m(T, k, E, act_dtype);
-  rc = smaul_moe_dispatch(topi, topw, counts, seg_off, tile_off, perm_row, perm_w, inv, T, E, k, bm, stream);
-  if (rc) return rc;
+  if (nb > 1) {
+    rc = launch_scan_scatter(topi, topw, blockcnt, blockoff, counts, seg_off, tile_off, perm_row, perm_w, inv,
+                             T, E, k, bm, route_tpb(E), stream);
+    if (rc) return rc;
+  }
   const int64_t max_tiles = (R + bm - 1) / bm + E;
   rc = smaul_moe_gate_up(x, act_dtype, perm_row, gate_w8, gate_s, up_w8, up_s, hdn, seg_off, tile_off,
                          max_tiles, E, d, h, tile, bm, flags, stream);
@@ -1186,7 +1685,8 @@ int smaul_selftest_topk(const float* vals, int64_t n, int64_t k, int64_t* out_id
     return fail(SMAUL_ERR_INVALID, "selftest_topk: need 1<=k<=n<=64");
   smaul_topk::Pair q[MAX_E];
   for (int i = 0; i < n; ++i) q[i] = smaul_topk::Pair{vals[i], i};
-  smaul_topk::topk(q, (int)n, (int)k);
+  if (k <= 17) smaul_topk::topk_small(q, (int)n, (int)k);  // the router's path
+  else smaul_topk::topk(q, (int)n, (int)k);
   for (int i = 0; i < k; ++i) out_idx[i] = q[i].i;
   return SMAUL_OK;
 }

@@ -2,7 +2,7 @@
 // the CPU, sorted=True, largest=True).
 //
 // torch's CPU top-k (ATen/native/TopKImpl.h, torch 2.x) builds (value, index)
-// pairs and, whenever k * 64 > n (always true for router widths E <= 64),
+// pairs and, whenever k * 64 > n (true for every router width below 64),
 // calls std::nth_element(q, q + k - 1, q + n, cmp) followed by
 // std::sort(q, q + k - 1, cmp) (otherwise std::partial_sort(q, q + k, q + n,
 // cmp)), where cmp(a, b) = (isnan(a) && !isnan(b)) ||
@@ -236,6 +236,19 @@ SMAUL_HD inline void topk(Pair* base, int n, int k) {
   }
   nth_element(base, k - 1, n);
   sort(base, k - 1);
+}
+
+// topk for k <= 17: std::sort on at most 16 elements is a plain insertion
+// sort (the introsort loop needs more than 16), so this is the same order as
+// topk() without the explicit stack.
+SMAUL_HD inline void topk_small(Pair* base, int n, int k) {
+  if (k * 64 <= n) {
+    heap_select(base, k, n);
+    sort_heap(base, k);
+    return;
+  }
+  nth_element(base, k - 1, n);
+  insertion_sort(base, 0, k - 1);
 }
 
 }  // namespace smaul_topk

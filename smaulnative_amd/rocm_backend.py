@@ -259,7 +259,7 @@ class RocmBackend:
         T, k = topi.shape
         E = int(num_experts)
         if block_m is None:
-            block_m = lib.smaul_moe_block_m(T, k, E, _lib.DTYPE_BF16)
+            block_m = 32
         dev = topi.device
         i32 = dict(dtype=torch.int32, device=dev)
         out = {
@@ -270,12 +270,14 @@ class RocmBackend:
             "perm_w": torch.empty(max(1, T * k), dtype=torch.float32, device=dev),
             "inv": torch.empty(max(1, T * k), **i32),
         }
+        ws_bytes = lib.smaul_moe_dispatch_workspace_size(T, E)
+        ws = torch.empty(max(1, ws_bytes), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
             rc = lib.smaul_moe_dispatch(topi.contiguous().data_ptr(), topw.contiguous().data_ptr(),
                                         out["counts"].data_ptr(), out["seg_off"].data_ptr(),
                                         out["tile_off"].data_ptr(), out["perm_row"].data_ptr(),
                                         out["perm_w"].data_ptr(), out["inv"].data_ptr(), T, E, k,
-                                        block_m, _stream_handle(dev))
+                                        block_m, ws.data_ptr(), ws_bytes, _stream_handle(dev))
         _lib.check(rc, "moe_dispatch")
         out["block_m"] = block_m
         return out
@@ -299,7 +301,7 @@ class RocmBackend:
         gw = gate_w.detach().float().contiguous()
         gb = None if gate_b is None else gate_b.detach().float().contiguous()
         R = T * top_k
-        bm = lib.smaul_moe_block_m(T, top_k, E, act)
+        bm = lib.smaul_moe_block_m(T, d, h, E, top_k, tile, act)
         max_tiles = (R + bm - 1) // bm + E
         hdn = torch.empty(max(1, R), h, dtype=x2.dtype, device=dev)
         yperm = torch.empty(max(1, R), d, dtype=x2.dtype, device=dev)

@@ -255,6 +255,22 @@ def test_moe_vs_oracle(T, d, h, E, k, dtype, tile):
     assert err < (2e-3 if dtype == torch.bfloat16 else 1e-5)
 
 
+@pytest.mark.parametrize("T,E,k,skew", [(1, 4, 2, None), (5, 8, 2, None), (33, 8, 3, None), (64, 16, 2, None),
+                                         (64, 8, 2, (9.0, [], 0.0)), (48, 4, 1, None)])
+def test_moe_decode_regime(T, E, k, skew):
+    """T <= 64 runs the decode kernels (weights streamed once per expert)."""
+    print(f"case decode T={T} E={E} k={k} skew={skew}", flush=True)
+    d, h = 256, 640
+    x, gw, gb, experts = make_moe(T * 7 + E, T, d, h, E, k, skew=skew)
+    ref = oracle.moe_forward(x, gw, gb, experts, k)
+    out, prob, topi, counts = gpu_moe(x, gw, gb, experts, k)
+    assert torch.equal(topi.reshape(-1, k), ref.topi.reshape(-1, k))
+    assert counts.tolist() == ref.counts
+    if skew is not None:
+        assert max(ref.counts) == T  # every token picked expert 0: 4 row tiles of 16
+    assert rel_l2(out.float(), ref.out.float()) < 2e-3
+
+
 def test_moe_skewed_segments():
     """Config-5 style skew (one expert ~40 %, three < 1 %) at a reduced size."""
     x, gw, gb, experts = make_moe(55, 2048, 256, 640, 16, 2, skew=(2.2, [13, 14, 15], 4.0))
