@@ -40,8 +40,11 @@ enum { SMAUL_DTYPE_F32 = 0, SMAUL_DTYPE_BF16 = 1 };
 
 /* flags: SMAUL_FLAG_CANONICAL_CODES promises that the code buffers contain no
  * 0x7F/0xFF bytes (see smaul_fp8_canonicalize), which lets the GEMMs skip
- * rewriting them on the fly.  Results are identical either way. */
-enum { SMAUL_FLAG_CANONICAL_CODES = 1 };
+ * rewriting them on the fly.  SMAUL_FLAG_ALIGNED_CODES promises that every
+ * expert code buffer starts on a 16-byte boundary, which lets the grouped
+ * GEMMs stage code rows with 16-byte LDS-DMA loads.  Results are identical
+ * with or without either flag. */
+enum { SMAUL_FLAG_CANONICAL_CODES = 1, SMAUL_FLAG_ALIGNED_CODES = 2 };
 
 /* Library version as an integer (major*10000 + minor*100 + patch). */
 int smaul_version(void);

@@ -20,6 +20,7 @@ SMAUL_ERR_HIP = 3
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 FLAG_CANONICAL_CODES = 1
+FLAG_ALIGNED_CODES = 2
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64

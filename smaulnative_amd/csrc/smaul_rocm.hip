@@ -17,6 +17,7 @@
 // include/smaul_rocm.h.  Nothing here allocates device memory or synchronises.
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <string.h>
@@ -527,6 +528,343 @@ fp8_gemm_kernel(GemmArgs p) {
         }
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// grouped GEMM for bf16 activations and 64-wide scale tiles: LDS-DMA staging,
+// per-wave decode, NSTAGE-deep pipeline
+// ---------------------------------------------------------------------------
+// Per 64-wide K stage a workgroup stages BM activation rows (bf16, 128 B per
+// row), BN weight columns (raw E4M3 codes, 64 B per column) and the BN fp32
+// scales of that K tile straight from global memory into LDS with
+// global_load_lds_dwordx4 / _dword: no staging registers and no VALU work.
+// Each wave then reads its A fragments and its raw codes from LDS, decodes the
+// codes to bf16 in registers (v_cvt_scalef32_pk_bf16_fp8) and runs
+// v_mfma_f32_32x32x16_bf16.  Codes (1 B) instead of decoded bf16 (2 B) in LDS
+// halve the weight side of the LDS traffic and footprint.  NSTAGE stages are
+// in flight: the loads of stage kt + NSTAGE - 1 are issued while stage kt is
+// computed, so the load latency is covered by NSTAGE - 1 stages of MFMA work.
+//
+// K order inside a stage: lane group g = lane / 32 feeds the MFMA k-slots
+// 8g..8g+7 of k-step ks with the actual k = (4g + ks) * 8 + 0..7, for A and
+// for B alike.  The four k-steps of a stage therefore cover the 64 k of one
+// scale tile exactly once; the partial sum of the stage is the same set of
+// exact bf16 x bf16 products, and each lane's A bytes (64) and code bytes (32)
+// of a stage are contiguous.
+//
+// LDS rows keep their 16-byte chunks XOR-swizzled by row index, so the 32
+// consecutive rows that one fragment read touches fall in distinct banks both
+// for 32 banks read 8 lanes at a time and for 64 banks read 16 at a time.
+__device__ __forceinline__ int swz_a(int r) { return (r & 6) | ((r ^ (r >> 3)) & 1); }        // 8 chunks
+__device__ __forceinline__ int swz_b(int r) { return ((r >> 1) & 2) | (((r >> 1) ^ (r >> 3)) & 1); }  // 4
+
+typedef __attribute__((address_space(3))) void* lds_vptr_t;
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) { return (uint32_t)(uintptr_t)(lds_vptr_t)p; }
+
+// LDS DMA: each lane copies 16 (or 4) bytes from base + off to LDS address
+// lds + 16 (or 4) * lane.  Issued as inline asm so the compiler's wait-count
+// pass does not treat every later LDS read as dependent on it (it cannot tell
+// the stage buffers apart); the kernels wait for it explicitly (vmcnt) before
+// the barrier that publishes a buffer.  M0 holds the LDS address (all 32 bits
+// are used: addresses above 64 KB land where they should on gfx950); nothing
+// else in these kernels uses M0.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(off), "s"(base) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(off), "s"(base) : "memory");
+}
+// wait until at most N of this wave's vector-memory loads are outstanding
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+  const bf16x2v v = {(__bf16)a, (__bf16)b};  // v_cvt_pk_bf16_f32: round to nearest even
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+template <int BM, int BN, int WM, int WN, int NSTAGE, bool SWIGLU>
+struct DmaGemmCfg {
+  static constexpr int NW = WM * WN;
+  static constexpr int BNO = SWIGLU ? BN / 2 : BN;       // output columns per workgroup
+  static constexpr int TM = BM / WM;                     // rows per wave
+  static constexpr int TN = BN / WN;                     // staged weight columns per wave
+  static constexpr int TNO = SWIGLU ? TN / 2 : TN;       // output columns per wave
+  static constexpr int FM = TM / 32, FN = TN / 32, FNO = TNO / 32;
+  static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 64, S_BYTES = BN * 4;
+  static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+  static constexpr int A_INS = A_BYTES / 1024 / NW;      // 1 KB DMA instructions per wave per stage
+  static constexpr int B_INS = B_BYTES / 1024 / NW;
+  static constexpr int S_INS = BN / 64;                  // 256 B scale DMAs per stage, waves 0..S_INS-1
+  static constexpr int DMA_MIN = A_INS + B_INS;          // DMAs per stage issued by every wave
+  static constexpr int OUT_LD = BNO + 8;                 // epilogue LDS row (bf16 elements)
+  static constexpr int LDS = (NSTAGE * STAGE > BM * OUT_LD * 2) ? NSTAGE * STAGE : BM * OUT_LD * 2;
+  static_assert(TM % 32 == 0 && TNO % 32 == 0, "wave tile must be a multiple of 32");
+  static_assert(A_INS >= 1 && A_BYTES % (1024 * NW) == 0, "A staging split");
+  static_assert(B_INS >= 1 && B_BYTES % (1024 * NW) == 0, "B staging split");
+  static_assert(S_INS <= NW && BN % 64 == 0, "scale staging split");
+  static_assert(!SWIGLU || BNO % 64 == 0, "gate/up halves must not share a DMA instruction");
+  static_assert(NSTAGE >= 2 && DMA_MIN * (NSTAGE - 2) < 64, "pipeline depth");
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+};
+
+template <int BM, int BN, int WM, int WN, int NSTAGE, bool SWIGLU, bool CANON, bool REMAP>
+__global__ void __launch_bounds__(WM * WN * 64, (WM * WN) / 4)
+fp8_gemm_dma_kernel(GemmArgs p) {
+  using C = DmaGemmCfg<BM, BN, WM, WN, NSTAGE, SWIGLU>;
+  constexpr int NW = C::NW, BNO = C::BNO, TM = C::TM, TN = C::TN, TNO = C::TNO, FM = C::FM, FN = C::FN,
+                FNO = C::FNO, A_BYTES = C::A_BYTES, B_BYTES = C::B_BYTES, STAGE = C::STAGE,
+                A_INS = C::A_INS, B_INS = C::B_INS, S_INS = C::S_INS;
+
+  __shared__ __attribute__((aligned(1024))) char smem[C::LDS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: DMA bases are scalar
+  const int wm = wave / WN, wn = wave % WN;
+
+  int mt, nt_idx;
+  {
+    const int n_tiles = gridDim.x, m_tiles = gridDim.y;
+    const int total = n_tiles * m_tiles;
+    int lin = blockIdx.y * n_tiles + blockIdx.x;
+    if constexpr (REMAP) {
+      constexpr int NXCD = 8;
+      const int full = (total / NXCD) * NXCD;
+      if (lin < full) lin = (lin % NXCD) * (full / NXCD) + lin / NXCD;
+      const int group = GROUP_M * n_tiles;
+      const int g = lin / group, within = lin % group;
+      const int m_first = g * GROUP_M;
+      const int gm = min(GROUP_M, m_tiles - m_first);
+      mt = m_first + within % gm;
+      nt_idx = within / gm;
+    } else {
+      mt = lin / n_tiles;
+      nt_idx = lin % n_tiles;
+    }
+  }
+  int e = 0, row0, rows_here;
+  if (p.seg_off) {
+    const int total = p.tile_off[p.E];
+    if (mt >= total) return;
+    while (p.tile_off[e + 1] <= mt) ++e;
+    row0 = p.seg_off[e] + (mt - p.tile_off[e]) * BM;
+    rows_here = min(BM, p.seg_off[e + 1] - row0);
+  } else {
+    row0 = mt * BM;
+    rows_here = (int)min<int64_t>(BM, p.R - row0);
+  }
+  if (rows_here <= 0) return;
+  const int n0 = nt_idx * BNO;
+  const int64_t K = p.K, nt = p.nt;
+
+  const uint8_t* W1 = p.wp ? p.wp[e] : p.w + e * p.w_estride;
+  const float* S1 = p.sp ? p.sp[e] : p.s + e * p.s_estride;
+  const uint8_t* W2 = W1;
+  const float* S2 = S1;
+  if constexpr (SWIGLU) {
+    W2 = p.wp2 ? p.wp2[e] : p.w2 + e * p.w_estride;
+    S2 = p.sp2 ? p.sp2[e] : p.s2 + e * p.s_estride;
+  }
+
+  // ---- DMA source offsets of this lane (32-bit; the host checks the range) --
+  // A instruction q stages rows 8q..8q+7: lane -> row 8q + lane/8, LDS chunk
+  // lane%8, which holds logical chunk (lane%8) ^ swz_a(row).  Rows past the
+  // segment end load the segment's last row: MFMA output rows depend only on
+  // their own A row and those rows are never stored.
+  uint32_t a_off[A_INS];
+#pragma unroll
+  for (int a = 0; a < A_INS; ++a) {
+    const int r = (wave * A_INS + a) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ swz_a(r);
+    const int64_t lr = row0 + (r < rows_here ? r : rows_here - 1);
+    const int64_t xr = p.row_idx ? (int64_t)p.row_idx[lr] : lr;
+    a_off[a] = (uint32_t)(xr * p.ldx * 2 + c * 16);
+  }
+  // B instruction q stages weight columns 16q..16q+15 (64 B each).  The host
+  // guarantees N % BNO == 0, so every staged column exists, the gate and up
+  // halves of a SwiGLU tile never share an instruction, and the lane's source
+  // offset is the same for all of its instructions (the swizzle depends only
+  // on row bits 1..3): the instruction's column block goes into the scalar
+  // base.
+  uint32_t b_off;
+  {
+    const int r = lane >> 2;
+    b_off = (uint32_t)(r * K + (((lane & 3) ^ swz_b(r)) << 4));
+  }
+  auto b_src = [&](int b) -> const uint8_t* {
+    const int q = wave * B_INS + b;
+    const bool up = SWIGLU && q * 16 >= BNO;
+    const int64_t col0 = n0 + (up ? q * 16 - BNO : q * 16);
+    return (up ? W2 : W1) + col0 * K;
+  };
+  // scale instruction `wave` (waves < S_INS) stages columns 64*wave + lane
+  const float* s_src = S1;
+  if (wave < S_INS) {
+    const bool up = SWIGLU && wave * 64 >= BNO;
+    s_src = (up ? S2 : S1) + (n0 + (up ? wave * 64 - BNO : wave * 64)) * nt;
+  }
+  const uint32_t s_off = (uint32_t)(lane * nt * 4);
+
+  // The K advance of a stage goes into the (scalar) base addresses; the
+  // per-lane offsets stay fixed.  Every wave issues DMA_MIN = A_INS + B_INS
+  // loads per stage, waves < S_INS one more (the scales, issued first).
+  const uint32_t lds0 = lds_offset(&smem[0]);
+  auto dma_stage = [&](int kt, int buf) {
+    const uint32_t lbase = lds0 + (uint32_t)(buf * STAGE);
+    if (S_INS == NW || wave < S_INS) dma4(s_src + kt, s_off, lbase + A_BYTES + B_BYTES + wave * 256);
+    const char* xa = (const char*)p.x + kt * 128;
+#pragma unroll
+    for (int a = 0; a < A_INS; ++a) dma16(xa, a_off[a], lbase + (wave * A_INS + a) * 1024);
+#pragma unroll
+    for (int b = 0; b < B_INS; ++b) dma16(b_src(b) + kt * 64, b_off, lbase + A_BYTES + (wave * B_INS + b) * 1024);
+  };
+
+  // ---- fragment addresses (fixed over K) -----------------------------------
+  // Row tiles are 32 rows apart and the swizzles depend only on row bits 0..3,
+  // so tile i / j adds a constant to the addresses of tile 0.
+  const int g = lane >> 5, l32 = lane & 31;
+  int a_addr[4];
+  {
+    const int r = wm * TM + l32;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) a_addr[ks] = r * 128 + (((g * 4 + ks) ^ swz_a(r)) << 4);
+  }
+  auto b_row = [&](int j) -> int {  // staged weight row of tile j (lane 0)
+    if constexpr (SWIGLU) return j < FNO ? wn * TNO + j * 32 : BNO + wn * TNO + (j - FNO) * 32;
+    else return wn * TN + j * 32;
+  };
+  int b_addr[2];
+  const int s_addr = A_BYTES + B_BYTES + (b_row(0) + l32) * 4;
+  {
+    const int r = b_row(0) + l32;
+    b_addr[0] = A_BYTES + r * 64 + (((g * 2) ^ swz_b(r)) << 4);
+    b_addr[1] = A_BYTES + r * 64 + (((g * 2 + 1) ^ swz_b(r)) << 4);
+  }
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  f32x16_t zacc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) zacc[r] = 0.0f;
+
+  auto compute_stage = [&](int buf) {
+    const char* base = smem + buf * STAGE;
+    bf16x8_t af[FM][4];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) af[i][ks] = *(const bf16x8_t*)(base + a_addr[ks] + i * 32 * 128);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int dj = b_row(j) - b_row(0);
+      const uint4 c0 = *(const uint4*)(base + b_addr[0] + dj * 64);
+      const uint4 c1 = *(const uint4*)(base + b_addr[1] + dj * 64);
+      const float sc = *(const float*)(base + s_addr + dj * 4);
+      uint32_t d[16];
+      decode4<CANON>(c0.x, d[0], d[1]);
+      decode4<CANON>(c0.y, d[2], d[3]);
+      decode4<CANON>(c0.z, d[4], d[5]);
+      decode4<CANON>(c0.w, d[6], d[7]);
+      decode4<CANON>(c1.x, d[8], d[9]);
+      decode4<CANON>(c1.y, d[10], d[11]);
+      decode4<CANON>(c1.z, d[12], d[13]);
+      decode4<CANON>(c1.w, d[14], d[15]);
+      bf16x8_t bfr[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        bfr[ks] = __builtin_bit_cast(bf16x8_t, make_uint4(d[4 * ks], d[4 * ks + 1], d[4 * ks + 2], d[4 * ks + 3]));
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        f32x16_t q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][0], bfr[0], zacc, 0, 0, 0);
+        q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][1], bfr[1], q, 0, 0, 0);
+        q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][2], bfr[2], q, 0, 0, 0);
+        q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][3], bfr[3], q, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(sc, q[r], acc[i][j][r]);
+      }
+    }
+  };
+
+  // ---- the pipeline ----------------------------------------------------------
+  // At the top of iteration kt this wave has the loads of stages
+  // kt .. kt+NSTAGE-2 in flight; waiting until at most (NSTAGE-2)*DMA_MIN are
+  // outstanding completes stage kt (a wave with the extra scale load may also
+  // wait for the oldest load of the next stage, which is only conservative).
+  // The barrier then publishes stage kt and tells every wave that buffer
+  // (kt-1) % NSTAGE, computed in the previous iteration, may be refilled.
+  // Stages past the end re-load the last stage into a buffer nobody reads
+  // again, so the loop body has no branch around its loads (a branch costs
+  // registers and spills).
+  const int nk = (int)(K >> 6);
+#pragma unroll
+  for (int s = 0; s + 1 < NSTAGE; ++s) dma_stage(s < nk ? s : nk - 1, s);
+  int buf = 0, nbuf = NSTAGE - 1;
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_vm<C::DMA_MIN * (NSTAGE - 2)>();
+    __syncthreads();
+    const int ks = kt + NSTAGE - 1;
+    dma_stage(ks < nk ? ks : nk - 1, nbuf);
+    compute_stage(buf);
+    buf = buf + 1 == NSTAGE ? 0 : buf + 1;
+    nbuf = nbuf + 1 == NSTAGE ? 0 : nbuf + 1;
+  }
+  wait_vm<0>();
+  __syncthreads();  // every wave is done with the stage buffers
+
+  // ---- epilogue: through LDS, then 16-byte row stores ----------------------
+  // A lane holds column l32 of each 32x32 tile, rows (r/4)*8 + g*4 + r%4.
+  // The tile is rounded to bf16 (SwiGLU: gate and up rounded first, as the
+  // reference's FP8Linear outputs are, then silu(gate)*up rounded again),
+  // written to LDS as [row][col] and stored row by row.
+  constexpr int OUT_LD = C::OUT_LD;
+  uint16_t* so = (uint16_t*)smem;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FNO; ++j) {
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float v0, v1;
+        if constexpr (SWIGLU) {
+          const uint32_t gb = pack_bf16(acc[i][j][r], acc[i][j][r + 1]);
+          const uint32_t ub = pack_bf16(acc[i][j + FNO][r], acc[i][j + FNO][r + 1]);
+          v0 = silu_f(bf2f(gb & 0xffffu)) * bf2f(ub & 0xffffu);
+          v1 = silu_f(bf2f(gb >> 16)) * bf2f(ub >> 16);
+        } else {
+          v0 = acc[i][j][r];
+          v1 = acc[i][j][r + 1];
+        }
+        const uint32_t o = pack_bf16(v0, v1);
+        const int lr = wm * TM + i * 32 + (r >> 2) * 8 + g * 4 + (r & 3);  // r even: rows lr, lr+1
+        const int lc = wn * TNO + j * 32 + l32;
+        so[lr * OUT_LD + lc] = (uint16_t)(o & 0xffffu);
+        so[(lr + 1) * OUT_LD + lc] = (uint16_t)(o >> 16);
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int CPR = BNO / 8;  // 16-byte chunks per output row
+  for (int c = tid; c < BM * CPR; c += NW * 64) {
+    const int row = c / CPR, ch = c - row * CPR;
+    if (row < rows_here)
+      *(uint4*)((uint16_t*)p.y + (int64_t)(row0 + row) * p.ldy + n0 + ch * 8) =
+          *(const uint4*)(so + row * OUT_LD + ch * 8);
   }
 }
 
@@ -1286,11 +1624,22 @@ constexpr int DECODE_BM = 16;
 
 bool decode_shape_ok(int64_t d, int64_t h, int64_t tile) { return tile == 64 && d % 128 == 0 && h % 128 == 0; }
 
+// block_m 256 selects the LDS-DMA grouped GEMMs (fp8_gemm_dma_kernel).
+constexpr int DMA_BM = 256;
+bool dma_gemm_enabled();
+
 int pick_block_m(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile, int act_dtype) {
   if (T <= 64 && act_dtype == SMAUL_DTYPE_BF16 && decode_shape_ok(d, h, tile)) return DECODE_BM;
   // rows per expert on average; small segments use the 32-row tile
   const int64_t avg = (T * k + E - 1) / (E > 0 ? E : 1);
   if (avg < 96) return CfgSmall::BM;
+  // LDS-DMA kernels: bf16, 64-wide scale tiles, d a multiple of the down
+  // GEMM's 256 output columns, h of the gate/up GEMM's 128, segments long
+  // enough for 256-row tiles, and activation offsets within 31 bits
+  const int64_t rows_bound = T * k + E * DMA_BM;
+  if (act_dtype == SMAUL_DTYPE_BF16 && tile == 64 && avg >= DMA_BM && d % 256 == 0 && h % 128 == 0 &&
+      rows_bound * (d > h ? d : h) * 2 < ((int64_t)1 << 31) && dma_gemm_enabled())
+    return DMA_BM;
   return act_dtype == SMAUL_DTYPE_BF16 ? CfgBig::BM : CfgBigF32::BM;
 }
 
@@ -1319,6 +1668,48 @@ int gemm_dispatch_dense(const GemmArgs& a, bool vec, bool canon, int64_t m_tiles
 }
 
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
+
+// LDS-DMA grouped GEMM shapes: (BM rows, BN staged weight columns, wave
+// grid, pipeline depth).  8 waves (2 per SIMD) and a 3-deep pipeline use
+// 147 KB of LDS: one workgroup per CU.
+struct CfgDmaGU {  // gate+up with the SwiGLU epilogue: 256 rows x 128 outputs
+  static constexpr int BM = 256, BN = 256, WM = 4, WN = 2, NSTAGE = 3;
+};
+struct CfgDmaDown {  // down projection: 256 rows x 256 outputs
+  static constexpr int BM = 256, BN = 256, WM = 4, WN = 2, NSTAGE = 3;
+};
+
+template <class CF, bool SWIGLU, bool CANON>
+int launch_gemm_dma(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
+  constexpr int BNO = SWIGLU ? CF::BN / 2 : CF::BN;
+  const int64_t n_tiles = (a.N + BNO - 1) / BNO;
+  if (m_tiles <= 0 || n_tiles <= 0) return SMAUL_OK;
+  if (m_tiles > 65535 || n_tiles > 65535) return fail(SMAUL_ERR_UNSUPPORTED, "gemm grid too large");
+  hipLaunchKernelGGL((fp8_gemm_dma_kernel<CF::BM, CF::BN, CF::WM, CF::WN, CF::NSTAGE, SWIGLU, CANON, true>),
+                     dim3((unsigned)n_tiles, (unsigned)m_tiles), dim3(CF::WM * CF::WN * 64), 0, stream, a);
+  return check_launch("fp8_gemm_dma_kernel");
+}
+
+// SMAUL_GEMM=legacy makes smaul_moe_block_m never choose the LDS-DMA kernels
+// (for comparisons); anything else lets eligible shapes use them.
+bool dma_gemm_enabled() {
+  static const bool on = [] {
+    const char* v = getenv("SMAUL_GEMM");
+    return !(v && strcmp(v, "legacy") == 0);
+  }();
+  return on;
+}
+
+// The LDS-DMA kernel needs bf16 activations, 64-wide scale tiles, K a
+// multiple of 64, N a multiple of the workgroup's output columns, 16-byte
+// aligned code rows and activation rows, and byte offsets that fit its 32-bit
+// per-lane offsets.
+bool dma_gemm_ok(const GemmArgs& a, int act_dtype, int flags, int64_t x_rows, int64_t bno) {
+  if (act_dtype != SMAUL_DTYPE_BF16 || a.tile != 64 || (a.K & 63) != 0 || a.N % bno != 0) return false;
+  if (!(flags & SMAUL_FLAG_ALIGNED_CODES) || !aligned16(a.x) || (a.ldx & 7) != 0) return false;
+  const int64_t lim = (int64_t)1 << 31;
+  return x_rows * a.ldx * 2 < lim && a.N * a.K < lim && a.N * a.nt < lim;
+}
 
 }  // namespace
 
@@ -1497,7 +1888,7 @@ static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* 
   if (K % 16 != 0 || !aligned16(act))
     return fail(SMAUL_ERR_UNSUPPORTED, "moe gemm: K must be a multiple of 16 and activations 16-byte aligned");
   const int64_t big_bm = act_dtype == SMAUL_DTYPE_BF16 ? CfgBig::BM : CfgBigF32::BM;
-  if (!(block_m == big_bm || block_m == CfgSmall::BM ||
+  if (!(block_m == big_bm || block_m == CfgSmall::BM || block_m == DMA_BM ||
         (block_m == DECODE_BM && act_dtype == SMAUL_DTYPE_BF16)))
     return fail(SMAUL_ERR_INVALID, "moe gemm: block_m must come from smaul_moe_block_m");
   if (!act || !w1 || !s1 || !out || !seg_off || !tile_off || (swiglu && (!w2 || !s2)))
@@ -1528,6 +1919,21 @@ static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* 
       return fail(SMAUL_ERR_INVALID, "moe gemm: block_m %d needs tile 64 and K a multiple of 128", DECODE_BM);
     if (swiglu) return canon ? launch_decode<true, true>(a, stream) : launch_decode<true, false>(a, stream);
     return canon ? launch_decode<false, true>(a, stream) : launch_decode<false, false>(a, stream);
+  }
+  if (block_m == DMA_BM) {
+    static_assert(CfgDmaGU::BM == DMA_BM && CfgDmaDown::BM == DMA_BM, "tile_off row tiles");
+    // row indices of x (tokens, < T <= T*k) and of hdn (< T*k) are both
+    // below max_tiles * block_m
+    if (!dma_gemm_ok(a, act_dtype, flags, max_tiles * block_m, swiglu ? CfgDmaGU::BN / 2 : CfgDmaDown::BN))
+      return fail(SMAUL_ERR_INVALID,
+                  "moe gemm: block_m %d needs bf16, tile 64, K %% 64 == 0, N a multiple of %d, 16-byte aligned "
+                  "activations and code buffers (SMAUL_FLAG_ALIGNED_CODES) and offsets below 2^31",
+                  DMA_BM, swiglu ? CfgDmaGU::BN / 2 : CfgDmaDown::BN);
+    if (swiglu)
+      return canon ? launch_gemm_dma<CfgDmaGU, true, true>(a, max_tiles, stream)
+                   : launch_gemm_dma<CfgDmaGU, true, false>(a, max_tiles, stream);
+    return canon ? launch_gemm_dma<CfgDmaDown, false, true>(a, max_tiles, stream)
+                 : launch_gemm_dma<CfgDmaDown, false, false>(a, max_tiles, stream);
   }
   if (block_m == big_bm)
     return gemm_dispatch_moe<CfgBig, CfgBigF32>(a, swiglu, act_dtype, max_tiles, canon, stream);

@@ -320,12 +320,12 @@ class RocmBackend:
             rc = lib.smaul_moe_gate_up(x2.data_ptr(), act, disp["perm_row"].data_ptr(), tp, tp + row,
                                        tp + 2 * row, tp + 3 * row, hdn.data_ptr(), disp["seg_off"].data_ptr(),
                                        disp["tile_off"].data_ptr(), max_tiles, E, d, h, tile, bm,
-                                       _lib.FLAG_CANONICAL_CODES, sh)
+                                       _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES, sh)
             _lib.check(rc, "moe_gate_up")
             rec(3)
             rc = lib.smaul_moe_down(hdn.data_ptr(), act, tp + 4 * row, tp + 5 * row, yperm.data_ptr(),
                                     disp["seg_off"].data_ptr(), disp["tile_off"].data_ptr(), max_tiles, E, d,
-                                    h, tile, bm, _lib.FLAG_CANONICAL_CODES, sh)
+                                    h, tile, bm, _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES, sh)
             _lib.check(rc, "moe_down")
             rec(4)
             rc = lib.smaul_moe_combine(yperm.data_ptr(), act, topi.data_ptr(), topw.data_ptr(),
@@ -389,7 +389,7 @@ class RocmBackend:
                     tp, tp + row, tp + 2 * row, tp + 3 * row, tp + 4 * row, tp + 5 * row,
                     out.data_ptr(), prob.data_ptr(), topi.data_ptr(), topw.data_ptr(),
                     counts.data_ptr(), ws.data_ptr(), ws_bytes, T, d, h, E, top_k, tile,
-                    _lib.FLAG_CANONICAL_CODES, _stream_handle(dev))
+                    _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES, _stream_handle(dev))
             _lib.check(rc, "moe_forward")
         lead = x.shape[:-1]
         return (out.reshape(*lead, d), prob.reshape(*lead, E), topi.reshape(*lead, top_k), counts)
