@@ -570,13 +570,21 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) { return (uint32_t
 // the barrier that publishes a buffer.  M0 holds the LDS address (all 32 bits
 // are used: addresses above 64 KB land where they should on gfx950); nothing
 // else in these kernels uses M0.
+// The base address is wave-uniform by construction; readfirstlane makes that
+// explicit so it always lands in scalar registers.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(off), "s"(base) : "memory");
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(off), "s"(uniform_ptr(base)) : "memory");
 }
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
-               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(off), "s"(base) : "memory");
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(off), "s"(uniform_ptr(base)) : "memory");
 }
 // wait until at most N of this wave's vector-memory loads are outstanding
 template <int N>
