@@ -942,35 +942,54 @@ int launch_gemm(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// decode-regime grouped GEMM (at most 64 rows per expert)
+// decode-regime grouped GEMM (at most 64 rows per expert), split over K
 // ---------------------------------------------------------------------------
-// One wave owns one expert and one 16-wide output column tile (for SwiGLU the
-// gate and the up tile of the same columns) over the whole K, for all of the
-// expert's rows (1..4 row tiles of 16).  Weight codes stream from HBM straight
-// into registers: lane l reads 16 consecutive codes of column (l & 15) at
-// k = (l >> 4) * 16 inside each 64-wide K block, DB blocks ahead of use, and
-// the A fragments are read with the same k mapping, so every MFMA still sums
-// exactly the products of one 64-wide scale tile.  No LDS, no barriers: the
-// wave's only job is to keep enough loads in flight to stream its weights.
-template <bool SWIGLU, bool OUT_BF16, bool CANON, int NRT, int DB>
-__device__ __forceinline__ void decode_wave(const GemmArgs& p, int e, int row0, int nrows, int64_t col,
-                                            bool col_ok, int lane) {
-  const int64_t K = p.K, nkb = K >> 6, nt = p.nt;
-  const uint8_t* W1 = p.wp[e] + col * K;
-  const float* S1 = p.sp[e] + col * nt;
-  const uint8_t* W2 = SWIGLU ? p.wp2[e] + col * K : W1;
-  const float* S2 = SWIGLU ? p.sp2[e] + col * nt : S1;
+// A workgroup owns one expert and one 16-wide output column tile (for SwiGLU
+// the gate and the up tile of the same columns) for all of the expert's rows
+// (1..4 row tiles of 16).  Its KS waves split the 64-wide K blocks evenly, so
+// a layer runs E * column tiles * KS waves and every wave can keep all (or a
+// large part) of its weight codes in flight at once: the decode GEMMs are
+// bound by how many bytes are outstanding, not by math.  Weight codes stream
+// from HBM straight into registers: lane l reads 16 consecutive codes of
+// column (l & 15) at k = (l >> 4) * 16 inside each 64-wide K block, DB blocks
+// ahead of use, and the A fragments are read with the same k mapping, so
+// every MFMA still sums exactly the products of one 64-wide scale tile.  The
+// waves' fp32 partials are summed through LDS in wave order (deterministic),
+// then wave 0 applies the epilogue.
+// At most 8 K-split waves per workgroup; a one-row-tile wave keeps a ring of
+// 4 K blocks in flight.
+template <bool SWIGLU>
+struct DecodeKS {
+  static constexpr int MAX = 8;
+};
+
+// Entry e of a per-expert pointer table, read through the constant address
+// space: the table is written by the host before the launch and never by a
+// kernel, so the (wave-uniform) read is a scalar load.
+template <class T>
+__device__ __forceinline__ T* table_entry(T* const* table, int e) {
+  typedef __attribute__((address_space(4))) const uint64_t* ctab_t;
+  return (T*)(uintptr_t)((ctab_t)(uintptr_t)table)[e];
+}
+
+// One wave: rows row0..row0+nrows-1 of one expert against 16 weight columns
+// (codes W1 + col*K, scales S1 + col*nt; with SWIGLU also the up columns W2,
+// S2) over K blocks kb0..kb0+nblk-1.  SWIGLU (gate/up) rows are token
+// indices read through p.row_idx; down reads its rows in place.
+template <bool SWIGLU, bool CANON, int NRT, int DB>
+__device__ __forceinline__ void decode_wave(const GemmArgs& p, const uint8_t* W1, const float* S1,
+                                            const uint8_t* W2, const float* S2, int row0, int nrows,
+                                            int64_t kb0, int64_t nblk, int lane, f32x4_t* acc1, f32x4_t* acc2) {
   const int kq = (lane >> 4) * 16;
-  const uint16_t* arow[NRT];
+  // Row indices first; rows past the segment are computed, never stored.
+  int64_t xr[NRT];
 #pragma unroll
   for (int rt = 0; rt < NRT; ++rt) {
-    int r = rt * 16 + (lane & 15);
-    if (r >= nrows) r = nrows - 1;  // rows past the segment: computed, never stored
-    const int64_t lr = row0 + r;
-    const int64_t xr = p.row_idx ? (int64_t)p.row_idx[lr] : lr;
-    arow[rt] = (const uint16_t*)p.x + xr * p.ldx;
+    const int64_t lr = row0 + min(rt * 16 + (lane & 15), nrows - 1);
+    if constexpr (SWIGLU) xr[rt] = p.row_idx[lr];
+    else xr[rt] = lr;
   }
-  f32x4_t acc1[NRT], acc2[NRT];
+  const uint16_t* arow[NRT];
   const f32x4_t z4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int rt = 0; rt < NRT; ++rt) acc1[rt] = acc2[rt] = z4;
@@ -979,20 +998,22 @@ __device__ __forceinline__ void decode_wave(const GemmArgs& p, int e, int row0, 
   // block's wait (vmcnt retires in order) never waits for a later block.
   uint4 b1[DB], b2[DB], a0[DB][NRT], a1[DB][NRT];
   float s1[DB], s2[DB];
-  auto fetch = [&](int slot, int64_t kb) {
+  auto fetch_w = [&](int slot, int64_t kb) {
     b1[slot] = ldg16(W1 + kb * 64 + kq);
     s1[slot] = ldgf(S1 + kb);
     if constexpr (SWIGLU) {
       b2[slot] = ldg16(W2 + kb * 64 + kq);
       s2[slot] = ldgf(S2 + kb);
     }
+  };
+  auto fetch_a = [&](int slot, int64_t kb) {
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
       a0[slot][rt] = ldg16(arow[rt] + kb * 64 + kq);
       a1[slot][rt] = ldg16(arow[rt] + kb * 64 + kq + 8);
     }
   };
-  // consume slot i (block kb); optionally refill it with block kb + DB
+  // consume slot i; optionally refill it with block `next`
   auto step = [&](int i, bool refill, int64_t next) {
     uint32_t d[8];
     decode4<CANON>(b1[i].x, d[0], d[1]);
@@ -1019,7 +1040,10 @@ __device__ __forceinline__ void decode_wave(const GemmArgs& p, int e, int row0, 
       x0[rt] = __builtin_bit_cast(bf16x8_t, a0[i][rt]);
       x1[rt] = __builtin_bit_cast(bf16x8_t, a1[i][rt]);
     }
-    if (refill) fetch(i, next);
+    if (refill) {
+      fetch_w(i, next);
+      fetch_a(i, next);
+    }
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
       f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0[rt], g0, z4, 0, 0, 0);
@@ -1034,103 +1058,134 @@ __device__ __forceinline__ void decode_wave(const GemmArgs& p, int e, int row0, 
       }
     }
   };
-  // nkb is a multiple of DB (the launcher picks DB): full rounds with
-  // refills, then a last round without, so no step is conditional.
+  // nblk is a multiple of DB (the launcher picks DB): full rounds with
+  // refills, then a last round without, so no step is conditional.  The
+  // first round issues every weight load before the activation loads, which
+  // wait for the row indices: the HBM stream starts one round trip earlier.
 #pragma unroll
-  for (int i = 0; i < DB; ++i) fetch(i, i);
-  const int64_t rounds = nkb / DB;
+  for (int i = 0; i < DB; ++i) fetch_w(i, kb0 + i);
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt) arow[rt] = (const uint16_t*)p.x + xr[rt] * p.ldx;
+#pragma unroll
+  for (int i = 0; i < DB; ++i) fetch_a(i, kb0 + i);
+  const int64_t rounds = nblk / DB;
   for (int64_t r = 0; r + 1 < rounds; ++r) {
 #pragma unroll
-    for (int i = 0; i < DB; ++i) step(i, true, (r + 1) * DB + i);
+    for (int i = 0; i < DB; ++i) step(i, true, kb0 + (r + 1) * DB + i);
   }
 #pragma unroll
   for (int i = 0; i < DB; ++i) step(i, false, 0);
-  if (!col_ok) return;
-#pragma unroll
-  for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int lr = rt * 16 + (lane >> 4) * 4 + r;
-      if (lr >= nrows) continue;
-      float v;
-      if constexpr (SWIGLU) {
-        float g = acc1[rt][r], u = acc2[rt][r];
-        if constexpr (OUT_BF16) {
-          g = bf2f(f2bf(g));
-          u = bf2f(f2bf(u));
-        }
-        v = silu_f(g) * u;
-      } else {
-        v = acc1[rt][r];
-      }
-      const int64_t orow = row0 + lr;
-      if constexpr (OUT_BF16) ((uint16_t*)p.y)[orow * p.ldy + col] = (uint16_t)f2bf(v);
-      else ((float*)p.y)[orow * p.ldy + col] = v;
-    }
 }
 
-constexpr int DECODE_WAVES = 4;
-
-template <bool SWIGLU, bool OUT_BF16, bool CANON, int DB>
-__global__ void __launch_bounds__(DECODE_WAVES * 64)
-decode_gemm_kernel(GemmArgs p, int col_tiles) {
+// A workgroup owns one expert and one 16-wide output column tile (for SwiGLU
+// the gate and the up tile of the same columns); its KS waves split the K
+// blocks evenly.
+template <bool SWIGLU, bool CANON, int DB>
+__global__ void __launch_bounds__(DecodeKS<SWIGLU>::MAX * 64)
+decode_gemm_kernel(GemmArgs p, int col_tiles, int ks_count) {
+  constexpr int NH = SWIGLU ? 2 : 1;  // weight streams (gate, up)
+  // every wave's partials: [K split][stream][row tile][r][lane] -- element
+  // (row rt*16 + (lane>>4)*4 + r, column lane & 15) of the 16-column tile
+  __shared__ float red[DecodeKS<SWIGLU>::MAX][NH][4][4][64];
   const int lane = threadIdx.x & 63;
-  const int wid = blockIdx.x * DECODE_WAVES + (threadIdx.x >> 6);
-  const int e = wid / col_tiles, ct = wid % col_tiles;
-  if (e >= p.E) return;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // uniform: the expert's pointer-table entries and segment bounds are scalar loads
+  const int e = __builtin_amdgcn_readfirstlane((int)blockIdx.x / col_tiles);
+  const int ct = (int)blockIdx.x - e * col_tiles;
+  if (e >= p.E) return;  // uniform per workgroup
   const int seg0 = p.seg_off[e];
   const int seg_rows = p.seg_off[e + 1] - seg0;
   const int64_t c = (int64_t)ct * 16 + (lane & 15);
-  const bool col_ok = c < p.N;
-  const int64_t col = col_ok ? c : p.N - 1;
+  const int64_t col = c < p.N ? c : p.N - 1;
+  const uint8_t* W1 = table_entry(p.wp, e) + col * p.K;
+  const float* S1 = table_entry(p.sp, e) + col * p.nt;
+  const uint8_t* W2 = SWIGLU ? table_entry(p.wp2, e) + col * p.K : W1;
+  const float* S2 = SWIGLU ? table_entry(p.sp2, e) + col * p.nt : S1;
+  const int64_t nblk = (p.K >> 6) / ks_count;
+  const int64_t kb0 = ks * nblk;
+  const int nthr = ks_count * 64;
   // up to 64 rows per pass (the decode regime has at most 64); more rows
   // re-stream the weights once per 64
   for (int rb = 0; rb < seg_rows; rb += 64) {
     const int row0 = seg0 + rb;
     const int nrows = min(64, seg_rows - rb);
-    // prefetch depth shrinks as the A fragments per block grow (DB divides
-    // the block count: the launcher guarantees nkb % DB == 0 and DB even)
-    switch ((nrows + 15) >> 4) {
-      case 1: decode_wave<SWIGLU, OUT_BF16, CANON, 1, DB>(p, e, row0, nrows, col, col_ok, lane); break;
-      case 2: decode_wave<SWIGLU, OUT_BF16, CANON, 2, (DB >= 4 ? DB / 2 : DB)>(p, e, row0, nrows, col, col_ok, lane); break;
-      case 3: decode_wave<SWIGLU, OUT_BF16, CANON, 3, (DB >= 4 ? DB / 4 * 2 / 2 : DB)>(p, e, row0, nrows, col, col_ok, lane); break;
-      default: decode_wave<SWIGLU, OUT_BF16, CANON, 4, (DB >= 4 ? DB / 4 * 2 / 2 : DB)>(p, e, row0, nrows, col, col_ok, lane); break;
+    const int nrt = (nrows + 15) >> 4;
+    f32x4_t acc1[4], acc2[4];
+    // prefetch depth shrinks as the A fragments per block grow (the launcher
+    // guarantees nblk % DB == 0 with DB a power of two)
+    switch (nrt) {
+      case 1: decode_wave<SWIGLU, CANON, 1, DB>(p, W1, S1, W2, S2, row0, nrows, kb0, nblk, lane, acc1, acc2); break;
+      case 2: decode_wave<SWIGLU, CANON, 2, (DB >= 2 ? DB / 2 : 1)>(p, W1, S1, W2, S2, row0, nrows, kb0, nblk, lane, acc1, acc2); break;
+      case 3: decode_wave<SWIGLU, CANON, 3, (DB >= 4 ? DB / 4 : 1)>(p, W1, S1, W2, S2, row0, nrows, kb0, nblk, lane, acc1, acc2); break;
+      default: decode_wave<SWIGLU, CANON, 4, (DB >= 4 ? DB / 4 : 1)>(p, W1, S1, W2, S2, row0, nrows, kb0, nblk, lane, acc1, acc2); break;
     }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+      if (rt < nrt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          red[ks][0][rt][r][lane] = acc1[rt][r];
+          if constexpr (SWIGLU) red[ks][NH - 1][rt][r][lane] = acc2[rt][r];
+        }
+    __syncthreads();
+    // The workgroup's threads share the sums (in K-split order,
+    // deterministic) and the epilogue: one output element each.
+    for (int q = threadIdx.x; q < nrt * 256; q += nthr) {
+      const int rt = q >> 8, r = (q >> 6) & 3, ln = q & 63;
+      const int lr = rt * 16 + (ln >> 4) * 4 + r;
+      const int64_t oc = (int64_t)ct * 16 + (ln & 15);
+      float g = red[0][0][rt][r][ln];
+      for (int k2 = 1; k2 < ks_count; ++k2) g += red[k2][0][rt][r][ln];
+      float v = g;
+      if constexpr (SWIGLU) {
+        float u = red[0][NH - 1][rt][r][ln];
+        for (int k2 = 1; k2 < ks_count; ++k2) u += red[k2][NH - 1][rt][r][ln];
+        v = silu_f(bf2f(f2bf(g))) * bf2f(f2bf(u));
+      }
+      if (lr < nrows && oc < p.N) ((uint16_t*)p.y)[(int64_t)(row0 + lr) * p.ldy + oc] = (uint16_t)f2bf(v);
+    }
+    __syncthreads();  // red[] is reused by the next 64-row pass
   }
 }
 
+// SWIGLU (gate/up) gathers its rows through a.row_idx; down reads its rows
+// in place (a.row_idx is null): the decode kernel relies on exactly that.
 template <bool SWIGLU, bool CANON, int DB>
-int launch_decode_db(const GemmArgs& a, hipStream_t stream) {
+int launch_decode_db(const GemmArgs& a, int ks_count, hipStream_t stream) {
+  if (SWIGLU != (a.row_idx != nullptr)) return fail(SMAUL_ERR_INVALID, "decode gemm: row gather mismatch");
   const int col_tiles = (int)((a.N + 15) / 16);
-  const int64_t waves = (int64_t)a.E * col_tiles;
-  const int64_t blocks = (waves + DECODE_WAVES - 1) / DECODE_WAVES;
-  hipLaunchKernelGGL((decode_gemm_kernel<SWIGLU, true, CANON, DB>), dim3((unsigned)blocks),
-                     dim3(DECODE_WAVES * 64), 0, stream, a, col_tiles);
+  const int64_t blocks = (int64_t)a.E * col_tiles;
+  hipLaunchKernelGGL((decode_gemm_kernel<SWIGLU, CANON, DB>), dim3((unsigned)blocks), dim3(ks_count * 64), 0,
+                     stream, a, col_tiles, ks_count);
   return check_launch("decode_gemm_kernel");
 }
 
-// ring depth: the largest of 8 / 4 / 2 dividing the K block count (K % 128 == 0)
 template <bool SWIGLU, bool CANON>
 int launch_decode(const GemmArgs& a, hipStream_t stream) {
   const int64_t nkb = a.K / 64;
-  if (nkb % 8 == 0) return launch_decode_db<SWIGLU, CANON, 8>(a, stream);
-  if (nkb % 4 == 0) return launch_decode_db<SWIGLU, CANON, 4>(a, stream);
-  return launch_decode_db<SWIGLU, CANON, 2>(a, stream);
+  for (int db = 4; db >= 2; db /= 2)
+    for (int ks = DecodeKS<SWIGLU>::MAX; ks >= 1; --ks) {
+      if (nkb % ks != 0 || (nkb / ks) % db != 0) continue;
+      if (db == 4) return launch_decode_db<SWIGLU, CANON, 4>(a, ks, stream);
+      return launch_decode_db<SWIGLU, CANON, 2>(a, ks, stream);
+    }
+  return fail(SMAUL_ERR_INVALID, "decode gemm: K/64 must be even");
 }
 
 // ---------------------------------------------------------------------------
 // router: logits, softmax, top-k (torch CPU order), renormalisation
 // ---------------------------------------------------------------------------
-// A workgroup of 16 waves owns a block of TB*16 tokens (64 when E <= 16, else
-// 16).  The router weight is staged in LDS (in column chunks of at most 32 KB);
-// inside a wave the 64 lanes split the model dimension into 8-wide groups
-// (coalesced 16-byte loads of x), each lane keeps TB tokens x EMAX experts of
-// partial dot products, and a butterfly over the lanes completes them.  One
-// thread per token then runs softmax, the top-k selection and the
-// renormalisation, and the block's per-expert dispatch counts are written for
-// the dispatch scan.  With a single block (T <= 64, the decode regime) the
-// same workgroup also performs the dispatch.
-constexpr int ROUTE_THREADS = 1024;
+// A workgroup of 4 waves owns a block of TB*4 tokens (32 when E <= 4, 16
+// when E <= 16, else 4), so a CU holds several blocks whose phases overlap and
+// a 64-token decode step spreads over several CUs.  The router weight is staged in LDS (in column
+// chunks of at most 32 KB); inside a wave the 64 lanes split the model
+// dimension into 8-wide groups (coalesced 16-byte loads of x), each lane keeps
+// TB tokens x EMAX experts of partial dot products, and a butterfly over the
+// lanes completes them.  One thread per token then runs softmax, the top-k
+// selection and the renormalisation, and the block's per-expert dispatch
+// counts are written for the dispatch scan.  With a single block (T <= TB*4)
+// the same workgroup also performs the dispatch.
+constexpr int ROUTE_THREADS = 256;
 constexpr int ROUTE_WAVES = ROUTE_THREADS / 64;
 constexpr int MAX_E = 64;
 constexpr int ROUTE_WFLOATS = 8192;  // router-weight chunk staged in LDS (32 KB)
@@ -1168,10 +1223,57 @@ __device__ __forceinline__ uint64_t selection_of(const int* ti, const float* tw,
   return sel;
 }
 
-template <bool XBF16, int TB, int EMAX>
+// Deterministic dispatch of up to 64 tokens by one wave: lane t holds token
+// t's top-k ids and weights; each expert's rows are the tokens that selected
+// it, ranked by ballot in ascending token order (model.py:574-581).
+__device__ __forceinline__ void dispatch_one_wave(const int* ti, const float* tw, bool valid, int lane,
+                                                  const RouteOut& o, int E, int k) {
+  const int64_t t = lane;
+  const uint64_t sel = valid ? selection_of(ti, tw, E, k) : 0ull;
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int off = 0, toff = 0;
+  for (int e = 0; e < E; ++e) {
+    const uint64_t b = __ballot((sel >> e) & 1ull);
+    const int n = __popcll(b);
+    if (lane == 0) {
+      o.counts[e] = n;
+      o.seg_off[e] = off;
+      o.tile_off[e] = toff;
+    }
+    if ((sel >> e) & 1ull) {
+      const int pos = off + __popcll(b & lt);
+      o.perm_row[pos] = (int32_t)t;
+      for (int j = 0; j < k; ++j)
+        if (ti[j] == e && tw[j] > 0.0f) {
+          o.perm_w[pos] = tw[j];
+          o.inv[t * k + j] = pos;
+          break;
+        }
+    }
+    off += n;
+    toff += (n + o.block_m - 1) / o.block_m;
+  }
+  if (lane == 0) {
+    o.seg_off[E] = off;
+    o.tile_off[E] = toff;
+  }
+  if (valid) {
+    uint64_t seen = 0;
+    for (int j = 0; j < k; ++j) {
+      const int ee = ti[j];
+      const bool ok = tw[j] > 0.0f && ee >= 0 && ee < E && !((seen >> ee) & 1ull);
+      if (ok) seen |= 1ull << ee;
+      else o.inv[t * k + j] = -1;
+    }
+  }
+}
+
+template <bool XBF16, int TB, int EMAX, bool EXACT>
 __global__ void __launch_bounds__(ROUTE_THREADS)
 router_kernel(const void* __restrict__ x, const float* __restrict__ gw, const float* __restrict__ gb,
-              RouteOut o, int64_t T, int d, int E, int k) {
+              RouteOut o, int64_t T, int d, int E_arg, int k) {
+  // EXACT: E == EMAX, so every expert guard below is decided at compile time
+  const int E = EXACT ? EMAX : E_arg;
   constexpr int TPB = TB * ROUTE_WAVES;
   __shared__ __attribute__((aligned(16))) float sW[ROUTE_WFLOATS];
   __shared__ float slog[TPB][EMAX];
@@ -1190,46 +1292,82 @@ router_kernel(const void* __restrict__ x, const float* __restrict__ gw, const fl
   float acc[TB * EMAX];
 #pragma unroll
   for (int i = 0; i < TB * EMAX; ++i) acc[i] = 0.0f;
-  const int dc = min(d, ROUTE_WFLOATS / EMAX);  // chunk of model columns (d % 8 == 0)
-  for (int c0 = 0; c0 < d; c0 += dc) {
-    const int cw = min(dc, d - c0);
-    __syncthreads();
-    for (int i = tid; i < EMAX * (cw >> 2); i += ROUTE_THREADS) {
-      const int e = i / (cw >> 2), q = i % (cw >> 2);
-      float4 w = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (e < E) w = *(const float4*)(gw + (int64_t)e * d + c0 + q * 4);
-      *(float4*)&sW[e * cw + q * 4] = w;
-    }
-    __syncthreads();
-    for (int g = lane; g < (cw >> 3); g += 64) {
-      float xv[TB][8];
+  // Model columns are processed in chunks of DC (the router-weight chunk that
+  // fits the 32 KB LDS stage).  Per chunk the activations are loaded first:
+  // they do not depend on the staged weights, so their latency overlaps the
+  // weight staging, and every load of a chunk is in flight before any is
+  // used.  The fp32 summation order (per lane: column groups in ascending
+  // order, then the butterfly) does not depend on this load order.
+  constexpr int DC = ROUTE_WFLOATS / EMAX;                                  // columns per chunk
+  constexpr int XG = (DC / 8 + 63) / 64;                                    // 8-column groups per lane
+  constexpr int WI = (EMAX * DC / 4 + ROUTE_THREADS - 1) / ROUTE_THREADS;  // weight float4s per thread
+  constexpr int XW = XBF16 ? 1 : 2;                                         // 16-byte loads per group
+  for (int c0 = 0; c0 < d; c0 += DC) {
+    const int cw = min(DC, d - c0);  // d % 8 == 0
+    uint4 xr[XG][TB][XW];
 #pragma unroll
-      for (int a = 0; a < TB; ++a) {
-        const int64_t t = tw0 + a < T ? tw0 + a : T - 1;  // rows past T are computed, never written
-        if constexpr (XBF16) {
-          const uint4 v = ldg16((const uint16_t*)x + t * d + c0 + g * 8);
-          xv[a][0] = bf2f(v.x & 0xffff); xv[a][1] = bf2f(v.x >> 16);
-          xv[a][2] = bf2f(v.y & 0xffff); xv[a][3] = bf2f(v.y >> 16);
-          xv[a][4] = bf2f(v.z & 0xffff); xv[a][5] = bf2f(v.z >> 16);
-          xv[a][6] = bf2f(v.w & 0xffff); xv[a][7] = bf2f(v.w >> 16);
-        } else {
-          const uint4 v0 = ldg16((const float*)x + t * d + c0 + g * 8);
-          const uint4 v1 = ldg16((const float*)x + t * d + c0 + g * 8 + 4);
-          xv[a][0] = __uint_as_float(v0.x); xv[a][1] = __uint_as_float(v0.y);
-          xv[a][2] = __uint_as_float(v0.z); xv[a][3] = __uint_as_float(v0.w);
-          xv[a][4] = __uint_as_float(v1.x); xv[a][5] = __uint_as_float(v1.y);
-          xv[a][6] = __uint_as_float(v1.z); xv[a][7] = __uint_as_float(v1.w);
+    for (int q = 0; q < XG; ++q) {
+      const int g = lane + 64 * q;
+      if (g < (cw >> 3)) {
+#pragma unroll
+        for (int a = 0; a < TB; ++a) {
+          const int64_t t = tw0 + a < T ? tw0 + a : T - 1;  // rows past T are computed, never written
+          if constexpr (XBF16) {
+            xr[q][a][0] = ldg16((const uint16_t*)x + t * d + c0 + g * 8);
+          } else {
+            xr[q][a][0] = ldg16((const float*)x + t * d + c0 + g * 8);
+            xr[q][a][XW - 1] = ldg16((const float*)x + t * d + c0 + g * 8 + 4);
+          }
         }
       }
+    }
+    __syncthreads();  // the previous chunk's readers are done with sW
+    const int nw = EMAX * (cw >> 2);
+    float4 wv[WI];
 #pragma unroll
-      for (int e = 0; e < EMAX; ++e) {
-        const float4 w0 = *(const float4*)&sW[e * cw + g * 8];
-        const float4 w1 = *(const float4*)&sW[e * cw + g * 8 + 4];
-        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    for (int i = 0; i < WI; ++i) {
+      const int idx = tid + i * ROUTE_THREADS;
+      const int e = idx / (cw >> 2), qq = idx % (cw >> 2);
+      wv[i] = (idx < nw && e < E) ? *(const float4*)(gw + (int64_t)e * d + c0 + qq * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 #pragma unroll
-        for (int a = 0; a < TB; ++a)
+    for (int i = 0; i < WI; ++i) {
+      const int idx = tid + i * ROUTE_THREADS;
+      if (idx < nw) *(float4*)&sW[(idx / (cw >> 2)) * cw + (idx % (cw >> 2)) * 4] = wv[i];
+    }
+    __syncthreads();
 #pragma unroll
-          for (int q = 0; q < 8; ++q) acc[a * EMAX + e] = __builtin_fmaf(xv[a][q], wv[q], acc[a * EMAX + e]);
+    for (int q = 0; q < XG; ++q) {
+      const int g = lane + 64 * q;
+      if (g < (cw >> 3)) {
+        float xv[TB][8];
+#pragma unroll
+        for (int a = 0; a < TB; ++a) {
+          if constexpr (XBF16) {
+            const uint4 v = xr[q][a][0];
+            xv[a][0] = bf2f(v.x & 0xffff); xv[a][1] = bf2f(v.x >> 16);
+            xv[a][2] = bf2f(v.y & 0xffff); xv[a][3] = bf2f(v.y >> 16);
+            xv[a][4] = bf2f(v.z & 0xffff); xv[a][5] = bf2f(v.z >> 16);
+            xv[a][6] = bf2f(v.w & 0xffff); xv[a][7] = bf2f(v.w >> 16);
+          } else {
+            const uint4 v0 = xr[q][a][0], v1 = xr[q][a][XW - 1];
+            xv[a][0] = __uint_as_float(v0.x); xv[a][1] = __uint_as_float(v0.y);
+            xv[a][2] = __uint_as_float(v0.z); xv[a][3] = __uint_as_float(v0.w);
+            xv[a][4] = __uint_as_float(v1.x); xv[a][5] = __uint_as_float(v1.y);
+            xv[a][6] = __uint_as_float(v1.z); xv[a][7] = __uint_as_float(v1.w);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) {
+          const float4 w0 = *(const float4*)&sW[e * cw + g * 8];
+          const float4 w1 = *(const float4*)&sW[e * cw + g * 8 + 4];
+          const float wv8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+          for (int a = 0; a < TB; ++a)
+#pragma unroll
+            for (int qq = 0; qq < 8; ++qq)
+              acc[a * EMAX + e] = __builtin_fmaf(xv[a][qq], wv8[qq], acc[a * EMAX + e]);
+        }
       }
     }
   }
@@ -1247,14 +1385,19 @@ router_kernel(const void* __restrict__ x, const float* __restrict__ gw, const fl
       const int m = 32 >> step;
       const int n = N >> step;
       const bool up = (lane & m) != 0;
+      const uint32_t upmask = up ? 0xffffffffu : 0u;
       if (n >= 2) {
         const int half = n >> 1;
 #pragma unroll
         for (int i = 0; i < N / 2; ++i) {
           if (i < half) {
-            const float give = up ? acc[i] : acc[i + half];
-            const float keep = up ? acc[i + half] : acc[i];
-            acc[i] = keep + __shfl_xor(give, m, 64);
+            // select with a bit mask, not `up ? acc[i] : acc[i + half]`: the
+            // compiler turns that into a dynamically indexed array read (a
+            // compare/select over every element of acc)
+            const uint32_t lo = __float_as_uint(acc[i]), hi = __float_as_uint(acc[i + half]);
+            const uint32_t give = (lo & upmask) | (hi & ~upmask);
+            const uint32_t keep = (hi & upmask) | (lo & ~upmask);
+            acc[i] = __uint_as_float(keep) + __shfl_xor(__uint_as_float(give), m, 64);
           }
         }
         if (up) vidx += half;
@@ -1363,47 +1506,10 @@ router_kernel(const void* __restrict__ x, const float* __restrict__ gw, const fl
   __syncthreads();
   if (o.blockcnt && tid < E) o.blockcnt[(int64_t)blockIdx.x * E + tid] = s_cnt[tid];
 
-  // ---- fused dispatch for a single block (T <= TPB <= 64) -------------------
+  // ---- fused dispatch for a single block (T <= TPB) ---------------------------
   if (o.counts && gridDim.x == 1 && wave == 0) {
-    const int64_t t = lane;
-    const bool valid = t < T && lane < TPB;
-    const uint64_t sel = valid ? selection_of(s_ti[lane], s_tw[lane], E, k) : 0ull;
-    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    int off = 0, toff = 0;
-    for (int e = 0; e < E; ++e) {
-      const uint64_t b = __ballot((sel >> e) & 1ull);
-      const int n = __popcll(b);
-      if (lane == 0) {
-        o.counts[e] = n;
-        o.seg_off[e] = off;
-        o.tile_off[e] = toff;
-      }
-      if ((sel >> e) & 1ull) {
-        const int pos = off + __popcll(b & lt);
-        o.perm_row[pos] = (int32_t)t;
-        for (int j = 0; j < k; ++j)
-          if (s_ti[lane][j] == e && s_tw[lane][j] > 0.0f) {
-            o.perm_w[pos] = s_tw[lane][j];
-            o.inv[t * k + j] = pos;
-            break;
-          }
-      }
-      off += n;
-      toff += (n + o.block_m - 1) / o.block_m;
-    }
-    if (lane == 0) {
-      o.seg_off[E] = off;
-      o.tile_off[E] = toff;
-    }
-    if (valid) {
-      uint64_t seen = 0;
-      for (int j = 0; j < k; ++j) {
-        const int ee = s_ti[lane][j];
-        const bool ok = s_tw[lane][j] > 0.0f && ee >= 0 && ee < E && !((seen >> ee) & 1ull);
-        if (ok) seen |= 1ull << ee;
-        else o.inv[t * k + j] = -1;
-      }
-    }
+    const bool valid = lane < T && lane < TPB;
+    dispatch_one_wave(s_ti[valid ? lane : 0], s_tw[valid ? lane : 0], valid, lane, o, E, k);
   }
 }
 
@@ -1525,6 +1631,23 @@ dispatch_scatter_kernel(const int64_t* __restrict__ topi, const float* __restric
       else inv[t * k + j] = -1;
     }
   }
+}
+
+// Dispatch of at most 64 tokens in one wave, straight from the router outputs
+// (the decode regime: one launch instead of block counts, scan and scatter).
+__global__ void __launch_bounds__(64)
+dispatch_small_kernel(const int64_t* __restrict__ topi, const float* __restrict__ topw, RouteOut o, int64_t T,
+                      int E, int k) {
+  const int lane = threadIdx.x;
+  const bool valid = lane < T;
+  int ti[8];
+  float tw[8];
+  for (int j = 0; j < k; ++j) {
+    const int64_t v = valid ? topi[lane * k + j] : -1;
+    ti[j] = (v >= 0 && v < E) ? (int)v : -1;
+    tw[j] = valid ? topw[lane * k + j] : 0.0f;
+  }
+  dispatch_one_wave(ti, tw, valid, lane, o, E, k);
 }
 
 // ---------------------------------------------------------------------------
@@ -1776,7 +1899,10 @@ int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* 
 }
 
 // router launch shape for E experts: (tokens per wave, expert register width)
-static int route_tpb(int64_t E) { return E <= 16 ? 4 * ROUTE_WAVES : ROUTE_WAVES; }
+// router tokens per wave for E experts (E <= 4, 8, 16, 64): TB * EMAX partial
+// sums per lane
+static constexpr int route_tb(int64_t E) { return E <= 4 ? 8 : E <= 16 ? 4 : 1; }
+static int route_tpb(int64_t E) { return route_tb(E) * ROUTE_WAVES; }
 
 static int launch_router(const void* x, int x_dtype, const float* gate_w, const float* gate_b,
                          const RouteOut& o, int64_t T, int64_t d, int64_t E, int64_t k,
@@ -1786,20 +1912,31 @@ static int launch_router(const void* x, int x_dtype, const float* gate_w, const 
   if (nb > 2147483647LL) return fail(SMAUL_ERR_UNSUPPORTED, "router: too many tokens");
   const dim3 grid((unsigned)nb), block(ROUTE_THREADS);
   const bool bf = x_dtype == SMAUL_DTYPE_BF16;
-#define SMAUL_ROUTE(TB, EMAX)                                                                       \
-  if (bf)                                                                                           \
-    hipLaunchKernelGGL((router_kernel<true, TB, EMAX>), grid, block, 0, stream, x, gate_w, gate_b, o, \
-                       T, (int)d, (int)E, (int)k);                                                  \
-  else                                                                                              \
-    hipLaunchKernelGGL((router_kernel<false, TB, EMAX>), grid, block, 0, stream, x, gate_w, gate_b, \
+#define SMAUL_ROUTE1(TB, EMAX, EXACT)                                                                     \
+  if (bf)                                                                                                 \
+    hipLaunchKernelGGL((router_kernel<true, TB, EMAX, EXACT>), grid, block, 0, stream, x, gate_w, gate_b, o, \
+                       T, (int)d, (int)E, (int)k);                                                        \
+  else                                                                                                    \
+    hipLaunchKernelGGL((router_kernel<false, TB, EMAX, EXACT>), grid, block, 0, stream, x, gate_w, gate_b, \
                        o, T, (int)d, (int)E, (int)k);
-  if (E <= 8) {
-    SMAUL_ROUTE(4, 8)
-  } else if (E <= 16) {
-    SMAUL_ROUTE(4, 16)
-  } else {
-    SMAUL_ROUTE(1, 64)
+#define SMAUL_ROUTE(TB, EMAX)    \
+  if (E == EMAX) {               \
+    SMAUL_ROUTE1(TB, EMAX, true)  \
+  } else {                       \
+    SMAUL_ROUTE1(TB, EMAX, false) \
   }
+  static_assert(route_tb(4) * 4 == 32 && route_tb(8) * 8 == 32 && route_tb(16) * 16 == 64 && route_tb(64) * 64 == 64,
+                "router butterfly expects 32 or 64 partial sums per lane");
+  if (E <= 4) {
+    SMAUL_ROUTE(route_tb(4), 4)
+  } else if (E <= 8) {
+    SMAUL_ROUTE(route_tb(8), 8)
+  } else if (E <= 16) {
+    SMAUL_ROUTE(route_tb(16), 16)
+  } else {
+    SMAUL_ROUTE(route_tb(64), 64)
+  }
+#undef SMAUL_ROUTE1
 #undef SMAUL_ROUTE
   return check_launch("router_kernel");
 }
@@ -2066,7 +2203,18 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
   }
   rc = launch_router(x, act_dtype, gate_w, gate_b, o, T, d, E, k, stream);
   if (rc) return rc;
-  if (nb > 1) {
+  if (nb > 1 && T <= 64) {  // one wave dispatches straight from topi/topw
+    RouteOut od = o;
+    od.counts = counts;
+    od.seg_off = seg_off;
+    od.tile_off = tile_off;
+    od.perm_row = perm_row;
+    od.perm_w = perm_w;
+    od.inv = inv;
+    hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(64), 0, stream, topi, topw, od, T, (int)E, (int)k);
+    rc = check_launch("dispatch_small_kernel");
+    if (rc) return rc;
+  } else if (nb > 1) {
     rc = launch_scan_scatter(topi, topw, blockcnt, blockoff, counts, seg_off, tile_off, perm_row, perm_w, inv,
                              T, E, k, bm, route_tpb(E), stream);
     if (rc) return rc;
