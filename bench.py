@@ -237,7 +237,7 @@ def main():
     flops_down = 2.0 * R * h * d
     total_flops = flops_router + flops_gate_up + flops_down
     gu_s = stages["gate_up"] * 1e-3
-    roof = {"kernel": "fp8_gemm_kernel (gate_up, SwiGLU epilogue)", "bound": "mfma",
+    roof = {"kernel": "fp8_gemm_dma_kernel (gate_up, SwiGLU epilogue)", "bound": "mfma",
             "achieved": flops_gate_up / gu_s / 1e12, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
             "frac": flops_gate_up / gu_s / PEAK_BF16_FLOPS, "traffic": read_traffic(),
             "flops_per_launch": flops_gate_up, "mean_launch_ms": stages["gate_up"]}

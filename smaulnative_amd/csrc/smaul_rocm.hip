@@ -972,15 +972,21 @@ __device__ __forceinline__ T* table_entry(T* const* table, int e) {
   return (T*)(uintptr_t)((ctab_t)(uintptr_t)table)[e];
 }
 
-// One wave: rows row0..row0+nrows-1 of one expert against 16 weight columns
-// (codes W1 + col*K, scales S1 + col*nt; with SWIGLU also the up columns W2,
-// S2) over K blocks kb0..kb0+nblk-1.  SWIGLU (gate/up) rows are token
-// indices read through p.row_idx; down reads its rows in place.
-template <bool SWIGLU, bool CANON, int NRT, int DB>
+// One wave: rows row0..row0+nrows-1 of one expert against CT tiles of 16
+// weight columns (tile t: codes W1 + t*16*K, scales S1 + t*16*nt, the lane's
+// column already folded in; with SWIGLU also the up columns W2, S2) over K
+// blocks kb0..kb0+nblk-1.  The CT tiles share the wave's A fragments, so per
+// byte of weight codes streamed from HBM the wave loads 1/CT of the
+// activation bytes.  SWIGLU (gate/up) rows are token indices read through
+// p.row_idx; down reads its rows in place.
+template <bool SWIGLU, bool CANON, int NRT, int DB, int CT>
 __device__ __forceinline__ void decode_wave(const GemmArgs& p, const uint8_t* W1, const float* S1,
                                             const uint8_t* W2, const float* S2, int row0, int nrows,
-                                            int64_t kb0, int64_t nblk, int lane, f32x4_t* acc1, f32x4_t* acc2) {
+                                            int64_t kb0, int64_t nblk, int lane, f32x4_t (*acc1)[4],
+                                            f32x4_t (*acc2)[4]) {
+  constexpr int NH = SWIGLU ? 2 : 1;
   const int kq = (lane >> 4) * 16;
+  const int64_t tstride_w = 16 * p.K, tstride_s = 16 * p.nt;
   // Row indices first; rows past the segment are computed, never stored.
   int64_t xr[NRT];
 #pragma unroll
@@ -992,19 +998,22 @@ __device__ __forceinline__ void decode_wave(const GemmArgs& p, const uint8_t* W1
   const uint16_t* arow[NRT];
   const f32x4_t z4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int rt = 0; rt < NRT; ++rt) acc1[rt] = acc2[rt] = z4;
+  for (int t = 0; t < CT; ++t)
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) acc1[t][rt] = acc2[t][rt] = z4;
   // Prefetch ring of DB 64-wide K blocks: weight codes, scales and the A
   // fragments all travel in it, in the order they are consumed, so each
   // block's wait (vmcnt retires in order) never waits for a later block.
-  uint4 b1[DB], b2[DB], a0[DB][NRT], a1[DB][NRT];
-  float s1[DB], s2[DB];
+  uint4 bw[DB][NH][CT], a0[DB][NRT], a1[DB][NRT];
+  float sw[DB][NH][CT];
   auto fetch_w = [&](int slot, int64_t kb) {
-    b1[slot] = ldg16(W1 + kb * 64 + kq);
-    s1[slot] = ldgf(S1 + kb);
-    if constexpr (SWIGLU) {
-      b2[slot] = ldg16(W2 + kb * 64 + kq);
-      s2[slot] = ldgf(S2 + kb);
-    }
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (int t = 0; t < CT; ++t) {
+        bw[slot][h][t] = ldg16((h ? W2 : W1) + t * tstride_w + kb * 64 + kq);
+        sw[slot][h][t] = ldgf((h ? S2 : S1) + t * tstride_s + kb);
+      }
   };
   auto fetch_a = [&](int slot, int64_t kb) {
 #pragma unroll
@@ -1015,25 +1024,21 @@ __device__ __forceinline__ void decode_wave(const GemmArgs& p, const uint8_t* W1
   };
   // consume slot i; optionally refill it with block `next`
   auto step = [&](int i, bool refill, int64_t next) {
-    uint32_t d[8];
-    decode4<CANON>(b1[i].x, d[0], d[1]);
-    decode4<CANON>(b1[i].y, d[2], d[3]);
-    decode4<CANON>(b1[i].z, d[4], d[5]);
-    decode4<CANON>(b1[i].w, d[6], d[7]);
-    const bf16x8_t g0 = __builtin_bit_cast(bf16x8_t, make_uint4(d[0], d[1], d[2], d[3]));
-    const bf16x8_t g1 = __builtin_bit_cast(bf16x8_t, make_uint4(d[4], d[5], d[6], d[7]));
-    const float sg = s1[i];
-    bf16x8_t u0, u1;
-    float su = 0.0f;
-    if constexpr (SWIGLU) {
-      decode4<CANON>(b2[i].x, d[0], d[1]);
-      decode4<CANON>(b2[i].y, d[2], d[3]);
-      decode4<CANON>(b2[i].z, d[4], d[5]);
-      decode4<CANON>(b2[i].w, d[6], d[7]);
-      u0 = __builtin_bit_cast(bf16x8_t, make_uint4(d[0], d[1], d[2], d[3]));
-      u1 = __builtin_bit_cast(bf16x8_t, make_uint4(d[4], d[5], d[6], d[7]));
-      su = s2[i];
-    }
+    bf16x8_t g0[NH][CT], g1[NH][CT];
+    float sg[NH][CT];
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (int t = 0; t < CT; ++t) {
+        uint32_t d[8];
+        decode4<CANON>(bw[i][h][t].x, d[0], d[1]);
+        decode4<CANON>(bw[i][h][t].y, d[2], d[3]);
+        decode4<CANON>(bw[i][h][t].z, d[4], d[5]);
+        decode4<CANON>(bw[i][h][t].w, d[6], d[7]);
+        g0[h][t] = __builtin_bit_cast(bf16x8_t, make_uint4(d[0], d[1], d[2], d[3]));
+        g1[h][t] = __builtin_bit_cast(bf16x8_t, make_uint4(d[4], d[5], d[6], d[7]));
+        sg[h][t] = sw[i][h][t];
+      }
     bf16x8_t x0[NRT], x1[NRT];
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
@@ -1045,18 +1050,17 @@ __device__ __forceinline__ void decode_wave(const GemmArgs& p, const uint8_t* W1
       fetch_a(i, next);
     }
 #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) {
-      f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0[rt], g0, z4, 0, 0, 0);
-      q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1[rt], g1, q, 0, 0, 0);
+    for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc1[rt][r] = __builtin_fmaf(sg, q[r], acc1[rt][r]);
-      if constexpr (SWIGLU) {
-        f32x4_t w = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0[rt], u0, z4, 0, 0, 0);
-        w = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1[rt], u1, w, 0, 0, 0);
+      for (int h = 0; h < NH; ++h)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc2[rt][r] = __builtin_fmaf(su, w[r], acc2[rt][r]);
-      }
-    }
+        for (int t = 0; t < CT; ++t) {
+          f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0[rt], g0[h][t], z4, 0, 0, 0);
+          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1[rt], g1[h][t], q, 0, 0, 0);
+          f32x4_t& acc = h ? acc2[t][rt] : acc1[t][rt];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(sg[h][t], q[r], acc[r]);
+        }
   };
   // nblk is a multiple of DB (the launcher picks DB): full rounds with
   // refills, then a last round without, so no step is conditional.  The
@@ -1077,26 +1081,33 @@ __device__ __forceinline__ void decode_wave(const GemmArgs& p, const uint8_t* W1
   for (int i = 0; i < DB; ++i) step(i, false, 0);
 }
 
-// A workgroup owns one expert and one 16-wide output column tile (for SwiGLU
-// the gate and the up tile of the same columns); its KS waves split the K
+// A workgroup owns one expert and DecodeCT output column tiles of 16 (for
+// SwiGLU the gate and the up tiles of the same columns: one tile, two weight
+// streams; for down two tiles of one stream); its KS waves split the K
 // blocks evenly.
+template <bool SWIGLU>
+constexpr int DecodeCT = SWIGLU ? 1 : 2;
+
 template <bool SWIGLU, bool CANON, int DB>
 __global__ void __launch_bounds__(DecodeKS<SWIGLU>::MAX * 64)
-decode_gemm_kernel(GemmArgs p, int col_tiles, int ks_count) {
+decode_gemm_kernel(GemmArgs p, int col_groups, int ks_count) {
   constexpr int NH = SWIGLU ? 2 : 1;  // weight streams (gate, up)
-  // every wave's partials: [K split][stream][row tile][r][lane] -- element
-  // (row rt*16 + (lane>>4)*4 + r, column lane & 15) of the 16-column tile
-  __shared__ float red[DecodeKS<SWIGLU>::MAX][NH][4][4][64];
+  constexpr int CT = DecodeCT<SWIGLU>;
+  // every wave's partials: [K split][stream][tile][row tile][r][lane] -- element
+  // (row rt*16 + (lane>>4)*4 + r, column t*16 + (lane & 15)) of the group
+  __shared__ float red[DecodeKS<SWIGLU>::MAX][NH][CT][4][4][64];
   const int lane = threadIdx.x & 63;
   const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // uniform: the expert's pointer-table entries and segment bounds are scalar loads
-  const int e = __builtin_amdgcn_readfirstlane((int)blockIdx.x / col_tiles);
-  const int ct = (int)blockIdx.x - e * col_tiles;
+  const int e = __builtin_amdgcn_readfirstlane((int)blockIdx.x / col_groups);
+  const int cg = (int)blockIdx.x - e * col_groups;
   if (e >= p.E) return;  // uniform per workgroup
   const int seg0 = p.seg_off[e];
   const int seg_rows = p.seg_off[e + 1] - seg0;
-  const int64_t c = (int64_t)ct * 16 + (lane & 15);
-  const int64_t col = c < p.N ? c : p.N - 1;
+  const int64_t n0 = (int64_t)cg * CT * 16;
+  // the lane's column of tile 0 (the launcher guarantees N % (16 * CT) == 0,
+  // so every tile of every group lies inside the matrix)
+  const int64_t col = n0 + (lane & 15);
   const uint8_t* W1 = table_entry(p.wp, e) + col * p.K;
   const float* S1 = table_entry(p.sp, e) + col * p.nt;
   const uint8_t* W2 = SWIGLU ? table_entry(p.wp2, e) + col * p.K : W1;
@@ -1110,36 +1121,39 @@ decode_gemm_kernel(GemmArgs p, int col_tiles, int ks_count) {
     const int row0 = seg0 + rb;
     const int nrows = min(64, seg_rows - rb);
     const int nrt = (nrows + 15) >> 4;
-    f32x4_t acc1[4], acc2[4];
+    f32x4_t acc1[CT][4], acc2[CT][4];
     // prefetch depth shrinks as the A fragments per block grow (the launcher
     // guarantees nblk % DB == 0 with DB a power of two)
     switch (nrt) {
-      case 1: decode_wave<SWIGLU, CANON, 1, DB>(p, W1, S1, W2, S2, row0, nrows, kb0, nblk, lane, acc1, acc2); break;
-      case 2: decode_wave<SWIGLU, CANON, 2, (DB >= 2 ? DB / 2 : 1)>(p, W1, S1, W2, S2, row0, nrows, kb0, nblk, lane, acc1, acc2); break;
-      case 3: decode_wave<SWIGLU, CANON, 3, (DB >= 4 ? DB / 4 : 1)>(p, W1, S1, W2, S2, row0, nrows, kb0, nblk, lane, acc1, acc2); break;
-      default: decode_wave<SWIGLU, CANON, 4, (DB >= 4 ? DB / 4 : 1)>(p, W1, S1, W2, S2, row0, nrows, kb0, nblk, lane, acc1, acc2); break;
+      case 1: decode_wave<SWIGLU, CANON, 1, DB, CT>(p, W1, S1, W2, S2, row0, nrows, kb0, nblk, lane, acc1, acc2); break;
+      case 2: decode_wave<SWIGLU, CANON, 2, (DB >= 2 ? DB / 2 : 1), CT>(p, W1, S1, W2, S2, row0, nrows, kb0, nblk, lane, acc1, acc2); break;
+      case 3: decode_wave<SWIGLU, CANON, 3, (DB >= 4 ? DB / 4 : 1), CT>(p, W1, S1, W2, S2, row0, nrows, kb0, nblk, lane, acc1, acc2); break;
+      default: decode_wave<SWIGLU, CANON, 4, (DB >= 4 ? DB / 4 : 1), CT>(p, W1, S1, W2, S2, row0, nrows, kb0, nblk, lane, acc1, acc2); break;
     }
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-      if (rt < nrt)
+    for (int t = 0; t < CT; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          red[ks][0][rt][r][lane] = acc1[rt][r];
-          if constexpr (SWIGLU) red[ks][NH - 1][rt][r][lane] = acc2[rt][r];
-        }
+      for (int rt = 0; rt < 4; ++rt)
+        if (rt < nrt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            red[ks][0][t][rt][r][lane] = acc1[t][rt][r];
+            if constexpr (SWIGLU) red[ks][NH - 1][t][rt][r][lane] = acc2[t][rt][r];
+          }
     __syncthreads();
     // The workgroup's threads share the sums (in K-split order,
     // deterministic) and the epilogue: one output element each.
-    for (int q = threadIdx.x; q < nrt * 256; q += nthr) {
-      const int rt = q >> 8, r = (q >> 6) & 3, ln = q & 63;
+    for (int q = threadIdx.x; q < CT * nrt * 256; q += nthr) {
+      const int t = q / (nrt * 256), qq = q - t * nrt * 256;
+      const int rt = qq >> 8, r = (qq >> 6) & 3, ln = qq & 63;
       const int lr = rt * 16 + (ln >> 4) * 4 + r;
-      const int64_t oc = (int64_t)ct * 16 + (ln & 15);
-      float g = red[0][0][rt][r][ln];
-      for (int k2 = 1; k2 < ks_count; ++k2) g += red[k2][0][rt][r][ln];
+      const int64_t oc = n0 + t * 16 + (ln & 15);
+      float g = red[0][0][t][rt][r][ln];
+      for (int k2 = 1; k2 < ks_count; ++k2) g += red[k2][0][t][rt][r][ln];
       float v = g;
       if constexpr (SWIGLU) {
-        float u = red[0][NH - 1][rt][r][ln];
-        for (int k2 = 1; k2 < ks_count; ++k2) u += red[k2][NH - 1][rt][r][ln];
+        float u = red[0][NH - 1][t][rt][r][ln];
+        for (int k2 = 1; k2 < ks_count; ++k2) u += red[k2][NH - 1][t][rt][r][ln];
         v = silu_f(bf2f(f2bf(g))) * bf2f(f2bf(u));
       }
       if (lr < nrows && oc < p.N) ((uint16_t*)p.y)[(int64_t)(row0 + lr) * p.ldy + oc] = (uint16_t)f2bf(v);
@@ -1153,10 +1167,12 @@ decode_gemm_kernel(GemmArgs p, int col_tiles, int ks_count) {
 template <bool SWIGLU, bool CANON, int DB>
 int launch_decode_db(const GemmArgs& a, int ks_count, hipStream_t stream) {
   if (SWIGLU != (a.row_idx != nullptr)) return fail(SMAUL_ERR_INVALID, "decode gemm: row gather mismatch");
-  const int col_tiles = (int)((a.N + 15) / 16);
-  const int64_t blocks = (int64_t)a.E * col_tiles;
+  constexpr int CT = DecodeCT<SWIGLU>;
+  if (a.N % (16 * CT) != 0) return fail(SMAUL_ERR_INVALID, "decode gemm: N must be a multiple of %d", 16 * CT);
+  const int col_groups = (int)(a.N / (16 * CT));
+  const int64_t blocks = (int64_t)a.E * col_groups;
   hipLaunchKernelGGL((decode_gemm_kernel<SWIGLU, CANON, DB>), dim3((unsigned)blocks), dim3(ks_count * 64), 0,
-                     stream, a, col_tiles, ks_count);
+                     stream, a, col_groups, ks_count);
   return check_launch("decode_gemm_kernel");
 }
 
