@@ -2202,7 +2202,10 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
   ws += align256(R * h * el);
   void* yperm = ws;
 
-  const int64_t bm = pick_block_m(T, d, h, E, k, tile, act_dtype);
+  int64_t bm = pick_block_m(T, d, h, E, k, tile, act_dtype);
+  // the LDS-DMA GEMMs need 16-byte aligned code buffers; without that promise
+  // the register-staged kernels (128-row tiles) run instead
+  if (bm == DMA_BM && (!(flags & SMAUL_FLAG_ALIGNED_CODES) || !aligned16(x))) bm = CfgBig::BM;
   RouteOut o{};
   o.prob = prob;
   o.topi = topi;

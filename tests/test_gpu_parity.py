@@ -293,6 +293,65 @@ def test_staged_call_equals_fused_call():
     assert torch.equal(counts, disp["counts"])
 
 
+def abi_moe(x, gw, gb, experts, k, tile, flags, code_tensors=None):
+    """smaul_moe_forward through the C-ABI on the caller's own code buffers."""
+    from smaulnative_amd import _lib
+    lib = _lib.load()
+    T, d = x.shape
+    E = len(experts)
+    ex = code_tensors or to_dev_experts(experts)
+    h = ex[0][0].shape[0]
+    table = torch.tensor([[int(ex[e][j].data_ptr()) for e in range(E)] for j in range(6)],
+                         dtype=torch.int64, device=DEV)
+    xd, gwd = x.to(DEV).contiguous(), gw.to(DEV).float().contiguous()
+    gbd = None if gb is None else gb.to(DEV).float().contiguous()
+    out = torch.empty_like(xd)
+    prob = torch.empty(T, E, device=DEV)
+    topi = torch.empty(T, k, dtype=torch.int64, device=DEV)
+    topw = torch.empty(T, k, device=DEV)
+    counts = torch.empty(E, dtype=torch.int32, device=DEV)
+    act = 1 if x.dtype == torch.bfloat16 else 0
+    ws_bytes = lib.smaul_moe_workspace_size(T, d, h, E, k, act)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    tp, row = table.data_ptr(), E * 8
+    rc = lib.smaul_moe_forward(xd.data_ptr(), act, gwd.data_ptr(), None if gbd is None else gbd.data_ptr(),
+                               tp, tp + row, tp + 2 * row, tp + 3 * row, tp + 4 * row, tp + 5 * row,
+                               out.data_ptr(), prob.data_ptr(), topi.data_ptr(), topw.data_ptr(),
+                               counts.data_ptr(), ws.data_ptr(), ws_bytes, T, d, h, E, k, tile, flags,
+                               torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "moe_forward")
+    torch.cuda.synchronize()
+    return out.cpu(), topi.cpu(), counts.cpu()
+
+
+@pytest.mark.parametrize("T,flags,block_m", [(1024, 0, 256), (1024, 2, 256), (64, 0, 16)])
+def test_moe_raw_codes_any_flags(T, flags, block_m):
+    """Raw stored codes (0x7F/0xFF included, no canonical copy).  At 256-row
+    tiles without SMAUL_FLAG_ALIGNED_CODES the register-staged kernels run;
+    with it the LDS-DMA kernels decode 0x7F/0xFF themselves; T = 64 runs the
+    decode kernels on the raw codes."""
+    from smaulnative_amd import _lib
+    print(f"case raw codes T={T} flags={flags}", flush=True)
+    d, h, E, k = 1024, 2560, 8, 2
+    x, gw, gb, experts = make_moe(4242 + T, T, d, h, E, k)
+    assert _lib.load().smaul_moe_block_m(T, d, h, E, k, 64, 1) == block_m
+    gen = torch.Generator().manual_seed(5)
+    for ex in experts:   # plant 0x7F (= 448, like 0x7E) where the quantizer chose 0x7E
+        for w in (ex.gate_w, ex.up_w, ex.down_w):
+            m = (w == 0x7E) & (torch.rand(w.shape, generator=gen) < 0.5)
+            w[m] = 0x7F
+    n7f = sum(int((w == 0x7F).sum()) for ex in experts for w in (ex.gate_w, ex.up_w, ex.down_w))
+    nff = sum(int((w == 0xFF).sum()) for ex in experts for w in (ex.gate_w, ex.up_w, ex.down_w))
+    assert n7f > 0 and nff > 0
+    ref = oracle.moe_forward(x, gw, gb, experts, k, 64)
+    out, topi, counts = abi_moe(x, gw, gb, experts, k, 64, flags)
+    assert torch.equal(topi, ref.topi.reshape(-1, k))
+    assert counts.tolist() == ref.counts
+    err = rel_l2(out.float(), ref.out.float())
+    print(f"rel_l2={err:.3e} (0x7F codes {n7f}, 0xFF codes {nff})")
+    assert err < 2e-3
+
+
 def test_moe_deterministic_and_empty():
     x, gw, gb, experts = make_moe(77, 700, 256, 640, 8, 2)
     a = gpu_moe(x, gw, gb, experts, 2)
