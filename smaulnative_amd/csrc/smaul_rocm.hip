@@ -17,6 +17,8 @@
 // include/smaul_rocm.h.  Nothing here allocates device memory or synchronises.
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
+
+#include <algorithm>
 #include <stdlib.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -1176,31 +1178,9 @@ int launch_decode_db(const GemmArgs& a, int ks_count, hipStream_t stream) {
   return check_launch("decode_gemm_kernel");
 }
 
-template <bool SWIGLU, bool CANON>
-int launch_decode(const GemmArgs& a, hipStream_t stream) {
-  const int64_t nkb = a.K / 64;
-  for (int db = 4; db >= 2; db /= 2)
-    for (int ks = DecodeKS<SWIGLU>::MAX; ks >= 1; --ks) {
-      if (nkb % ks != 0 || (nkb / ks) % db != 0) continue;
-      if (db == 4) return launch_decode_db<SWIGLU, CANON, 4>(a, ks, stream);
-      return launch_decode_db<SWIGLU, CANON, 2>(a, ks, stream);
-    }
-  return fail(SMAUL_ERR_INVALID, "decode gemm: K/64 must be even");
-}
-
 // ---------------------------------------------------------------------------
-// router: logits, softmax, top-k (torch CPU order), renormalisation
+// routing results shared by the router and the dispatch kernels
 // ---------------------------------------------------------------------------
-// A workgroup of 4 waves owns a block of TB*4 tokens (32 when E <= 4, 16
-// when E <= 16, else 4), so a CU holds several blocks whose phases overlap and
-// a 64-token decode step spreads over several CUs.  The router weight is staged in LDS (in column
-// chunks of at most 32 KB); inside a wave the 64 lanes split the model
-// dimension into 8-wide groups (coalesced 16-byte loads of x), each lane keeps
-// TB tokens x EMAX experts of partial dot products, and a butterfly over the
-// lanes completes them.  One thread per token then runs softmax, the top-k
-// selection and the renormalisation, and the block's per-expert dispatch
-// counts are written for the dispatch scan.  With a single block (T <= TB*4)
-// the same workgroup also performs the dispatch.
 constexpr int ROUTE_THREADS = 256;
 constexpr int ROUTE_WAVES = ROUTE_THREADS / 64;
 constexpr int MAX_E = 64;
@@ -1284,6 +1264,424 @@ __device__ __forceinline__ void dispatch_one_wave(const int* ti, const float* tw
   }
 }
 
+// ---------------------------------------------------------------------------
+// decode, streaming form (decode_stream_kernel)
+// ---------------------------------------------------------------------------
+// The grid is one workgroup per CU.  The work is a list of units, one per
+// (segment, 16-column tile), where a segment is up to DS_ROWS rows of one
+// expert; workgroup g walks the contiguous unit range [g*U/G, (g+1)*U/G).
+// Its waves split K: wave ks owns KBW consecutive 64-wide blocks and keeps
+// that slice of the segment's activation rows in registers for as long as the
+// segment lasts, so per unit it streams only weight codes and scales, and it
+// keeps DS_D units of them in flight (a register ring that runs across unit
+// boundaries; the refill of a block is issued as soon as the block is
+// decoded).  Per unit the waves' fp32 partials meet in LDS (two buffers, one
+// barrier per unit) and are summed in K-split order: deterministic.
+constexpr int DS_ROWS = 32;
+constexpr int DS_WMAX = 8;
+constexpr int DS_D = 2;
+
+// Segments of the executed experts, one lane per expert (E <= 64).  The lane
+// also holds its expert's weight and scale pointers, loaded beside the
+// segment bounds, so no pointer-table read waits in the unit loop.
+struct DsSegs {
+  int incl;    // inclusive prefix of segment counts up to this lane's expert
+  int nseg;    // segments of this lane's expert
+  int lo;      // its first row
+  int rows;    // its rows
+  int total;   // segments over all experts (uniform)
+  uint64_t w1, s1, w2, s2;  // its codes and scales (w2/s2: the up projection)
+};
+
+// pointer held by lane e (uniform e) -> scalar
+template <class T>
+__device__ __forceinline__ T* ds_ptr(uint64_t v, int e) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, e);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), e);
+  return (T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// lane e < E: its expert's weight and scale pointers
+__device__ __forceinline__ void ds_pointers(const GemmArgs& p, int lane, DsSegs& s) {
+  s.w1 = s.s1 = s.w2 = s.s2 = 0;
+  if (lane < p.E) {
+    s.w1 = (uint64_t)(uintptr_t)p.wp[lane];
+    s.s1 = (uint64_t)(uintptr_t)p.sp[lane];
+    if (p.wp2) {
+      s.w2 = (uint64_t)(uintptr_t)p.wp2[lane];
+      s.s2 = (uint64_t)(uintptr_t)p.sp2[lane];
+    }
+  }
+}
+
+// lane e < E: its expert's rows [lo, hi); segment counts and their prefix
+__device__ __forceinline__ void ds_finish(int lo, int hi, int lane, DsSegs& s) {
+  s.lo = lo;
+  s.rows = hi - lo;
+  s.nseg = (s.rows + DS_ROWS - 1) / DS_ROWS;
+  int inc = s.nseg;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += u;
+  }
+  s.incl = inc;
+  s.total = __builtin_amdgcn_readlane(inc, 63);
+}
+
+__device__ __forceinline__ DsSegs ds_segments(const GemmArgs& p, int lane) {
+  DsSegs s;
+  int lo = 0, hi = 0;
+  if (lane < p.E) {
+    lo = p.seg_off[lane];
+    hi = p.seg_off[lane + 1];
+  }
+  ds_pointers(p, lane, s);
+  ds_finish(lo, hi, lane, s);
+  return s;
+}
+
+// segment j (uniform, < total) -> expert, first row, rows (all uniform)
+__device__ __forceinline__ void ds_locate(const DsSegs& s, int j, int& e, int& row0, int& nrows) {
+  e = (int)__popcll(__ballot(s.incl <= j));
+  const int pass = j - __builtin_amdgcn_readlane(s.incl - s.nseg, e);
+  row0 = __builtin_amdgcn_readlane(s.lo, e) + pass * DS_ROWS;
+  nrows = min(DS_ROWS, __builtin_amdgcn_readlane(s.rows, e) - pass * DS_ROWS);
+}
+
+// ridx: logical row -> activation row (SwiGLU only; down reads its rows in place)
+template <bool SWIGLU, bool CANON, int KBW, int NRT>
+__device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, const int32_t* ridx, int u0,
+                                        int u1, int ctn, float* red, int nw) {
+  constexpr int NH = SWIGLU ? 2 : 1;
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kq = (lane >> 4) * 16;
+  const int64_t kb0 = (int64_t)ks * KBW;
+  const f32x4_t z4 = {0.f, 0.f, 0.f, 0.f};
+  const int last = u1 - 1;
+
+  // the wave's codes and scales of unit u: block b of stream h at
+  // wsrc[h] + b*64 and ssrc[h] + b
+  auto unit_src = [&](int u, const uint8_t* (&wsrc)[NH], const float* (&ssrc)[NH]) {
+    const int j = u / ctn;
+    const int ct = u - j * ctn;
+    int e, r0, nr;
+    ds_locate(sg, j, e, r0, nr);
+    const int64_t col = (int64_t)ct * 16 + (lane & 15);
+    wsrc[0] = ds_ptr<const uint8_t>(sg.w1, e) + col * p.K + kb0 * 64 + kq;
+    ssrc[0] = ds_ptr<const float>(sg.s1, e) + col * p.nt + kb0;
+    if constexpr (SWIGLU) {
+      wsrc[NH - 1] = ds_ptr<const uint8_t>(sg.w2, e) + col * p.K + kb0 * 64 + kq;
+      ssrc[NH - 1] = ds_ptr<const float>(sg.s2, e) + col * p.nt + kb0;
+    }
+  };
+  uint4 bw[DS_D][KBW][NH];
+  float sw[DS_D][KBW][NH];
+  auto fetch = [&](int slot, int u) {
+    const uint8_t* ws[NH];
+    const float* ss[NH];
+    unit_src(u, ws, ss);
+#pragma unroll
+    for (int b = 0; b < KBW; ++b)
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        bw[slot][b][h] = ldg16(ws[h] + b * 64);
+        sw[slot][b][h] = ldgf(ss[h] + b);
+      }
+  };
+  // the segment's activation rows, this wave's K slice
+  uint4 a0[NRT][KBW], a1[NRT][KBW];
+  auto load_a = [&](int j) {
+    int e, r0, nr;
+    ds_locate(sg, j, e, r0, nr);
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+      const int64_t lr = r0 + min(rt * 16 + (lane & 15), nr - 1);
+      const int64_t xr = SWIGLU ? (int64_t)ridx[lr] : lr;
+      const uint16_t* ar = (const uint16_t*)p.x + xr * p.ldx + kb0 * 64 + kq;
+#pragma unroll
+      for (int b = 0; b < KBW; ++b) {
+        a0[rt][b] = ldg16(ar + b * 64);
+        a1[rt][b] = ldg16(ar + b * 64 + 8);
+      }
+    }
+    // Wait for the rows here: on the path that reloads them they are the
+    // newest loads, and a wait placed after the branch would have to assume
+    // that path, draining the whole ring on every unit.
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int b = 0; b < KBW; ++b)
+        asm volatile("" ::"v"(__builtin_bit_cast(u32x4_t, a0[rt][b])), "v"(__builtin_bit_cast(u32x4_t, a1[rt][b])));
+  };
+
+  // the first unit's codes go out first, then its rows, then the rest of the ring
+  fetch(0, u0);
+  int cur_j = u0 / ctn;
+  load_a(cur_j);
+#pragma unroll
+  for (int i = 1; i < DS_D; ++i) fetch(i, min(u0 + i, last));
+
+  const int nthr = nw * 64;
+  const int per_buf = nw * NH * NRT * 256;
+  int buf = 0;
+  // whole rounds of DS_D units; units past the range recompute the last one
+  // and store nothing, so every wave reaches every barrier
+  for (int it = u0; it <= last; it += DS_D) {
+#pragma unroll
+    for (int i = 0; i < DS_D; ++i) {
+      const bool live = it + i <= last;
+      const int u = min(it + i, last);
+      const int j = u / ctn;
+      if (j != cur_j) {  // uniform: a new segment's rows
+        load_a(j);
+        cur_j = j;
+      }
+      const uint8_t* nws[NH];
+      const float* nss[NH];
+      unit_src(min(it + i + DS_D, last), nws, nss);
+      f32x4_t acc[NH][NRT];
+#pragma unroll
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) acc[h][rt] = z4;
+#pragma unroll
+      for (int b = 0; b < KBW; ++b) {
+        bf16x8_t g0[NH], g1[NH];
+        float sc[NH];
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+          uint32_t d[8];
+          decode4<CANON>(bw[i][b][h].x, d[0], d[1]);
+          decode4<CANON>(bw[i][b][h].y, d[2], d[3]);
+          decode4<CANON>(bw[i][b][h].z, d[4], d[5]);
+          decode4<CANON>(bw[i][b][h].w, d[6], d[7]);
+          g0[h] = __builtin_bit_cast(bf16x8_t, make_uint4(d[0], d[1], d[2], d[3]));
+          g1[h] = __builtin_bit_cast(bf16x8_t, make_uint4(d[4], d[5], d[6], d[7]));
+          sc[h] = sw[i][b][h];
+          bw[i][b][h] = ldg16(nws[h] + b * 64);
+          sw[i][b][h] = ldgf(nss[h] + b);
+        }
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+          for (int h = 0; h < NH; ++h) {
+            f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a0[rt][b]), g0[h],
+                                                                z4, 0, 0, 0);
+            q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a1[rt][b]), g1[h], q, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[h][rt][r] = __builtin_fmaf(sc[h], q[r], acc[h][rt][r]);
+          }
+      }
+      // partials: red[buf][ks][h][rt][r][lane]
+      float* rb = red + buf * per_buf;
+#pragma unroll
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) rb[((ks * NH + h) * NRT + rt) * 256 + r * 64 + lane] = acc[h][rt][r];
+      __syncthreads();
+      if (live) {
+        int e, r0, nr;
+        ds_locate(sg, j, e, r0, nr);
+        const int ct = u - j * ctn;
+        for (int q = threadIdx.x; q < NRT * 256; q += nthr) {
+          const int rt = q >> 8, r = (q >> 6) & 3, ln = q & 63;
+          const int lr = rt * 16 + (ln >> 4) * 4 + r;
+          // all partials are read before the first add (independent LDS
+          // reads in flight together), then summed in K-split order
+          float pg[DS_WMAX], pu[DS_WMAX];
+#pragma unroll
+          for (int k2 = 0; k2 < DS_WMAX; ++k2)
+            if (k2 < nw) {
+              pg[k2] = rb[(k2 * NH) * NRT * 256 + q];
+              if constexpr (SWIGLU) pu[k2] = rb[(k2 * NH + 1) * NRT * 256 + q];
+            }
+          float g = pg[0];
+#pragma unroll
+          for (int k2 = 1; k2 < DS_WMAX; ++k2)
+            if (k2 < nw) g += pg[k2];
+          float v = g;
+          if constexpr (SWIGLU) {
+            float uu = pu[0];
+#pragma unroll
+            for (int k2 = 1; k2 < DS_WMAX; ++k2)
+              if (k2 < nw) uu += pu[k2];
+            v = silu_f(bf2f(f2bf(g))) * bf2f(f2bf(uu));
+          }
+          if (lr < nr)
+            ((uint16_t*)p.y)[(int64_t)(r0 + lr) * p.ldy + (int64_t)ct * 16 + (ln & 15)] = (uint16_t)f2bf(v);
+        }
+      }
+      buf ^= 1;
+    }
+  }
+}
+
+// Inputs of the dispatch that the gate/up kernel performs itself (FUSED):
+// the router's top-k ids and weights of T <= 64 tokens, and where workgroup 0
+// writes the dispatch for the later stages.
+struct DsDispatch {
+  const int64_t* topi;
+  const float* topw;
+  RouteOut o;
+  int T, k;
+};
+
+// FUSED (gate/up only): every workgroup ranks the T <= 64 tokens per expert
+// itself, from topi/topw, into LDS (one wave, ballot ranks in token order,
+// the same rule as dispatch_one_wave) instead of reading a dispatch written by
+// an earlier kernel; workgroup 0 also writes that dispatch (counts, seg_off,
+// tile_off, perm_row, perm_w, inv) for the down projection and the combine.
+template <bool SWIGLU, bool CANON, int KBW, bool FUSED>
+__global__ void __launch_bounds__(DS_WMAX * 64)
+decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
+  constexpr int NH = SWIGLU ? 2 : 1;
+  static_assert(!FUSED || SWIGLU, "the fused dispatch feeds the gate/up projection");
+  __shared__ float red[2 * DS_WMAX * NH * 2 * 256];
+  __shared__ int32_t s_perm[FUSED ? 64 * 8 : 1];
+  __shared__ int32_t s_off[FUSED ? MAX_E + 1 : 1];
+  const int lane = threadIdx.x & 63;
+  DsSegs sg;
+  if constexpr (FUSED) {
+    ds_pointers(p, lane, sg);
+    if (threadIdx.x < 64) {
+      const bool valid = lane < dd.T;
+      int ti[8];
+      float tw[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < dd.k) {
+          const int64_t v = valid ? dd.topi[lane * dd.k + j] : -1;
+          ti[j] = (v >= 0 && v < p.E) ? (int)v : -1;
+          tw[j] = valid ? dd.topw[lane * dd.k + j] : 0.0f;
+        }
+      const uint64_t sel = valid ? selection_of(ti, tw, p.E, dd.k) : 0ull;
+      const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+      int off = 0;
+      for (int e = 0; e < p.E; ++e) {
+        const uint64_t b = __ballot((sel >> e) & 1ull);
+        if (lane == 0) s_off[e] = off;
+        if ((sel >> e) & 1ull) s_perm[off + __popcll(b & lt)] = lane;
+        off += __popcll(b);
+      }
+      if (lane == 0) s_off[p.E] = off;
+      if (blockIdx.x == 0) dispatch_one_wave(ti, tw, valid, lane, dd.o, p.E, dd.k);
+    }
+    __syncthreads();
+    ds_finish(lane < p.E ? s_off[lane] : 0, lane < p.E ? s_off[lane + 1] : 0, lane, sg);
+  } else {
+    sg = ds_segments(p, lane);
+  }
+  const int32_t* ridx = FUSED ? (const int32_t*)s_perm : p.row_idx;
+  const int ctn = (int)(p.N >> 4);
+  const int64_t U = (int64_t)sg.total * ctn;
+  const int u0 = (int)((int64_t)blockIdx.x * U / gridDim.x);
+  const int u1 = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
+  if (u0 >= u1) return;  // uniform per workgroup
+  // two row tiles when any segment has more than 16 rows
+  if (__ballot(sg.rows > 16) != 0) ds_body<SWIGLU, CANON, KBW, 2>(p, sg, ridx, u0, u1, ctn, red, nw);
+  else ds_body<SWIGLU, CANON, KBW, 1>(p, sg, ridx, u0, u1, ctn, red, nw);
+}
+
+// K blocks per wave of the streaming decode kernel for K/64 = nkb blocks
+// (at most DS_WMAX waves), or 0 when no instance fits
+int ds_kbw(int64_t nkb, bool swiglu) {
+  const int cand[3] = {2, 4, 5};
+  for (int kb : cand) {
+    if (swiglu && kb == 5) continue;  // gate/up at 5 blocks per wave spills
+    if (nkb % kb == 0 && nkb / kb <= DS_WMAX) return kb;
+  }
+  return 0;
+}
+
+// SMAUL_DECODE=split runs decode_gemm_kernel for every decode GEMM (A/B timing)
+bool decode_stream_enabled() {
+  static const bool on = [] {
+    const char* v = getenv("SMAUL_DECODE");
+    return !(v && strcmp(v, "split") == 0);
+  }();
+  return on;
+}
+
+// compute units of the current device (cached per device)
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Returns 1 when the shape has no streaming instance (the caller then runs
+// decode_gemm_kernel), else the launch status.  dd != nullptr: the gate/up
+// kernel performs the dispatch itself (FUSED).
+template <bool SWIGLU, bool CANON>
+int launch_decode_stream(const GemmArgs& a, const DsDispatch* dd, hipStream_t stream) {
+  const int64_t nkb = a.K / 64;
+  if (a.N % 16 != 0 || a.E > 64) return 1;
+  const int kbw = ds_kbw(nkb, SWIGLU);
+  if (kbw == 0) return 1;
+  const int nw = (int)(nkb / kbw);
+  const int64_t ctn = a.N / 16;
+  // units: at most E * ctn * (64 / DS_ROWS) in the decode regime; a grid of
+  // one workgroup per CU, never more workgroups than that
+  const int64_t g = std::min<int64_t>(cu_count(), std::max<int64_t>(1, a.E * ctn * (64 / DS_ROWS)));
+  const DsDispatch none{};
+  const dim3 grid((unsigned)g), block(nw * 64);
+  if constexpr (SWIGLU) {
+    if (dd) {
+      if (kbw == 2) hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true>), grid, block, 0, stream, a, nw, *dd);
+      else hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 4, true>), grid, block, 0, stream, a, nw, *dd);
+      return check_launch("decode_stream_kernel");
+    }
+  }
+  switch (kbw) {
+    case 2: hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 2, false>), grid, block, 0, stream, a, nw, none); break;
+    case 4: hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 4, false>), grid, block, 0, stream, a, nw, none); break;
+    default:
+      if constexpr (!SWIGLU) hipLaunchKernelGGL((decode_stream_kernel<false, CANON, 5, false>), grid, block, 0, stream, a, nw, none);
+      break;
+  }
+  return check_launch("decode_stream_kernel");
+}
+
+template <bool SWIGLU, bool CANON>
+int launch_decode(const GemmArgs& a, hipStream_t stream) {
+  if (SWIGLU != (a.row_idx != nullptr)) return fail(SMAUL_ERR_INVALID, "decode gemm: row gather mismatch");
+  if (decode_stream_enabled()) {
+    const int rc = launch_decode_stream<SWIGLU, CANON>(a, nullptr, stream);
+    if (rc != 1) return rc;
+  }
+  const int64_t nkb = a.K / 64;
+  for (int db = 4; db >= 2; db /= 2)
+    for (int ks = DecodeKS<SWIGLU>::MAX; ks >= 1; --ks) {
+      if (nkb % ks != 0 || (nkb / ks) % db != 0) continue;
+      if (db == 4) return launch_decode_db<SWIGLU, CANON, 4>(a, ks, stream);
+      return launch_decode_db<SWIGLU, CANON, 2>(a, ks, stream);
+    }
+  return fail(SMAUL_ERR_INVALID, "decode gemm: K/64 must be even");
+}
+
+// ---------------------------------------------------------------------------
+// router: logits, softmax, top-k (torch CPU order), renormalisation
+// ---------------------------------------------------------------------------
+// A workgroup of 4 waves owns a block of TB*4 tokens (32 when E <= 4, 16
+// when E <= 16, else 4), so a CU holds several blocks whose phases overlap and
+// a 64-token decode step spreads over several CUs.  The router weight is staged in LDS (in column
+// chunks of at most 32 KB); inside a wave the 64 lanes split the model
+// dimension into 8-wide groups (coalesced 16-byte loads of x), each lane keeps
+// TB tokens x EMAX experts of partial dot products, and a butterfly over the
+// lanes completes them.  One thread per token then runs softmax, the top-k
+// selection and the renormalisation, and the block's per-expert dispatch
+// counts are written for the dispatch scan.  With a single block (T <= TB*4)
+// the same workgroup also performs the dispatch.
 template <bool XBF16, int TB, int EMAX, bool EXACT>
 __global__ void __launch_bounds__(ROUTE_THREADS)
 router_kernel(const void* __restrict__ x, const float* __restrict__ gw, const float* __restrict__ gb,
@@ -2206,30 +2604,53 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
   // the LDS-DMA GEMMs need 16-byte aligned code buffers; without that promise
   // the register-staged kernels (128-row tiles) run instead
   if (bm == DMA_BM && (!(flags & SMAUL_FLAG_ALIGNED_CODES) || !aligned16(x))) bm = CfgBig::BM;
+  // decode regime: the gate/up kernel dispatches for itself
+  const bool fused = bm == DECODE_BM && decode_stream_enabled() && aligned16(x) && h % 16 == 0 &&
+                     ds_kbw(d / 64, true) != 0;
   RouteOut o{};
   o.prob = prob;
   o.topi = topi;
   o.topw = topw;
   o.blockcnt = blockcnt;
   o.block_m = (int)bm;
-  if (nb == 1) {  // one router block: it dispatches too
-    o.counts = counts;
-    o.seg_off = seg_off;
-    o.tile_off = tile_off;
-    o.perm_row = perm_row;
-    o.perm_w = perm_w;
-    o.inv = inv;
-  }
+  RouteOut od = o;
+  od.counts = counts;
+  od.seg_off = seg_off;
+  od.tile_off = tile_off;
+  od.perm_row = perm_row;
+  od.perm_w = perm_w;
+  od.inv = inv;
+  if (nb == 1 && !fused) o = od;  // one router block: it dispatches too
   rc = launch_router(x, act_dtype, gate_w, gate_b, o, T, d, E, k, stream);
   if (rc) return rc;
+  const int64_t max_tiles = (R + bm - 1) / bm + E;
+  if (fused) {
+    GemmArgs a{};
+    a.x = x;
+    a.ldx = d;
+    a.wp = gate_w8;
+    a.sp = gate_s;
+    a.wp2 = up_w8;
+    a.sp2 = up_s;
+    a.y = hdn;
+    a.ldy = h;
+    a.K = d;
+    a.N = h;
+    a.nt = d / 64;
+    a.tile = 64;
+    a.seg_off = seg_off;
+    a.tile_off = tile_off;
+    a.E = (int)E;
+    const DsDispatch dd{topi, topw, od, (int)T, (int)k};
+    rc = (flags & SMAUL_FLAG_CANONICAL_CODES) ? launch_decode_stream<true, true>(a, &dd, stream)
+                                              : launch_decode_stream<true, false>(a, &dd, stream);
+    if (rc) return rc;
+    rc = smaul_moe_down(hdn, act_dtype, down_w8, down_s, yperm, seg_off, tile_off, max_tiles, E, d, h, tile,
+                        bm, flags, stream);
+    if (rc) return rc;
+    return smaul_moe_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, stream);
+  }
   if (nb > 1 && T <= 64) {  // one wave dispatches straight from topi/topw
-    RouteOut od = o;
-    od.counts = counts;
-    od.seg_off = seg_off;
-    od.tile_off = tile_off;
-    od.perm_row = perm_row;
-    od.perm_w = perm_w;
-    od.inv = inv;
     hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(64), 0, stream, topi, topw, od, T, (int)E, (int)k);
     rc = check_launch("dispatch_small_kernel");
     if (rc) return rc;
@@ -2238,7 +2659,6 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
                              T, E, k, bm, route_tpb(E), stream);
     if (rc) return rc;
   }
-  const int64_t max_tiles = (R + bm - 1) / bm + E;
   rc = smaul_moe_gate_up(x, act_dtype, perm_row, gate_w8, gate_s, up_w8, up_s, hdn, seg_off, tile_off,
                          max_tiles, E, d, h, tile, bm, flags, stream);
   if (rc) return rc;
