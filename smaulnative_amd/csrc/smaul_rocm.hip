@@ -1264,6 +1264,426 @@ __device__ __forceinline__ void dispatch_one_wave(const int* ti, const float* tw
   }
 }
 
+// ---- router building blocks (shared by router_kernel and the decode gate/up
+// kernel that routes for itself; the same code gives the same bits) ---------
+
+// Router columns per LDS chunk and the lane's 8-column groups per chunk.
+template <int EMAX>
+struct RouteShape {
+  static constexpr int DC = ROUTE_WFLOATS / EMAX;   // columns per chunk
+  static constexpr int XG = (DC / 8 + 63) / 64;     // 8-column groups per lane
+};
+
+// Activations of TB tokens (rows tw0.., rows past T clamped to T-1: computed,
+// never written) for the lane's column groups of chunk [c0, c0 + cw).
+template <bool XBF16, int TB, int EMAX>
+__device__ __forceinline__ void route_load_x(const void* x, int64_t T, int64_t tw0, int c0, int cw, int d,
+                                             int lane, uint4 (&xr)[RouteShape<EMAX>::XG][TB][XBF16 ? 1 : 2]) {
+  constexpr int XG = RouteShape<EMAX>::XG;
+  constexpr int XW = XBF16 ? 1 : 2;
+#pragma unroll
+  for (int q = 0; q < XG; ++q) {
+    const int g = lane + 64 * q;
+    if (g < (cw >> 3)) {
+#pragma unroll
+      for (int a = 0; a < TB; ++a) {
+        const int64_t t = tw0 + a < T ? tw0 + a : T - 1;
+        if constexpr (XBF16) {
+          xr[q][a][0] = ldg16((const uint16_t*)x + t * d + c0 + g * 8);
+        } else {
+          xr[q][a][0] = ldg16((const float*)x + t * d + c0 + g * 8);
+          xr[q][a][XW - 1] = ldg16((const float*)x + t * d + c0 + g * 8 + 4);
+        }
+      }
+    }
+  }
+}
+
+// acc[a * EMAX + e] += the lane's column groups of chunk (width cw) of token a
+// times router row e, staged in sW[e * cw + c]; per lane the groups are summed
+// in ascending order, 8 columns at a time in column order (fmaf).
+template <bool XBF16, int TB, int EMAX>
+__device__ __forceinline__ void route_fma(const uint4 (&xr)[RouteShape<EMAX>::XG][TB][XBF16 ? 1 : 2],
+                                          const float* sW, int cw, int lane, float (&acc)[TB * EMAX]) {
+  constexpr int XG = RouteShape<EMAX>::XG;
+  constexpr int XW = XBF16 ? 1 : 2;
+#pragma unroll
+  for (int q = 0; q < XG; ++q) {
+    const int g = lane + 64 * q;
+    if (g < (cw >> 3)) {
+      float xv[TB][8];
+#pragma unroll
+      for (int a = 0; a < TB; ++a) {
+        if constexpr (XBF16) {
+          const uint4 v = xr[q][a][0];
+          xv[a][0] = bf2f(v.x & 0xffff); xv[a][1] = bf2f(v.x >> 16);
+          xv[a][2] = bf2f(v.y & 0xffff); xv[a][3] = bf2f(v.y >> 16);
+          xv[a][4] = bf2f(v.z & 0xffff); xv[a][5] = bf2f(v.z >> 16);
+          xv[a][6] = bf2f(v.w & 0xffff); xv[a][7] = bf2f(v.w >> 16);
+        } else {
+          const uint4 v0 = xr[q][a][0], v1 = xr[q][a][XW - 1];
+          xv[a][0] = __uint_as_float(v0.x); xv[a][1] = __uint_as_float(v0.y);
+          xv[a][2] = __uint_as_float(v0.z); xv[a][3] = __uint_as_float(v0.w);
+          xv[a][4] = __uint_as_float(v1.x); xv[a][5] = __uint_as_float(v1.y);
+          xv[a][6] = __uint_as_float(v1.z); xv[a][7] = __uint_as_float(v1.w);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e) {
+        const float4 w0 = *(const float4*)&sW[e * cw + g * 8];
+        const float4 w1 = *(const float4*)&sW[e * cw + g * 8 + 4];
+        const float wv8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int a = 0; a < TB; ++a)
+#pragma unroll
+          for (int qq = 0; qq < 8; ++qq)
+            acc[a * EMAX + e] = __builtin_fmaf(xv[a][qq], wv8[qq], acc[a * EMAX + e]);
+      }
+    }
+  }
+}
+
+// Halving butterfly over the 64 lanes: at each step a lane keeps half of its
+// values and adds the partner's copy of them, so the TB*EMAX sums need
+// TB*EMAX-1 exchanges in all (instead of 6 per value) and the exchanges of a
+// step are independent.  Every value is summed over the same xor tree of
+// lanes whatever TB is.  Afterwards acc[0] of lane l is the full sum of value
+// index vidx (returned); with 32 values the even lanes hold them.
+template <int TB, int EMAX>
+__device__ __forceinline__ int route_butterfly(float (&acc)[TB * EMAX], int lane) {
+  constexpr int N = TB * EMAX;
+  static_assert(N == 32 || N == 64, "router reduction expects 32 or 64 partial sums per lane");
+  int vidx = 0;
+#pragma unroll
+  for (int step = 0; step < 6; ++step) {
+    const int m = 32 >> step;
+    const int n = N >> step;
+    const bool up = (lane & m) != 0;
+    const uint32_t upmask = up ? 0xffffffffu : 0u;
+    if (n >= 2) {
+      const int half = n >> 1;
+#pragma unroll
+      for (int i = 0; i < N / 2; ++i) {
+        if (i < half) {
+          // select with a bit mask, not `up ? acc[i] : acc[i + half]`: the
+          // compiler turns that into a dynamically indexed array read (a
+          // compare/select over every element of acc)
+          const uint32_t lo = __float_as_uint(acc[i]), hi = __float_as_uint(acc[i + half]);
+          const uint32_t give = (lo & upmask) | (hi & ~upmask);
+          const uint32_t keep = (hi & upmask) | (lo & ~upmask);
+          acc[i] = __uint_as_float(keep) + __shfl_xor(__uint_as_float(give), m, 64);
+        }
+      }
+      if (up) vidx += half;
+    } else {
+      acc[0] += __shfl_xor(acc[0], m, 64);
+    }
+  }
+  return vidx;
+}
+
+// One token (model.py:558-570): softmax of its logits lg[0..E) (torch's
+// exp(v - max) / sum form), top-k (torch's CPU order; q is scratch for the
+// tie path), the < 1e-6 guarded renormalisation.  Writes prob/topi/topw of
+// token t when `write`; returns the ids and weights in ti/tv.
+template <int EMAX>
+__device__ __forceinline__ void route_select(const float* lg, smaul_topk::Pair* q, int E, int k, int64_t t,
+                                             const RouteOut& o, bool write, int (&ti)[8], float (&tv)[8]) {
+  float v[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) v[e] = e < E ? lg[e] : 0.0f;
+  float mx = v[0];  // NaN propagates, as in torch's max reduction
+#pragma unroll
+  for (int e = 1; e < EMAX; ++e)
+    if (e < E) mx = (v[e] > mx || v[e] != v[e]) ? v[e] : mx;
+  float sum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e)
+    if (e < E) {
+      v[e] = expf(v[e] - mx);
+      sum = sum + v[e];
+    }
+  const float rs = 1.0f / sum;
+  bool ties = false;
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e)
+    if (e < E) {
+      v[e] = v[e] * rs;
+      if (write) o.prob[t * E + e] = v[e];
+      ties |= v[e] != v[e];
+    }
+  // Top-k.  With all-distinct values the selection is unique: the k largest
+  // in descending order, found in registers.  Equal values (or NaN) go
+  // through the exact restatement of torch's selection steps.
+  if constexpr (EMAX <= 16) {
+#pragma unroll
+    for (int a = 0; a < EMAX; ++a)
+#pragma unroll
+      for (int b = a + 1; b < EMAX; ++b)
+        if (b < E) ties |= v[a] == v[b];
+  } else {
+    ties = true;
+  }
+  if (!ties) {
+    uint64_t used = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < k) {
+        int bi = -1;
+        float bv = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e)
+          if (e < E && !((used >> e) & 1ull) && (bi < 0 || v[e] > bv)) {
+            bi = e;
+            bv = v[e];
+          }
+        used |= 1ull << bi;
+        ti[j] = bi;
+        tv[j] = bv;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+      if (e < E) q[e] = smaul_topk::Pair{v[e], e};
+    smaul_topk::topk_small(q, E, k);  // k <= 8
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < k) {
+        ti[j] = q[j].i;
+        tv[j] = q[j].v;
+      }
+  }
+  float denom = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (j < k) denom = denom + tv[j];
+  const bool tiny = denom < 1e-6f;
+  const float dcl = fmaxf(denom, 1e-9f);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (j < k) {
+      tv[j] = tiny ? 1.0f / (float)k : tv[j] / dcl;
+      if (write) {
+        o.topi[t * k + j] = ti[j];
+        o.topw[t * k + j] = tv[j];
+      }
+    }
+}
+
+// ---- router logits on the matrix cores (bf16 activations) ------------------
+// The fp32 router weight is split exactly into three bf16 terms,
+// w = w0 + w1 + w2 (w0 = bf16(w), w1 = bf16(w - w0), w2 = w - w0 - w1, which
+// has at most 8 significant bits), so every product x * wi of a bf16
+// activation is exact in fp32 and v_mfma_f32_16x16x32_bf16 sums them in fp32:
+// the logits carry fp32 accumulation error only, as a scalar fmaf chain does.
+// A pass covers 64 tokens (four MFMA N-tiles of 16) and up to 16 experts (the
+// M rows; rows past E are zero).  K is cut into RK_SLICES fixed slices of
+// KSW 32-wide k-steps; a wave computes whole slices (each with all four token
+// tiles, the three weight terms in separate accumulators) and leaves one
+// partial per (slice, token, expert) in LDS; the logit is the sum of the
+// slices in slice order plus the bias.  Nothing depends on the number of
+// waves, so router_mfma_kernel and the decode gate/up kernel produce the same
+// bits.  The weight terms are made in registers from the lane's own fp32
+// weights (no LDS staging).
+constexpr int RK_SLICES = 8;
+constexpr int RK_TOK = 64;
+constexpr int RK_PART_FLOATS = RK_SLICES * RK_TOK * 16;
+
+// fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// d <= RK_SLICES * 32 * KSW columns; part[(slice * 64 + token) * 16 + expert]
+template <int KSW>
+__device__ __forceinline__ void route_slice(const uint16_t* x, const float* gw, int E, int64_t T, int64_t t0, int d,
+                                            int slice, int lane, float* part) {
+  const int n = lane & 15, g = lane >> 4;
+  uint4 xr[4][KSW];
+  float4 wr[KSW][2];
+  // Every load is issued unconditionally from an in-bounds address (column 0,
+  // expert 0 or token T-1 where the true one is out of range) and masked
+  // afterwards, so all of them are in flight together.
+#pragma unroll
+  for (int i = 0; i < KSW; ++i) {
+    const int c = (slice * KSW + i) * 32 + 8 * g;
+    const int cc = c < d ? c : 0;  // d % 8 == 0: a group is all in or all out
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const int64_t t = t0 + tt * 16 + n < T ? t0 + tt * 16 + n : T - 1;  // computed, never written
+      xr[tt][i] = ldg16(x + t * d + cc);
+    }
+    const int64_t wrow = n < E ? n : 0;
+    wr[i][0] = *(const float4*)(gw + wrow * d + cc);
+    wr[i][1] = *(const float4*)(gw + wrow * d + cc + 4);
+  }
+#pragma unroll
+  for (int i = 0; i < KSW; ++i) {
+    const int c = (slice * KSW + i) * 32 + 8 * g;
+    if (c >= d) {
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) xr[tt][i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (c >= d || n >= E) wr[i][0] = wr[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  f32x4_t acc[4][3];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int term = 0; term < 3; ++term) acc[tt][term] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < KSW; ++i) {
+    const float w8[8] = {wr[i][0].x, wr[i][0].y, wr[i][0].z, wr[i][0].w,
+                         wr[i][1].x, wr[i][1].y, wr[i][1].z, wr[i][1].w};
+    uint32_t q0[8], q1[8], q2[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      q0[j] = bf16_rne(w8[j]);
+      const float r1 = w8[j] - bf2f(q0[j]);
+      q1[j] = bf16_rne(r1);
+      q2[j] = bf16_rne(r1 - bf2f(q1[j]));
+    }
+    bf16x8_t a[3];
+    a[0] = __builtin_bit_cast(bf16x8_t, make_uint4(q0[0] | (q0[1] << 16), q0[2] | (q0[3] << 16),
+                                                   q0[4] | (q0[5] << 16), q0[6] | (q0[7] << 16)));
+    a[1] = __builtin_bit_cast(bf16x8_t, make_uint4(q1[0] | (q1[1] << 16), q1[2] | (q1[3] << 16),
+                                                   q1[4] | (q1[5] << 16), q1[6] | (q1[7] << 16)));
+    a[2] = __builtin_bit_cast(bf16x8_t, make_uint4(q2[0] | (q2[1] << 16), q2[2] | (q2[3] << 16),
+                                                   q2[4] | (q2[5] << 16), q2[6] | (q2[7] << 16)));
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int term = 0; term < 3; ++term)
+        acc[tt][term] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[term], __builtin_bit_cast(bf16x8_t, xr[tt][i]),
+                                                                acc[tt][term], 0, 0, 0);
+  }
+  // lane holds experts 4g + r of token tt*16 + n
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      part[(slice * RK_TOK + tt * 16 + n) * 16 + 4 * g + r] = (acc[tt][0][r] + acc[tt][1][r]) + acc[tt][2][r];
+}
+
+// Logits of tokens t0 .. t0+63 (rows past T: not written) into slog[token][e]
+// for e < E <= EMAX <= 16, by nw waves of this workgroup (all must call it).
+// part: RK_PART_FLOATS of LDS.  Ends with a barrier.
+template <int KSW, int EMAX>
+__device__ __forceinline__ void route_logits(const uint16_t* x, const float* gw, const float* gb, int E, int64_t T,
+                                             int64_t t0, int d, int nw, float* part, float (*slog)[EMAX]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int sl = wave; sl < RK_SLICES; sl += nw) route_slice<KSW>(x, gw, E, T, t0, d, sl, lane, part);
+  __syncthreads();
+  for (int q = threadIdx.x; q < RK_TOK * EMAX; q += nw * 64) {
+    const int tok = q / EMAX, e = q - tok * EMAX;
+    if (e < E && t0 + tok < T) {
+      float v = part[tok * 16 + e];
+#pragma unroll
+      for (int sl = 1; sl < RK_SLICES; ++sl) v += part[(sl * RK_TOK + tok) * 16 + e];
+      slog[tok][e] = gb ? v + gb[e] : v;
+    }
+  }
+  __syncthreads();
+}
+
+// the k-steps per slice for model width d (0: too wide for the MFMA router)
+inline int route_ksw(int64_t d) {
+  if (d % 8 != 0) return 0;
+  if (d <= RK_SLICES * 32 * 4) return 4;
+  if (d <= RK_SLICES * 32 * 8) return 8;
+  return 0;
+}
+
+// Softmax / top-k / renormalisation of one token by a group of EMAX lanes
+// (lane j of the group: expert j), the arithmetic of route_select: the same
+// max, expf, sequential sum (the group's values gathered in expert order),
+// 1/sum scaling and rank-order renormalisation, so the bits match it.  With
+// equal probabilities or NaN in the group its first lane runs route_select
+// itself (torch's tie order).  Writes prob/topi/topw when `write`, and the
+// top-k to s_ti/s_tw (rows of EMAX... 8 slots) and the selection counts to
+// s_cnt (if not null).  Every lane of the wave must call it.
+template <int EMAX>
+__device__ __forceinline__ void route_select_group(const float* lg, smaul_topk::Pair* q, int E, int k, int64_t t,
+                                                   bool tvalid, const RouteOut& o, bool write, int* s_ti_row,
+                                                   float* s_tw_row, int* s_cnt) {
+  constexpr int G = EMAX;
+  static_assert(G == 4 || G == 8 || G == 16, "group width");
+  const int lane = threadIdx.x & 63;
+  const int j = lane & (G - 1);
+  const int gbase = lane & ~(G - 1);
+  const uint64_t gmask = ((G == 64 ? 0ull : (1ull << G)) - 1ull) << gbase;
+  const bool ev = j < E;
+  const float v = (tvalid && ev) ? lg[j] : 0.0f;
+  float mx = ev ? v : -__builtin_inff();
+#pragma unroll
+  for (int m = 1; m < G; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+  const float ex = ev ? expf(v - mx) : 0.0f;
+  float sum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < G; ++e) {
+    const float xe = __shfl(ex, gbase + e, 64);
+    if (e < E) sum = sum + xe;
+  }
+  const float rs = 1.0f / sum;
+  const float p = ex * rs;
+  int rank = 0;
+  bool tie = p != p;
+#pragma unroll
+  for (int e = 0; e < G; ++e) {
+    const float pe = __shfl(p, gbase + e, 64);
+    if (e < E && e != j) {
+      rank += pe > p ? 1 : 0;
+      tie |= (pe == p) || (pe != pe);
+    }
+  }
+  const bool gtie = (__ballot(tie && ev && tvalid) & gmask) != 0ull;
+  // renormalisation denominator: the selected probabilities in rank order
+  const uint64_t lt_mask = gmask;
+  float denom = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+    if (r < k) {
+      const uint64_t m = __ballot(ev && rank == r) & lt_mask;
+      const int src = m ? (int)__builtin_ctzll(m) : gbase;
+      const float pr = __shfl(p, src, 64);
+      denom = denom + pr;
+    }
+  if (!tvalid) return;
+  if (!gtie) {
+    if (ev) {
+      if (write) o.prob[t * E + j] = p;
+      if (rank < k) {
+        const bool tiny = denom < 1e-6f;
+        const float dcl = fmaxf(denom, 1e-9f);
+        const float tv = tiny ? 1.0f / (float)k : p / dcl;
+        if (write) {
+          o.topi[t * k + rank] = j;
+          o.topw[t * k + rank] = tv;
+        }
+        s_ti_row[rank] = j;
+        s_tw_row[rank] = tv;
+        if (s_cnt && tv > 0.0f) atomicAdd(&s_cnt[j], 1);
+      }
+    }
+  } else if (j == 0) {
+    int ti[8];
+    float tv[8];
+    route_select<EMAX>(lg, q, E, k, t, o, write, ti, tv);
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      if (jj < k) {
+        s_ti_row[jj] = ti[jj];
+        s_tw_row[jj] = tv[jj];
+      }
+    if (s_cnt) {
+      const uint64_t sel = selection_of(ti, tv, E, k);
+      for (int e = 0; e < E; ++e)
+        if ((sel >> e) & 1ull) atomicAdd(&s_cnt[e], 1);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // decode, streaming form (decode_stream_kernel)
 // ---------------------------------------------------------------------------
@@ -1522,31 +1942,65 @@ __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, con
 
 // Inputs of the dispatch that the gate/up kernel performs itself (FUSED):
 // the router's top-k ids and weights of T <= 64 tokens, and where workgroup 0
-// writes the dispatch for the later stages.
+// writes the dispatch for the later stages.  With ROUTE the kernel also
+// routes: gw/gb are the router weight and bias, and workgroup 0 writes
+// prob/topi/topw through o.
 struct DsDispatch {
   const int64_t* topi;
   const float* topw;
   RouteOut o;
   int T, k;
+  const float* gw;
+  const float* gb;
+  int ksw;  // route_ksw(d)
 };
 
+// Expert register width of the routing inside the decode gate/up kernel
+// (E <= 8; waves 0..3 own 16 tokens each).
+constexpr int DS_RT_E = 8;
+
 // FUSED (gate/up only): every workgroup ranks the T <= 64 tokens per expert
-// itself, from topi/topw, into LDS (one wave, ballot ranks in token order,
-// the same rule as dispatch_one_wave) instead of reading a dispatch written by
-// an earlier kernel; workgroup 0 also writes that dispatch (counts, seg_off,
-// tile_off, perm_row, perm_w, inv) for the down projection and the combine.
-template <bool SWIGLU, bool CANON, int KBW, bool FUSED>
+// itself into LDS (one wave, ballot ranks in token order, the same rule as
+// dispatch_one_wave) instead of reading a dispatch written by an earlier
+// kernel; workgroup 0 also writes that dispatch (counts, seg_off, tile_off,
+// perm_row, perm_w, inv) for the down projection and the combine.  ROUTE: the
+// top-k comes from the router's own building blocks run in every workgroup
+// (route_mfma, 16 tokens per wave), bit for bit what router_mfma_kernel
+// computes; otherwise it is read from dd.topi/dd.topw.
+template <bool SWIGLU, bool CANON, int KBW, bool FUSED, bool ROUTE>
 __global__ void __launch_bounds__(DS_WMAX * 64)
 decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
   constexpr int NH = SWIGLU ? 2 : 1;
   static_assert(!FUSED || SWIGLU, "the fused dispatch feeds the gate/up projection");
-  __shared__ float red[2 * DS_WMAX * NH * 2 * 256];
+  static_assert(!ROUTE || FUSED, "routing feeds the fused dispatch");
+  // the partial sums of the GEMM; with ROUTE also the routing scratch before it
+  constexpr int RED_FLOATS = 2 * DS_WMAX * NH * 2 * 256;
+  constexpr int RT_FLOATS = RK_PART_FLOATS + 64 * DS_RT_E + 64 * DS_RT_E * 2;
+  __shared__ __attribute__((aligned(16))) float red[ROUTE && RT_FLOATS > RED_FLOATS ? RT_FLOATS : RED_FLOATS];
   __shared__ int32_t s_perm[FUSED ? 64 * 8 : 1];
   __shared__ int32_t s_off[FUSED ? MAX_E + 1 : 1];
+  __shared__ int s_ti[ROUTE ? 64 : 1][8];
+  __shared__ float s_tw[ROUTE ? 64 : 1][8];
   const int lane = threadIdx.x & 63;
   DsSegs sg;
   if constexpr (FUSED) {
     ds_pointers(p, lane, sg);
+    if constexpr (ROUTE) {
+      // red is free until the GEMM: the logit partials, the logits [64][8]
+      // and the tie scratch [64][8] live in it
+      constexpr int EM = DS_RT_E;
+      static_assert(RT_FLOATS * 4 <= (int)sizeof(red), "routing scratch must fit");
+      float* part = red;
+      float(*slog)[EM] = (float(*)[EM])(red + RK_PART_FLOATS);
+      smaul_topk::Pair(*spair)[EM] = (smaul_topk::Pair(*)[EM])(red + RK_PART_FLOATS + 64 * EM);
+      route_logits<4, EM>((const uint16_t*)p.x, dd.gw, dd.gb, p.E, dd.T, 0, (int)p.K, nw, part, slog);
+      // EM lanes per token, as in router_mfma_kernel
+      constexpr int TPW = 64 / EM;
+      for (int tl = (int)(threadIdx.x >> 6) * TPW + lane / EM; tl < 64; tl += nw * TPW)
+        route_select_group<EM>(slog[tl], spair[tl], p.E, dd.k, tl, tl < dd.T, dd.o, blockIdx.x == 0, s_ti[tl],
+                               s_tw[tl], nullptr);
+      __syncthreads();
+    }
     if (threadIdx.x < 64) {
       const bool valid = lane < dd.T;
       int ti[8];
@@ -1554,9 +2008,14 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         if (j < dd.k) {
-          const int64_t v = valid ? dd.topi[lane * dd.k + j] : -1;
-          ti[j] = (v >= 0 && v < p.E) ? (int)v : -1;
-          tw[j] = valid ? dd.topw[lane * dd.k + j] : 0.0f;
+          if constexpr (ROUTE) {
+            ti[j] = valid ? s_ti[lane][j] : -1;
+            tw[j] = valid ? s_tw[lane][j] : 0.0f;
+          } else {
+            const int64_t v = valid ? dd.topi[lane * dd.k + j] : -1;
+            ti[j] = (v >= 0 && v < p.E) ? (int)v : -1;
+            tw[j] = valid ? dd.topw[lane * dd.k + j] : 0.0f;
+          }
         }
       const uint64_t sel = valid ? selection_of(ti, tw, p.E, dd.k) : 0ull;
       const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
@@ -1584,6 +2043,21 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
   // two row tiles when any segment has more than 16 rows
   if (__ballot(sg.rows > 16) != 0) ds_body<SWIGLU, CANON, KBW, 2>(p, sg, ridx, u0, u1, ctn, red, nw);
   else ds_body<SWIGLU, CANON, KBW, 1>(p, sg, ridx, u0, u1, ctn, red, nw);
+}
+
+// The decode gate/up kernel routes for itself when E <= 8, d <= 1024 (4
+// k-steps per router slice) and it has at least 4 waves.
+// SMAUL_DECODE_ROUTE=0 keeps the router a kernel of its own (A/B timing)
+bool ds_route_enabled() {
+  static const bool on = [] {
+    const char* v = getenv("SMAUL_DECODE_ROUTE");
+    return !(v && strcmp(v, "0") == 0);
+  }();
+  return on;
+}
+
+bool ds_route_ok(int64_t E, int64_t d, int64_t T, int64_t nw) {
+  return ds_route_enabled() && E <= DS_RT_E && route_ksw(d) == 4 && nw >= 4 && T >= 1 && T <= 64;
 }
 
 // K blocks per wave of the streaming decode kernel for K/64 = nkb blocks
@@ -1637,16 +2111,22 @@ int launch_decode_stream(const GemmArgs& a, const DsDispatch* dd, hipStream_t st
   const dim3 grid((unsigned)g), block(nw * 64);
   if constexpr (SWIGLU) {
     if (dd) {
-      if (kbw == 2) hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true>), grid, block, 0, stream, a, nw, *dd);
-      else hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 4, true>), grid, block, 0, stream, a, nw, *dd);
+      if (dd->gw) {
+        if (!ds_route_ok(a.E, a.K, dd->T, nw)) return fail(SMAUL_ERR_INVALID, "decode gate/up: routing shape");
+        if (kbw == 2) hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true, true>), grid, block, 0, stream, a, nw, *dd);
+        else hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 4, true, true>), grid, block, 0, stream, a, nw, *dd);
+      } else {
+        if (kbw == 2) hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true, false>), grid, block, 0, stream, a, nw, *dd);
+        else hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 4, true, false>), grid, block, 0, stream, a, nw, *dd);
+      }
       return check_launch("decode_stream_kernel");
     }
   }
   switch (kbw) {
-    case 2: hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 2, false>), grid, block, 0, stream, a, nw, none); break;
-    case 4: hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 4, false>), grid, block, 0, stream, a, nw, none); break;
+    case 2: hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 2, false, false>), grid, block, 0, stream, a, nw, none); break;
+    case 4: hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 4, false, false>), grid, block, 0, stream, a, nw, none); break;
     default:
-      if constexpr (!SWIGLU) hipLaunchKernelGGL((decode_stream_kernel<false, CANON, 5, false>), grid, block, 0, stream, a, nw, none);
+      if constexpr (!SWIGLU) hipLaunchKernelGGL((decode_stream_kernel<false, CANON, 5, false, false>), grid, block, 0, stream, a, nw, none);
       break;
   }
   return check_launch("decode_stream_kernel");
@@ -1712,29 +2192,14 @@ router_kernel(const void* __restrict__ x, const float* __restrict__ gw, const fl
   // weight staging, and every load of a chunk is in flight before any is
   // used.  The fp32 summation order (per lane: column groups in ascending
   // order, then the butterfly) does not depend on this load order.
-  constexpr int DC = ROUTE_WFLOATS / EMAX;                                  // columns per chunk
-  constexpr int XG = (DC / 8 + 63) / 64;                                    // 8-column groups per lane
+  constexpr int DC = RouteShape<EMAX>::DC;
+  constexpr int XG = RouteShape<EMAX>::XG;
   constexpr int WI = (EMAX * DC / 4 + ROUTE_THREADS - 1) / ROUTE_THREADS;  // weight float4s per thread
   constexpr int XW = XBF16 ? 1 : 2;                                         // 16-byte loads per group
   for (int c0 = 0; c0 < d; c0 += DC) {
     const int cw = min(DC, d - c0);  // d % 8 == 0
     uint4 xr[XG][TB][XW];
-#pragma unroll
-    for (int q = 0; q < XG; ++q) {
-      const int g = lane + 64 * q;
-      if (g < (cw >> 3)) {
-#pragma unroll
-        for (int a = 0; a < TB; ++a) {
-          const int64_t t = tw0 + a < T ? tw0 + a : T - 1;  // rows past T are computed, never written
-          if constexpr (XBF16) {
-            xr[q][a][0] = ldg16((const uint16_t*)x + t * d + c0 + g * 8);
-          } else {
-            xr[q][a][0] = ldg16((const float*)x + t * d + c0 + g * 8);
-            xr[q][a][XW - 1] = ldg16((const float*)x + t * d + c0 + g * 8 + 4);
-          }
-        }
-      }
-    }
+    route_load_x<XBF16, TB, EMAX>(x, T, tw0, c0, cw, d, lane, xr);
     __syncthreads();  // the previous chunk's readers are done with sW
     const int nw = EMAX * (cw >> 2);
     float4 wv[WI];
@@ -1750,77 +2215,12 @@ router_kernel(const void* __restrict__ x, const float* __restrict__ gw, const fl
       if (idx < nw) *(float4*)&sW[(idx / (cw >> 2)) * cw + (idx % (cw >> 2)) * 4] = wv[i];
     }
     __syncthreads();
-#pragma unroll
-    for (int q = 0; q < XG; ++q) {
-      const int g = lane + 64 * q;
-      if (g < (cw >> 3)) {
-        float xv[TB][8];
-#pragma unroll
-        for (int a = 0; a < TB; ++a) {
-          if constexpr (XBF16) {
-            const uint4 v = xr[q][a][0];
-            xv[a][0] = bf2f(v.x & 0xffff); xv[a][1] = bf2f(v.x >> 16);
-            xv[a][2] = bf2f(v.y & 0xffff); xv[a][3] = bf2f(v.y >> 16);
-            xv[a][4] = bf2f(v.z & 0xffff); xv[a][5] = bf2f(v.z >> 16);
-            xv[a][6] = bf2f(v.w & 0xffff); xv[a][7] = bf2f(v.w >> 16);
-          } else {
-            const uint4 v0 = xr[q][a][0], v1 = xr[q][a][XW - 1];
-            xv[a][0] = __uint_as_float(v0.x); xv[a][1] = __uint_as_float(v0.y);
-            xv[a][2] = __uint_as_float(v0.z); xv[a][3] = __uint_as_float(v0.w);
-            xv[a][4] = __uint_as_float(v1.x); xv[a][5] = __uint_as_float(v1.y);
-            xv[a][6] = __uint_as_float(v1.z); xv[a][7] = __uint_as_float(v1.w);
-          }
-        }
-#pragma unroll
-        for (int e = 0; e < EMAX; ++e) {
-          const float4 w0 = *(const float4*)&sW[e * cw + g * 8];
-          const float4 w1 = *(const float4*)&sW[e * cw + g * 8 + 4];
-          const float wv8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-          for (int a = 0; a < TB; ++a)
-#pragma unroll
-            for (int qq = 0; qq < 8; ++qq)
-              acc[a * EMAX + e] = __builtin_fmaf(xv[a][qq], wv8[qq], acc[a * EMAX + e]);
-        }
-      }
-    }
+    route_fma<XBF16, TB, EMAX>(xr, sW, cw, lane, acc);
   }
-  // Halving butterfly over the 64 lanes: at each step a lane keeps half of
-  // its values and adds the partner's copy of them, so the TB*EMAX sums need
-  // TB*EMAX-1 exchanges in all (instead of 6 per value) and the exchanges of
-  // a step are independent.  Afterwards lane l holds the full sum of value
-  // index vidx(l).
   {
-    constexpr int N = TB * EMAX;
-    static_assert(N == 32 || N == 64, "router reduction expects 32 or 64 partial sums per lane");
-    int vidx = 0;
-#pragma unroll
-    for (int step = 0; step < 6; ++step) {
-      const int m = 32 >> step;
-      const int n = N >> step;
-      const bool up = (lane & m) != 0;
-      const uint32_t upmask = up ? 0xffffffffu : 0u;
-      if (n >= 2) {
-        const int half = n >> 1;
-#pragma unroll
-        for (int i = 0; i < N / 2; ++i) {
-          if (i < half) {
-            // select with a bit mask, not `up ? acc[i] : acc[i + half]`: the
-            // compiler turns that into a dynamically indexed array read (a
-            // compare/select over every element of acc)
-            const uint32_t lo = __float_as_uint(acc[i]), hi = __float_as_uint(acc[i + half]);
-            const uint32_t give = (lo & upmask) | (hi & ~upmask);
-            const uint32_t keep = (hi & upmask) | (lo & ~upmask);
-            acc[i] = __uint_as_float(keep) + __shfl_xor(__uint_as_float(give), m, 64);
-          }
-        }
-        if (up) vidx += half;
-      } else {
-        acc[0] += __shfl_xor(acc[0], m, 64);
-      }
-    }
+    const int vidx = route_butterfly<TB, EMAX>(acc, lane);
     const int a = vidx / EMAX, e = vidx % EMAX;
-    const bool writer = N == 64 || (lane & 1) == 0;
+    const bool writer = TB * EMAX == 64 || (lane & 1) == 0;
     if (writer && e < E) slog[wave * TB + a][e] = gb ? acc[0] + gb[e] : acc[0];
   }
   __syncthreads();
@@ -1829,86 +2229,12 @@ router_kernel(const void* __restrict__ x, const float* __restrict__ gw, const fl
   if (tid < TPB) {
     const int64_t t = t0 + tid;
     if (t < T) {
-      float v[EMAX];
-#pragma unroll
-      for (int e = 0; e < EMAX; ++e) v[e] = e < E ? slog[tid][e] : 0.0f;
-      float mx = v[0];  // NaN propagates, as in torch's max reduction
-#pragma unroll
-      for (int e = 1; e < EMAX; ++e)
-        if (e < E) mx = (v[e] > mx || v[e] != v[e]) ? v[e] : mx;
-      float sum = 0.0f;
-#pragma unroll
-      for (int e = 0; e < EMAX; ++e)
-        if (e < E) {
-          v[e] = expf(v[e] - mx);
-          sum = sum + v[e];
-        }
-      const float rs = 1.0f / sum;
-      bool ties = false;
-#pragma unroll
-      for (int e = 0; e < EMAX; ++e)
-        if (e < E) {
-          v[e] = v[e] * rs;
-          o.prob[t * E + e] = v[e];
-          ties |= v[e] != v[e];
-        }
-      // Top-k.  With all-distinct values the selection is unique: the k
-      // largest in descending order, found in registers.  Equal values (or
-      // NaN) go through the exact restatement of torch's selection steps.
       int ti[8];
       float tv[8];
-      if constexpr (EMAX <= 16) {
-#pragma unroll
-        for (int a = 0; a < EMAX; ++a)
-#pragma unroll
-          for (int b = a + 1; b < EMAX; ++b)
-            if (b < E) ties |= v[a] == v[b];
-      } else {
-        ties = true;
-      }
-      if (!ties) {
-        uint64_t used = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (j < k) {
-            int bi = -1;
-            float bv = 0.0f;
-#pragma unroll
-            for (int e = 0; e < EMAX; ++e)
-              if (e < E && !((used >> e) & 1ull) && (bi < 0 || v[e] > bv)) {
-                bi = e;
-                bv = v[e];
-              }
-            used |= 1ull << bi;
-            ti[j] = bi;
-            tv[j] = bv;
-          }
-        }
-      } else {
-        smaul_topk::Pair* q = spair[tid];
-#pragma unroll
-        for (int e = 0; e < EMAX; ++e)
-          if (e < E) q[e] = smaul_topk::Pair{v[e], e};
-        smaul_topk::topk_small(q, E, k);  // k <= 8
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (j < k) {
-            ti[j] = q[j].i;
-            tv[j] = q[j].v;
-          }
-      }
-      float denom = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (j < k) denom = denom + tv[j];
-      const bool tiny = denom < 1e-6f;
-      const float dcl = fmaxf(denom, 1e-9f);
+      route_select<EMAX>(slog[tid], spair[tid], E, k, t, o, true, ti, tv);
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         if (j < k) {
-          tv[j] = tiny ? 1.0f / (float)k : tv[j] / dcl;
-          o.topi[t * k + j] = ti[j];
-          o.topw[t * k + j] = tv[j];
           s_ti[tid][j] = ti[j];
           s_tw[tid][j] = tv[j];
         }
@@ -1921,6 +2247,48 @@ router_kernel(const void* __restrict__ x, const float* __restrict__ gw, const fl
   if (o.blockcnt && tid < E) o.blockcnt[(int64_t)blockIdx.x * E + tid] = s_cnt[tid];
 
   // ---- fused dispatch for a single block (T <= TPB) ---------------------------
+  if (o.counts && gridDim.x == 1 && wave == 0) {
+    const bool valid = lane < T && lane < TPB;
+    dispatch_one_wave(s_ti[valid ? lane : 0], s_tw[valid ? lane : 0], valid, lane, o, E, k);
+  }
+}
+
+// bf16 activations, E <= 16: the logits on the matrix cores (route_logits,
+// 64 tokens per workgroup of 8 waves), then the per-token softmax / top-k /
+// renormalisation by groups of EMAX lanes, block counts and the single-block
+// dispatch, as router_kernel.
+constexpr int ROUTE_MFMA_TPB = RK_TOK;
+constexpr int ROUTE_MFMA_THREADS = 512;
+
+template <int EMAX, bool EXACT, int KSW>
+__global__ void __launch_bounds__(ROUTE_MFMA_THREADS)
+router_mfma_kernel(const uint16_t* __restrict__ x, const float* __restrict__ gw, const float* __restrict__ gb,
+                   RouteOut o, int64_t T, int d, int E_arg, int k) {
+  static_assert(EMAX <= 16, "the MFMA router covers up to 16 experts");
+  const int E = EXACT ? EMAX : E_arg;
+  constexpr int TPB = ROUTE_MFMA_TPB;
+  constexpr int NWAVES = ROUTE_MFMA_THREADS / 64;
+  __shared__ __attribute__((aligned(16))) float part[RK_PART_FLOATS];
+  __shared__ float slog[TPB][EMAX];
+  __shared__ smaul_topk::Pair spair[TPB][EMAX];
+  __shared__ int s_ti[TPB][8];
+  __shared__ float s_tw[TPB][8];
+  __shared__ int s_cnt[EMAX];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * TPB;
+  if (tid < EMAX) s_cnt[tid] = 0;
+  route_logits<KSW, EMAX>(x, gw, gb, E, T, t0, d, NWAVES, part, slog);
+
+  {
+    // EMAX lanes per token
+    constexpr int TPW = 64 / EMAX;
+    for (int tl = wave * TPW + (lane / EMAX); tl < TPB; tl += NWAVES * TPW) {
+      const int64_t t = t0 + tl;
+      route_select_group<EMAX>(slog[tl], spair[tl], E, k, t, t < T, o, true, s_ti[tl], s_tw[tl], s_cnt);
+    }
+  }
+  __syncthreads();
+  if (o.blockcnt && tid < E) o.blockcnt[(int64_t)blockIdx.x * E + tid] = s_cnt[tid];
   if (o.counts && gridDim.x == 1 && wave == 0) {
     const bool valid = lane < T && lane < TPB;
     dispatch_one_wave(s_ti[valid ? lane : 0], s_tw[valid ? lane : 0], valid, lane, o, E, k);
@@ -2316,16 +2684,50 @@ int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* 
 // router tokens per wave for E experts (E <= 4, 8, 16, 64): TB * EMAX partial
 // sums per lane
 static constexpr int route_tb(int64_t E) { return E <= 4 ? 8 : E <= 16 ? 4 : 1; }
-static int route_tpb(int64_t E) { return route_tb(E) * ROUTE_WAVES; }
+// tokens per router workgroup: bf16 activations run router_mfma_kernel
+static bool route_mfma_ok(int64_t E, int64_t d, int x_dtype) {
+  return x_dtype == SMAUL_DTYPE_BF16 && E <= 16 && route_ksw(d) != 0;
+}
+static int route_tpb(int64_t E, int64_t d, int x_dtype) {
+  return route_mfma_ok(E, d, x_dtype) ? ROUTE_MFMA_TPB : route_tb(E) * ROUTE_WAVES;
+}
 
 static int launch_router(const void* x, int x_dtype, const float* gate_w, const float* gate_b,
                          const RouteOut& o, int64_t T, int64_t d, int64_t E, int64_t k,
                          hipStream_t stream) {
-  const int64_t tpb = route_tpb(E);
+  const int64_t tpb = route_tpb(E, d, x_dtype);
   const int64_t nb = (T + tpb - 1) / tpb;
   if (nb > 2147483647LL) return fail(SMAUL_ERR_UNSUPPORTED, "router: too many tokens");
-  const dim3 grid((unsigned)nb), block(ROUTE_THREADS);
   const bool bf = x_dtype == SMAUL_DTYPE_BF16;
+  if (route_mfma_ok(E, d, x_dtype)) {
+    const uint16_t* xb = (const uint16_t*)x;
+    const dim3 grid((unsigned)nb), block(ROUTE_MFMA_THREADS);
+    const int ksw = route_ksw(d);
+#define SMAUL_ROUTE_M2(EMAX, EXACT)                                                                          \
+  if (ksw == 4)                                                                                              \
+    hipLaunchKernelGGL((router_mfma_kernel<EMAX, EXACT, 4>), grid, block, 0, stream, xb, gate_w, gate_b, o, T, \
+                       (int)d, (int)E, (int)k);                                                              \
+  else                                                                                                       \
+    hipLaunchKernelGGL((router_mfma_kernel<EMAX, EXACT, 8>), grid, block, 0, stream, xb, gate_w, gate_b, o, T, \
+                       (int)d, (int)E, (int)k);
+#define SMAUL_ROUTE_M(EMAX)     \
+  if (E == EMAX) {              \
+    SMAUL_ROUTE_M2(EMAX, true)  \
+  } else {                      \
+    SMAUL_ROUTE_M2(EMAX, false) \
+  }
+    if (E <= 4) {
+      SMAUL_ROUTE_M(4)
+    } else if (E <= 8) {
+      SMAUL_ROUTE_M(8)
+    } else {
+      SMAUL_ROUTE_M(16)
+    }
+#undef SMAUL_ROUTE_M
+#undef SMAUL_ROUTE_M2
+    return check_launch("router_mfma_kernel");
+  }
+  const dim3 grid((unsigned)nb), block(ROUTE_THREADS);
 #define SMAUL_ROUTE1(TB, EMAX, EXACT)                                                                     \
   if (bf)                                                                                                 \
     hipLaunchKernelGGL((router_kernel<true, TB, EMAX, EXACT>), grid, block, 0, stream, x, gate_w, gate_b, o, \
@@ -2542,8 +2944,8 @@ int smaul_moe_combine(const void* yperm, int act_dtype, const int64_t* topi, con
 //   seg_off[E+1] tile_off[E+1] perm_row[T*k] perm_w[T*k] inv[T*k]
 //   blockcnt[nb*E] blockoff[nb*E]  (nb = router token blocks)
 //   hdn[T*k, h] (act dtype)  yperm[T*k, d] (act dtype)
-static int64_t route_blocks(int64_t T, int64_t E) {
-  const int64_t tpb = route_tpb(E);
+static int64_t route_blocks(int64_t T, int64_t E, int64_t d, int x_dtype) {
+  const int64_t tpb = route_tpb(E, d, x_dtype);
   return (T + tpb - 1) / tpb;
 }
 
@@ -2555,7 +2957,7 @@ int64_t smaul_moe_workspace_size(int64_t T, int64_t d, int64_t h, int64_t E, int
   int64_t n = 0;
   n += align256((E + 1) * 4) * 2;
   n += align256(R * 4) * 3;
-  n += align256(route_blocks(T, E) * E * 4) * 2;
+  n += align256(route_blocks(T, E, d, act_dtype) * E * 4) * 2;
   n += align256(R * h * el);
   n += align256(R * d * el);
   return n;
@@ -2580,7 +2982,7 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
   if (((uintptr_t)workspace & 255u) != 0) return fail(SMAUL_ERR_INVALID, "moe_forward: workspace not 256-byte aligned");
   const int64_t el = act_dtype == SMAUL_DTYPE_BF16 ? 2 : 4;
   const int64_t R = T * k;
-  const int64_t nb = route_blocks(T, E);
+  const int64_t nb = route_blocks(T, E, d, act_dtype);
   char* ws = (char*)workspace;
   int32_t* seg_off = (int32_t*)ws;
   ws += align256((E + 1) * 4);
@@ -2621,8 +3023,13 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
   od.perm_w = perm_w;
   od.inv = inv;
   if (nb == 1 && !fused) o = od;  // one router block: it dispatches too
-  rc = launch_router(x, act_dtype, gate_w, gate_b, o, T, d, E, k, stream);
-  if (rc) return rc;
+  // ... and at E == 8 it also routes (no router launch)
+  const bool self_routed =
+      fused && act_dtype == SMAUL_DTYPE_BF16 && ds_route_ok(E, d, T, (d / 64) / ds_kbw(d / 64, true));
+  if (!self_routed) {
+    rc = launch_router(x, act_dtype, gate_w, gate_b, o, T, d, E, k, stream);
+    if (rc) return rc;
+  }
   const int64_t max_tiles = (R + bm - 1) / bm + E;
   if (fused) {
     GemmArgs a{};
@@ -2641,7 +3048,8 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
     a.seg_off = seg_off;
     a.tile_off = tile_off;
     a.E = (int)E;
-    const DsDispatch dd{topi, topw, od, (int)T, (int)k};
+    const DsDispatch dd{topi, topw, od, (int)T, (int)k, self_routed ? gate_w : nullptr,
+                        self_routed ? gate_b : nullptr, route_ksw(d)};
     rc = (flags & SMAUL_FLAG_CANONICAL_CODES) ? launch_decode_stream<true, true>(a, &dd, stream)
                                               : launch_decode_stream<true, false>(a, &dd, stream);
     if (rc) return rc;
@@ -2656,7 +3064,7 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
     if (rc) return rc;
   } else if (nb > 1) {
     rc = launch_scan_scatter(topi, topw, blockcnt, blockoff, counts, seg_off, tile_off, perm_row, perm_w, inv,
-                             T, E, k, bm, route_tpb(E), stream);
+                             T, E, k, bm, route_tpb(E, d, act_dtype), stream);
     if (rc) return rc;
   }
   rc = smaul_moe_gate_up(x, act_dtype, perm_row, gate_w8, gate_s, up_w8, up_s, hdn, seg_off, tile_off,
