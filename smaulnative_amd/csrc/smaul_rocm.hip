@@ -1495,86 +1495,96 @@ __device__ __forceinline__ uint32_t bf16_rne(float f) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
-// d <= RK_SLICES * 32 * KSW columns; part[(slice * 64 + token) * 16 + expert]
+// One K slice of the logits: load() issues every activation and weight load
+// of the slice, compute() waits for them, runs the MFMAs and writes the
+// partials part[(slice * 64 + token) * 16 + expert].  Split so that a caller
+// can issue other loads in between that compute() does not wait for.
+// d <= RK_SLICES * 32 * KSW columns.
 template <int KSW>
-__device__ __forceinline__ void route_slice(const uint16_t* x, const float* gw, int E, int64_t T, int64_t t0, int d,
-                                            int slice, int lane, float* part) {
-  const int n = lane & 15, g = lane >> 4;
+struct RouteSlice {
   uint4 xr[4][KSW];
   float4 wr[KSW][2];
-  // Every load is issued unconditionally from an in-bounds address (column 0,
-  // expert 0 or token T-1 where the true one is out of range) and masked
-  // afterwards, so all of them are in flight together.
+  int slice;
+
+  // Every load is issued unconditionally from an in-bounds address (column
+  // 0, expert 0 or token T-1 where the true one is out of range) and masked
+  // in compute(), so all of them are in flight together.
+  __device__ __forceinline__ void load(const uint16_t* x, const float* gw, int E, int64_t T, int64_t t0, int d,
+                                       int sl, int lane) {
+    slice = sl;
+    const int n = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int i = 0; i < KSW; ++i) {
-    const int c = (slice * KSW + i) * 32 + 8 * g;
-    const int cc = c < d ? c : 0;  // d % 8 == 0: a group is all in or all out
+    for (int i = 0; i < KSW; ++i) {
+      const int c = (slice * KSW + i) * 32 + 8 * g;
+      const int cc = c < d ? c : 0;  // d % 8 == 0: a group is all in or all out
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const int64_t t = t0 + tt * 16 + n < T ? t0 + tt * 16 + n : T - 1;  // computed, never written
-      xr[tt][i] = ldg16(x + t * d + cc);
+      for (int tt = 0; tt < 4; ++tt) {
+        const int64_t t = t0 + tt * 16 + n < T ? t0 + tt * 16 + n : T - 1;  // computed, never written
+        xr[tt][i] = ldg16(x + t * d + cc);
+      }
+      const int64_t wrow = n < E ? n : 0;
+      wr[i][0] = *(const float4*)(gw + wrow * d + cc);
+      wr[i][1] = *(const float4*)(gw + wrow * d + cc + 4);
     }
-    const int64_t wrow = n < E ? n : 0;
-    wr[i][0] = *(const float4*)(gw + wrow * d + cc);
-    wr[i][1] = *(const float4*)(gw + wrow * d + cc + 4);
   }
+
+  __device__ __forceinline__ void compute(int E, int d, int lane, float* part) {
+    const int n = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int i = 0; i < KSW; ++i) {
-    const int c = (slice * KSW + i) * 32 + 8 * g;
-    if (c >= d) {
+    for (int i = 0; i < KSW; ++i) {
+      const int c = (slice * KSW + i) * 32 + 8 * g;
+      if (c >= d) {
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) xr[tt][i] = make_uint4(0u, 0u, 0u, 0u);
+        for (int tt = 0; tt < 4; ++tt) xr[tt][i] = make_uint4(0u, 0u, 0u, 0u);
+      }
+      if (c >= d || n >= E) wr[i][0] = wr[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    if (c >= d || n >= E) wr[i][0] = wr[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  f32x4_t acc[4][3];
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int term = 0; term < 3; ++term) acc[tt][term] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < KSW; ++i) {
-    const float w8[8] = {wr[i][0].x, wr[i][0].y, wr[i][0].z, wr[i][0].w,
-                         wr[i][1].x, wr[i][1].y, wr[i][1].z, wr[i][1].w};
-    uint32_t q0[8], q1[8], q2[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      q0[j] = bf16_rne(w8[j]);
-      const float r1 = w8[j] - bf2f(q0[j]);
-      q1[j] = bf16_rne(r1);
-      q2[j] = bf16_rne(r1 - bf2f(q1[j]));
-    }
-    bf16x8_t a[3];
-    a[0] = __builtin_bit_cast(bf16x8_t, make_uint4(q0[0] | (q0[1] << 16), q0[2] | (q0[3] << 16),
-                                                   q0[4] | (q0[5] << 16), q0[6] | (q0[7] << 16)));
-    a[1] = __builtin_bit_cast(bf16x8_t, make_uint4(q1[0] | (q1[1] << 16), q1[2] | (q1[3] << 16),
-                                                   q1[4] | (q1[5] << 16), q1[6] | (q1[7] << 16)));
-    a[2] = __builtin_bit_cast(bf16x8_t, make_uint4(q2[0] | (q2[1] << 16), q2[2] | (q2[3] << 16),
-                                                   q2[4] | (q2[5] << 16), q2[6] | (q2[7] << 16)));
+    f32x4_t acc[4][3];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-      for (int term = 0; term < 3; ++term)
-        acc[tt][term] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[term], __builtin_bit_cast(bf16x8_t, xr[tt][i]),
-                                                                acc[tt][term], 0, 0, 0);
+      for (int term = 0; term < 3; ++term) acc[tt][term] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < KSW; ++i) {
+      const float w8[8] = {wr[i][0].x, wr[i][0].y, wr[i][0].z, wr[i][0].w,
+                           wr[i][1].x, wr[i][1].y, wr[i][1].z, wr[i][1].w};
+      uint32_t q0[8], q1[8], q2[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        q0[j] = bf16_rne(w8[j]);
+        const float r1 = w8[j] - bf2f(q0[j]);
+        q1[j] = bf16_rne(r1);
+        q2[j] = bf16_rne(r1 - bf2f(q1[j]));
+      }
+      bf16x8_t a[3];
+      a[0] = __builtin_bit_cast(bf16x8_t, make_uint4(q0[0] | (q0[1] << 16), q0[2] | (q0[3] << 16),
+                                                     q0[4] | (q0[5] << 16), q0[6] | (q0[7] << 16)));
+      a[1] = __builtin_bit_cast(bf16x8_t, make_uint4(q1[0] | (q1[1] << 16), q1[2] | (q1[3] << 16),
+                                                     q1[4] | (q1[5] << 16), q1[6] | (q1[7] << 16)));
+      a[2] = __builtin_bit_cast(bf16x8_t, make_uint4(q2[0] | (q2[1] << 16), q2[2] | (q2[3] << 16),
+                                                     q2[4] | (q2[5] << 16), q2[6] | (q2[7] << 16)));
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int term = 0; term < 3; ++term)
+          acc[tt][term] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[term], __builtin_bit_cast(bf16x8_t, xr[tt][i]),
+                                                                  acc[tt][term], 0, 0, 0);
+    }
+    // lane holds experts 4g + r of token tt*16 + n
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        part[(slice * RK_TOK + tt * 16 + n) * 16 + 4 * g + r] = (acc[tt][0][r] + acc[tt][1][r]) + acc[tt][2][r];
   }
-  // lane holds experts 4g + r of token tt*16 + n
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      part[(slice * RK_TOK + tt * 16 + n) * 16 + 4 * g + r] = (acc[tt][0][r] + acc[tt][1][r]) + acc[tt][2][r];
-}
+};
 
-// Logits of tokens t0 .. t0+63 (rows past T: not written) into slog[token][e]
-// for e < E <= EMAX <= 16, by nw waves of this workgroup (all must call it).
-// part: RK_PART_FLOATS of LDS.  Ends with a barrier.
-template <int KSW, int EMAX>
-__device__ __forceinline__ void route_logits(const uint16_t* x, const float* gw, const float* gb, int E, int64_t T,
-                                             int64_t t0, int d, int nw, float* part, float (*slog)[EMAX]) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int sl = wave; sl < RK_SLICES; sl += nw) route_slice<KSW>(x, gw, E, T, t0, d, sl, lane, part);
-  __syncthreads();
+// The sum over slices, in slice order, plus the bias: slog[token][e] for
+// e < E, tokens t0.. below T.  Follows the barrier after the partials; ends
+// with a barrier.
+template <int EMAX>
+__device__ __forceinline__ void route_reduce(const float* gb, int E, int64_t T, int64_t t0, int nw,
+                                             const float* part, float (*slog)[EMAX]) {
   for (int q = threadIdx.x; q < RK_TOK * EMAX; q += nw * 64) {
     const int tok = q / EMAX, e = q - tok * EMAX;
     if (e < E && t0 + tok < T) {
@@ -1585,6 +1595,22 @@ __device__ __forceinline__ void route_logits(const uint16_t* x, const float* gw,
     }
   }
   __syncthreads();
+}
+
+// Logits of tokens t0 .. t0+63 (rows past T: not written) into slog[token][e]
+// for e < E <= EMAX <= 16, by nw waves of this workgroup (all must call it).
+// part: RK_PART_FLOATS of LDS.  Ends with a barrier.
+template <int KSW, int EMAX>
+__device__ __forceinline__ void route_logits(const uint16_t* x, const float* gw, const float* gb, int E, int64_t T,
+                                             int64_t t0, int d, int nw, float* part, float (*slog)[EMAX]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int sl = wave; sl < RK_SLICES; sl += nw) {
+    RouteSlice<KSW> rs;
+    rs.load(x, gw, E, T, t0, d, sl, lane);
+    rs.compute(E, d, lane, part);
+  }
+  __syncthreads();
+  route_reduce<EMAX>(gb, E, T, t0, nw, part, slog);
 }
 
 // the k-steps per slice for model width d (0: too wide for the MFMA router)
@@ -1769,21 +1795,20 @@ __device__ __forceinline__ void ds_locate(const DsSegs& s, int j, int& e, int& r
   nrows = min(DS_ROWS, __builtin_amdgcn_readlane(s.rows, e) - pass * DS_ROWS);
 }
 
-// ridx: logical row -> activation row (SwiGLU only; down reads its rows in place)
-template <bool SWIGLU, bool CANON, int KBW, int NRT>
-__device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, const int32_t* ridx, int u0,
-                                        int u1, int ctn, float* red, int nw) {
-  constexpr int NH = SWIGLU ? 2 : 1;
-  const int lane = threadIdx.x & 63;
-  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kq = (lane >> 4) * 16;
-  const int64_t kb0 = (int64_t)ks * KBW;
-  const f32x4_t z4 = {0.f, 0.f, 0.f, 0.f};
-  const int last = u1 - 1;
+// The register ring of weight codes and scales: DS_D units of this wave's K
+// slice (blocks kb0 .. kb0+KBW-1 of 16 columns), unit u of segment j = u / ctn
+// at column tile u % ctn.
+template <bool SWIGLU, int KBW>
+struct DsRing {
+  static constexpr int NH = SWIGLU ? 2 : 1;
+  uint4 bw[DS_D][KBW][NH];
+  float sw[DS_D][KBW][NH];
 
   // the wave's codes and scales of unit u: block b of stream h at
   // wsrc[h] + b*64 and ssrc[h] + b
-  auto unit_src = [&](int u, const uint8_t* (&wsrc)[NH], const float* (&ssrc)[NH]) {
+  __device__ __forceinline__ static void unit_src(const GemmArgs& p, const DsSegs& sg, int ctn, int64_t kb0, int kq,
+                                                  int lane, int u, const uint8_t* (&wsrc)[NH],
+                                                  const float* (&ssrc)[NH]) {
     const int j = u / ctn;
     const int ct = u - j * ctn;
     int e, r0, nr;
@@ -1795,13 +1820,12 @@ __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, con
       wsrc[NH - 1] = ds_ptr<const uint8_t>(sg.w2, e) + col * p.K + kb0 * 64 + kq;
       ssrc[NH - 1] = ds_ptr<const float>(sg.s2, e) + col * p.nt + kb0;
     }
-  };
-  uint4 bw[DS_D][KBW][NH];
-  float sw[DS_D][KBW][NH];
-  auto fetch = [&](int slot, int u) {
+  }
+  __device__ __forceinline__ void fetch(const GemmArgs& p, const DsSegs& sg, int ctn, int64_t kb0, int kq, int lane,
+                                        int slot, int u) {
     const uint8_t* ws[NH];
     const float* ss[NH];
-    unit_src(u, ws, ss);
+    unit_src(p, sg, ctn, kb0, kq, lane, u, ws, ss);
 #pragma unroll
     for (int b = 0; b < KBW; ++b)
 #pragma unroll
@@ -1809,22 +1833,46 @@ __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, con
         bw[slot][b][h] = ldg16(ws[h] + b * 64);
         sw[slot][b][h] = ldgf(ss[h] + b);
       }
-  };
+  }
+};
+
+// ridx: logical row -> activation row (SwiGLU only; down reads its rows in
+// place).  prefetched: the ring already holds units u0 .. u0+DS_D-1 (clamped
+// to u1-1).
+template <bool SWIGLU, bool CANON, int KBW, int NRT>
+__device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, const int32_t* ridx, int u0,
+                                        int u1, int ctn, float* red, int nw, DsRing<SWIGLU, KBW>& ring,
+                                        bool prefetched) {
+  constexpr int NH = SWIGLU ? 2 : 1;
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kq = (lane >> 4) * 16;
+  const int64_t kb0 = (int64_t)ks * KBW;
+  const f32x4_t z4 = {0.f, 0.f, 0.f, 0.f};
+  const int last = u1 - 1;
+
   // the segment's activation rows, this wave's K slice
   uint4 a0[NRT][KBW], a1[NRT][KBW];
   auto load_a = [&](int j) {
     int e, r0, nr;
     ds_locate(sg, j, e, r0, nr);
+    if (nr > 0) {  // uniform (always true unless a caller asks for empty segments)
 #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) {
-      const int64_t lr = r0 + min(rt * 16 + (lane & 15), nr - 1);
-      const int64_t xr = SWIGLU ? (int64_t)ridx[lr] : lr;
-      const uint16_t* ar = (const uint16_t*)p.x + xr * p.ldx + kb0 * 64 + kq;
+      for (int rt = 0; rt < NRT; ++rt) {
+        const int64_t lr = r0 + min(rt * 16 + (lane & 15), nr - 1);
+        const int64_t xr = SWIGLU ? (int64_t)ridx[lr] : lr;
+        const uint16_t* ar = (const uint16_t*)p.x + xr * p.ldx + kb0 * 64 + kq;
 #pragma unroll
-      for (int b = 0; b < KBW; ++b) {
-        a0[rt][b] = ldg16(ar + b * 64);
-        a1[rt][b] = ldg16(ar + b * 64 + 8);
+        for (int b = 0; b < KBW; ++b) {
+          a0[rt][b] = ldg16(ar + b * 64);
+          a1[rt][b] = ldg16(ar + b * 64 + 8);
+        }
       }
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int b = 0; b < KBW; ++b) a0[rt][b] = a1[rt][b] = make_uint4(0u, 0u, 0u, 0u);
     }
     // Wait for the rows here: on the path that reloads them they are the
     // newest loads, and a wait placed after the branch would have to assume
@@ -1837,107 +1885,118 @@ __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, con
   };
 
   // the first unit's codes go out first, then its rows, then the rest of the ring
-  fetch(0, u0);
+  if (!prefetched) ring.fetch(p, sg, ctn, kb0, kq, lane, 0, u0);
   int cur_j = u0 / ctn;
   load_a(cur_j);
+  if (!prefetched) {
 #pragma unroll
-  for (int i = 1; i < DS_D; ++i) fetch(i, min(u0 + i, last));
+    for (int i = 1; i < DS_D; ++i) ring.fetch(p, sg, ctn, kb0, kq, lane, i, min(u0 + i, last));
+  }
 
   const int nthr = nw * 64;
   const int per_buf = nw * NH * NRT * 256;
   int buf = 0;
-  // whole rounds of DS_D units; units past the range recompute the last one
-  // and store nothing, so every wave reaches every barrier
-  for (int it = u0; it <= last; it += DS_D) {
+  // Unit u in ring slot i: its segment's rows, the MFMAs and scale FMAs of the
+  // wave's K slice, the refill of slot i with unit `next` (when refill), the
+  // partials to LDS, one barrier, and the workgroup's epilogue.
+  auto unit = [&](int i, int u, bool refill, int next) {
+    const int j = u / ctn;
+    if (j != cur_j) {  // uniform: a new segment's rows
+      load_a(j);
+      cur_j = j;
+    }
+    const uint8_t* nws[NH];
+    const float* nss[NH];
+    if (refill) DsRing<SWIGLU, KBW>::unit_src(p, sg, ctn, kb0, kq, lane, next, nws, nss);
+    f32x4_t acc[NH][NRT];
 #pragma unroll
-    for (int i = 0; i < DS_D; ++i) {
-      const bool live = it + i <= last;
-      const int u = min(it + i, last);
-      const int j = u / ctn;
-      if (j != cur_j) {  // uniform: a new segment's rows
-        load_a(j);
-        cur_j = j;
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt) acc[h][rt] = z4;
+#pragma unroll
+    for (int b = 0; b < KBW; ++b) {
+      bf16x8_t g0[NH], g1[NH];
+      float sc[NH];
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        uint32_t d[8];
+        decode4<CANON>(ring.bw[i][b][h].x, d[0], d[1]);
+        decode4<CANON>(ring.bw[i][b][h].y, d[2], d[3]);
+        decode4<CANON>(ring.bw[i][b][h].z, d[4], d[5]);
+        decode4<CANON>(ring.bw[i][b][h].w, d[6], d[7]);
+        g0[h] = __builtin_bit_cast(bf16x8_t, make_uint4(d[0], d[1], d[2], d[3]));
+        g1[h] = __builtin_bit_cast(bf16x8_t, make_uint4(d[4], d[5], d[6], d[7]));
+        sc[h] = ring.sw[i][b][h];
+        if (refill) {
+          ring.bw[i][b][h] = ldg16(nws[h] + b * 64);
+          ring.sw[i][b][h] = ldgf(nss[h] + b);
+        }
       }
-      const uint8_t* nws[NH];
-      const float* nss[NH];
-      unit_src(min(it + i + DS_D, last), nws, nss);
-      f32x4_t acc[NH][NRT];
 #pragma unroll
-      for (int h = 0; h < NH; ++h)
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) acc[h][rt] = z4;
-#pragma unroll
-      for (int b = 0; b < KBW; ++b) {
-        bf16x8_t g0[NH], g1[NH];
-        float sc[NH];
+      for (int rt = 0; rt < NRT; ++rt) {
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
-          uint32_t d[8];
-          decode4<CANON>(bw[i][b][h].x, d[0], d[1]);
-          decode4<CANON>(bw[i][b][h].y, d[2], d[3]);
-          decode4<CANON>(bw[i][b][h].z, d[4], d[5]);
-          decode4<CANON>(bw[i][b][h].w, d[6], d[7]);
-          g0[h] = __builtin_bit_cast(bf16x8_t, make_uint4(d[0], d[1], d[2], d[3]));
-          g1[h] = __builtin_bit_cast(bf16x8_t, make_uint4(d[4], d[5], d[6], d[7]));
-          sc[h] = sw[i][b][h];
-          bw[i][b][h] = ldg16(nws[h] + b * 64);
-          sw[i][b][h] = ldgf(nss[h] + b);
-        }
+          f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a0[rt][b]), g0[h], z4, 0,
+                                                              0, 0);
+          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a1[rt][b]), g1[h], q, 0, 0, 0);
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-          for (int h = 0; h < NH; ++h) {
-            f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a0[rt][b]), g0[h],
-                                                                z4, 0, 0, 0);
-            q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a1[rt][b]), g1[h], q, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[h][rt][r] = __builtin_fmaf(sc[h], q[r], acc[h][rt][r]);
-          }
-      }
-      // partials: red[buf][ks][h][rt][r][lane]
-      float* rb = red + buf * per_buf;
-#pragma unroll
-      for (int h = 0; h < NH; ++h)
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) rb[((ks * NH + h) * NRT + rt) * 256 + r * 64 + lane] = acc[h][rt][r];
-      __syncthreads();
-      if (live) {
-        int e, r0, nr;
-        ds_locate(sg, j, e, r0, nr);
-        const int ct = u - j * ctn;
-        for (int q = threadIdx.x; q < NRT * 256; q += nthr) {
-          const int rt = q >> 8, r = (q >> 6) & 3, ln = q & 63;
-          const int lr = rt * 16 + (ln >> 4) * 4 + r;
-          // all partials are read before the first add (independent LDS
-          // reads in flight together), then summed in K-split order
-          float pg[DS_WMAX], pu[DS_WMAX];
-#pragma unroll
-          for (int k2 = 0; k2 < DS_WMAX; ++k2)
-            if (k2 < nw) {
-              pg[k2] = rb[(k2 * NH) * NRT * 256 + q];
-              if constexpr (SWIGLU) pu[k2] = rb[(k2 * NH + 1) * NRT * 256 + q];
-            }
-          float g = pg[0];
-#pragma unroll
-          for (int k2 = 1; k2 < DS_WMAX; ++k2)
-            if (k2 < nw) g += pg[k2];
-          float v = g;
-          if constexpr (SWIGLU) {
-            float uu = pu[0];
-#pragma unroll
-            for (int k2 = 1; k2 < DS_WMAX; ++k2)
-              if (k2 < nw) uu += pu[k2];
-            v = silu_f(bf2f(f2bf(g))) * bf2f(f2bf(uu));
-          }
-          if (lr < nr)
-            ((uint16_t*)p.y)[(int64_t)(r0 + lr) * p.ldy + (int64_t)ct * 16 + (ln & 15)] = (uint16_t)f2bf(v);
+          for (int r = 0; r < 4; ++r) acc[h][rt][r] = __builtin_fmaf(sc[h], q[r], acc[h][rt][r]);
         }
       }
-      buf ^= 1;
     }
+    // partials: red[buf][ks][h][rt][r][lane]
+    float* rb = red + buf * per_buf;
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rb[((ks * NH + h) * NRT + rt) * 256 + r * 64 + lane] = acc[h][rt][r];
+    __syncthreads();
+    int e, r0, nr;
+    ds_locate(sg, j, e, r0, nr);
+    const int ct = u - j * ctn;
+    for (int q = threadIdx.x; q < NRT * 256; q += nthr) {
+      const int rt = q >> 8, r = (q >> 6) & 3, ln = q & 63;
+      const int lr = rt * 16 + (ln >> 4) * 4 + r;
+      // all partials are read before the first add (independent LDS reads in
+      // flight together), then summed in K-split order
+      float pg[DS_WMAX], pu[DS_WMAX];
+#pragma unroll
+      for (int k2 = 0; k2 < DS_WMAX; ++k2)
+        if (k2 < nw) {
+          pg[k2] = rb[(k2 * NH) * NRT * 256 + q];
+          if constexpr (SWIGLU) pu[k2] = rb[(k2 * NH + 1) * NRT * 256 + q];
+        }
+      float g = pg[0];
+#pragma unroll
+      for (int k2 = 1; k2 < DS_WMAX; ++k2)
+        if (k2 < nw) g += pg[k2];
+      float v = g;
+      if constexpr (SWIGLU) {
+        float uu = pu[0];
+#pragma unroll
+        for (int k2 = 1; k2 < DS_WMAX; ++k2)
+          if (k2 < nw) uu += pu[k2];
+        v = silu_f(bf2f(f2bf(g))) * bf2f(f2bf(uu));
+      }
+      if (lr < nr) ((uint16_t*)p.y)[(int64_t)(r0 + lr) * p.ldy + (int64_t)ct * 16 + (ln & 15)] = (uint16_t)f2bf(v);
+    }
+    buf ^= 1;
+  };
+  // Whole rounds of DS_D units with every refill issued (past the range they
+  // re-load the last unit, which is never consumed), then a last partial
+  // round without refills: no unit is computed twice and no load sits behind
+  // a branch inside the rounds.
+  const int n = u1 - u0;
+  int it = 0;
+  for (; it + DS_D < n; it += DS_D) {
+#pragma unroll
+    for (int i = 0; i < DS_D; ++i) unit(i, u0 + it + i, true, min(u0 + it + i + DS_D, last));
   }
+#pragma unroll
+  for (int i = 0; i < DS_D; ++i)
+    if (it + i < n) unit(i, u0 + it + i, false, 0);  // uniform
 }
 
 // Inputs of the dispatch that the gate/up kernel performs itself (FUSED):
@@ -1974,7 +2033,7 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
   static_assert(!FUSED || SWIGLU, "the fused dispatch feeds the gate/up projection");
   static_assert(!ROUTE || FUSED, "routing feeds the fused dispatch");
   // the partial sums of the GEMM; with ROUTE also the routing scratch before it
-  constexpr int RED_FLOATS = 2 * DS_WMAX * NH * 2 * 256;
+  constexpr int RED_FLOATS = 2 * DS_WMAX * NH * (DS_ROWS / 16) * 256;
   constexpr int RT_FLOATS = RK_PART_FLOATS + 64 * DS_RT_E + 64 * DS_RT_E * 2;
   __shared__ __attribute__((aligned(16))) float red[ROUTE && RT_FLOATS > RED_FLOATS ? RT_FLOATS : RED_FLOATS];
   __shared__ int32_t s_perm[FUSED ? 64 * 8 : 1];
@@ -1982,9 +2041,19 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
   __shared__ int s_ti[ROUTE ? 64 : 1][8];
   __shared__ float s_tw[ROUTE ? 64 : 1][8];
   const int lane = threadIdx.x & 63;
+  const int ctn = (int)(p.N >> 4);
+  const int64_t kb0 = (int64_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * KBW;
+  const int kq = (lane >> 4) * 16;
+  DsRing<SWIGLU, KBW> ring;
+  const bool prefetched = false;
   DsSegs sg;
   if constexpr (FUSED) {
     ds_pointers(p, lane, sg);
+    // With ROUTE, the wave's router loads go out first (waves 0..7 own the
+    // eight K slices; nw == 8 is required), then the ring below, so the
+    // routing waits for its own data only.
+    RouteSlice<4> rs;
+    if constexpr (ROUTE) rs.load((const uint16_t*)p.x, dd.gw, p.E, dd.T, 0, (int)p.K, (int)(threadIdx.x >> 6), lane);
     if constexpr (ROUTE) {
       // red is free until the GEMM: the logit partials, the logits [64][8]
       // and the tie scratch [64][8] live in it
@@ -1993,7 +2062,10 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
       float* part = red;
       float(*slog)[EM] = (float(*)[EM])(red + RK_PART_FLOATS);
       smaul_topk::Pair(*spair)[EM] = (smaul_topk::Pair(*)[EM])(red + RK_PART_FLOATS + 64 * EM);
-      route_logits<4, EM>((const uint16_t*)p.x, dd.gw, dd.gb, p.E, dd.T, 0, (int)p.K, nw, part, slog);
+      static_assert(RK_SLICES == DS_WMAX, "one router slice per wave");
+      rs.compute(p.E, (int)p.K, lane, part);
+      __syncthreads();
+      route_reduce<EM>(dd.gb, p.E, dd.T, 0, nw, part, slog);
       // EM lanes per token, as in router_mfma_kernel
       constexpr int TPW = 64 / EM;
       for (int tl = (int)(threadIdx.x >> 6) * TPW + lane / EM; tl < 64; tl += nw * TPW)
@@ -2035,18 +2107,17 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
     sg = ds_segments(p, lane);
   }
   const int32_t* ridx = FUSED ? (const int32_t*)s_perm : p.row_idx;
-  const int ctn = (int)(p.N >> 4);
   const int64_t U = (int64_t)sg.total * ctn;
   const int u0 = (int)((int64_t)blockIdx.x * U / gridDim.x);
   const int u1 = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
   if (u0 >= u1) return;  // uniform per workgroup
   // two row tiles when any segment has more than 16 rows
-  if (__ballot(sg.rows > 16) != 0) ds_body<SWIGLU, CANON, KBW, 2>(p, sg, ridx, u0, u1, ctn, red, nw);
-  else ds_body<SWIGLU, CANON, KBW, 1>(p, sg, ridx, u0, u1, ctn, red, nw);
+  if (__ballot(sg.rows > 16) != 0) ds_body<SWIGLU, CANON, KBW, 2>(p, sg, ridx, u0, u1, ctn, red, nw, ring, prefetched);
+  else ds_body<SWIGLU, CANON, KBW, 1>(p, sg, ridx, u0, u1, ctn, red, nw, ring, prefetched);
 }
 
 // The decode gate/up kernel routes for itself when E <= 8, d <= 1024 (4
-// k-steps per router slice) and it has at least 4 waves.
+// k-steps per router slice) and it has 8 waves (one router slice each).
 // SMAUL_DECODE_ROUTE=0 keeps the router a kernel of its own (A/B timing)
 bool ds_route_enabled() {
   static const bool on = [] {
@@ -2057,15 +2128,18 @@ bool ds_route_enabled() {
 }
 
 bool ds_route_ok(int64_t E, int64_t d, int64_t T, int64_t nw) {
-  return ds_route_enabled() && E <= DS_RT_E && route_ksw(d) == 4 && nw >= 4 && T >= 1 && T <= 64;
+  return ds_route_enabled() && E <= DS_RT_E && route_ksw(d) == 4 && nw == RK_SLICES && T >= 1 && T <= 64;
 }
 
 // K blocks per wave of the streaming decode kernel for K/64 = nkb blocks
 // (at most DS_WMAX waves), or 0 when no instance fits
 int ds_kbw(int64_t nkb, bool swiglu) {
-  const int cand[3] = {2, 4, 5};
+  // gate/up beyond 2 blocks per wave, and 4 blocks per wave for down, spill
+  // registers with rows held for up to 64 tokens; those shapes run
+  // decode_gemm_kernel
+  const int cand[2] = {2, 5};
   for (int kb : cand) {
-    if (swiglu && kb == 5) continue;  // gate/up at 5 blocks per wave spills
+    if (swiglu && kb != 2) continue;
     if (nkb % kb == 0 && nkb / kb <= DS_WMAX) return kb;
   }
   return 0;
@@ -2113,21 +2187,17 @@ int launch_decode_stream(const GemmArgs& a, const DsDispatch* dd, hipStream_t st
     if (dd) {
       if (dd->gw) {
         if (!ds_route_ok(a.E, a.K, dd->T, nw)) return fail(SMAUL_ERR_INVALID, "decode gate/up: routing shape");
-        if (kbw == 2) hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true, true>), grid, block, 0, stream, a, nw, *dd);
-        else hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 4, true, true>), grid, block, 0, stream, a, nw, *dd);
+        hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true, true>), grid, block, 0, stream, a, nw, *dd);
       } else {
-        if (kbw == 2) hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true, false>), grid, block, 0, stream, a, nw, *dd);
-        else hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 4, true, false>), grid, block, 0, stream, a, nw, *dd);
+        hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true, false>), grid, block, 0, stream, a, nw, *dd);
       }
       return check_launch("decode_stream_kernel");
     }
   }
-  switch (kbw) {
-    case 2: hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 2, false, false>), grid, block, 0, stream, a, nw, none); break;
-    case 4: hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 4, false, false>), grid, block, 0, stream, a, nw, none); break;
-    default:
-      if constexpr (!SWIGLU) hipLaunchKernelGGL((decode_stream_kernel<false, CANON, 5, false, false>), grid, block, 0, stream, a, nw, none);
-      break;
+  if (kbw == 2) {
+    hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 2, false, false>), grid, block, 0, stream, a, nw, none);
+  } else {
+    if constexpr (!SWIGLU) hipLaunchKernelGGL((decode_stream_kernel<false, CANON, 5, false, false>), grid, block, 0, stream, a, nw, none);
   }
   return check_launch("decode_stream_kernel");
 }

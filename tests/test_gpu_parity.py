@@ -271,6 +271,25 @@ def test_moe_decode_regime(T, E, k, skew):
     assert rel_l2(out.float(), ref.out.float()) < 2e-3
 
 
+@pytest.mark.parametrize("T,skew", [(64, (9.0, [], 0.0)), (40, (9.0, [3, 4, 5, 6, 7], 9.0)), (7, None)])
+def test_moe_decode_c4_shape(T, skew):
+    """Config-4 widths in the decode regime: one expert holding every token
+    (four 16-row tiles), experts left idle (the gate/up kernel's early weight
+    loads assume every expert runs and are re-issued), and a tiny step."""
+    print(f"case decode c4 T={T} skew={skew}", flush=True)
+    d, h, E, k = 1024, 2560, 8, 2
+    x, gw, gb, experts = make_moe(640 + T, T, d, h, E, k, skew=skew)
+    ref = oracle.moe_forward(x, gw, gb, experts, k)
+    out, prob, topi, counts = gpu_moe(x, gw, gb, experts, k)
+    assert torch.equal(topi.reshape(-1, k), ref.topi.reshape(-1, k))
+    assert counts.tolist() == ref.counts
+    if skew is not None:
+        assert max(ref.counts) == T
+    err = rel_l2(out.float(), ref.out.float())
+    print(f"counts {ref.counts} rel_l2={err:.3e}")
+    assert err < 2e-3
+
+
 def test_moe_skewed_segments():
     """Config-5 style skew (one expert ~40 %, three < 1 %) at a reduced size."""
     x, gw, gb, experts = make_moe(55, 2048, 256, 640, 16, 2, skew=(2.2, [13, 14, 15], 4.0))
