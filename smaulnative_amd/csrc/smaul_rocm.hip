@@ -2505,17 +2505,20 @@ dispatch_small_kernel(const int64_t* __restrict__ topi, const float* __restrict_
 // ---------------------------------------------------------------------------
 // combine: out[t] = cast(sum over ascending expert id of y * w), fp32, no FMA
 // ---------------------------------------------------------------------------
-template <bool BF16>
+template <bool BF16, int CW>
 __global__ void __launch_bounds__(256)
 combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
                const float* __restrict__ topw, const int32_t* __restrict__ inv,
                void* __restrict__ out, int64_t T, int d, int k) {
-  // thread handles 8 consecutive columns of one token
-  const int cpt = d / 8;  // chunks per token (d % 8 == 0 enforced by the host)
+  // a thread handles CW (16, or 8 when d % 16 != 0) consecutive columns of
+  // one token; every row load of its k slots is issued before the first product
+  static_assert(CW == 8 || CW == 16, "columns per thread");
+  constexpr int NV = BF16 ? CW / 8 : CW / 4;  // 16-byte loads per row chunk
+  const int cpt = d / CW;                      // chunks per token (d % CW == 0)
   const int64_t gidx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t t = gidx / cpt;
   if (t >= T) return;
-  const int c0 = (int)(gidx % cpt) * 8;
+  const int c0 = (int)(gidx % cpt) * CW;
   // gather (expert, row, weight) of dispatched slots, sort by expert id
   int ex[8];
   int rw[8];
@@ -2536,40 +2539,56 @@ combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
     rw[q] = pos;
     wt[q] = topw[t * k + j];
   }
-  float acc[8];
+  uint4 yv[8][NV];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
-  for (int s = 0; s < n; ++s) {
-    float yv[8];
-    if constexpr (BF16) {
-      const uint4 v = *(const uint4*)((const uint16_t*)yperm + (int64_t)rw[s] * d + c0);
-      yv[0] = bf2f(v.x & 0xffff); yv[1] = bf2f(v.x >> 16);
-      yv[2] = bf2f(v.y & 0xffff); yv[3] = bf2f(v.y >> 16);
-      yv[4] = bf2f(v.z & 0xffff); yv[5] = bf2f(v.z >> 16);
-      yv[6] = bf2f(v.w & 0xffff); yv[7] = bf2f(v.w >> 16);
-    } else {
-      const float4* src = (const float4*)((const float*)yperm + (int64_t)rw[s] * d + c0);
-      const float4 a = src[0], b = src[1];
-      yv[0] = a.x; yv[1] = a.y; yv[2] = a.z; yv[3] = a.w;
-      yv[4] = b.x; yv[5] = b.y; yv[6] = b.z; yv[7] = b.w;
-    }
+  for (int s = 0; s < 8; ++s)
+    if (s < n) {
+      const char* src = (const char*)yperm + ((int64_t)rw[s] * d + c0) * (BF16 ? 2 : 4);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const float pr = yv[q] * wt[s];   // rounded product (library built with -ffp-contract=off)
-      acc[q] = acc[q] + pr;
+      for (int v = 0; v < NV; ++v) yv[s][v] = ldg16(src + v * 16);
     }
-  }
+  float acc[CW];
+#pragma unroll
+  for (int q = 0; q < CW; ++q) acc[q] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    if (s < n) {
+      float y[CW];
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        if constexpr (BF16) {
+          const uint4 w = yv[s][v];
+          y[v * 8 + 0] = bf2f(w.x & 0xffff); y[v * 8 + 1] = bf2f(w.x >> 16);
+          y[v * 8 + 2] = bf2f(w.y & 0xffff); y[v * 8 + 3] = bf2f(w.y >> 16);
+          y[v * 8 + 4] = bf2f(w.z & 0xffff); y[v * 8 + 5] = bf2f(w.z >> 16);
+          y[v * 8 + 6] = bf2f(w.w & 0xffff); y[v * 8 + 7] = bf2f(w.w >> 16);
+        } else {
+          const uint4 w = yv[s][v];
+          y[v * 4 + 0] = __uint_as_float(w.x); y[v * 4 + 1] = __uint_as_float(w.y);
+          y[v * 4 + 2] = __uint_as_float(w.z); y[v * 4 + 3] = __uint_as_float(w.w);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < CW; ++q) {
+        const float pr = y[q] * wt[s];  // rounded product (library built with -ffp-contract=off)
+        acc[q] = acc[q] + pr;
+      }
+    }
   if constexpr (BF16) {
-    uint4 o;
-    o.x = f2bf(acc[0]) | (f2bf(acc[1]) << 16);
-    o.y = f2bf(acc[2]) | (f2bf(acc[3]) << 16);
-    o.z = f2bf(acc[4]) | (f2bf(acc[5]) << 16);
-    o.w = f2bf(acc[6]) | (f2bf(acc[7]) << 16);
-    *(uint4*)((uint16_t*)out + t * d + c0) = o;
+    uint4* dst = (uint4*)((uint16_t*)out + t * d + c0);
+#pragma unroll
+    for (int v = 0; v < CW / 8; ++v) {
+      uint4 o;
+      o.x = f2bf(acc[v * 8 + 0]) | (f2bf(acc[v * 8 + 1]) << 16);
+      o.y = f2bf(acc[v * 8 + 2]) | (f2bf(acc[v * 8 + 3]) << 16);
+      o.z = f2bf(acc[v * 8 + 4]) | (f2bf(acc[v * 8 + 5]) << 16);
+      o.w = f2bf(acc[v * 8 + 6]) | (f2bf(acc[v * 8 + 7]) << 16);
+      dst[v] = o;
+    }
   } else {
     float4* dst = (float4*)((float*)out + t * d + c0);
-    dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+#pragma unroll
+    for (int v = 0; v < CW / 4; ++v) dst[v] = make_float4(acc[v * 4], acc[v * 4 + 1], acc[v * 4 + 2], acc[v * 4 + 3]);
   }
 }
 
@@ -2999,14 +3018,17 @@ int smaul_moe_combine(const void* yperm, int act_dtype, const int64_t* topi, con
   if (T == 0) return SMAUL_OK;
   if (!yperm || !topi || !topw || !inv || !out) return fail(SMAUL_ERR_INVALID, "combine: null pointer");
   if (!aligned16(yperm) || !aligned16(out)) return fail(SMAUL_ERR_INVALID, "combine: unaligned buffers");
-  const int64_t total = T * (d / 8);
+  const bool wide = d % 16 == 0;
+  const int64_t total = T * (d / (wide ? 16 : 8));
   const int64_t blocks = (total + 255) / 256;
-  if (act_dtype == SMAUL_DTYPE_BF16)
-    hipLaunchKernelGGL(combine_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, yperm, topi,
-                       topw, inv, out, T, (int)d, (int)k);
-  else
-    hipLaunchKernelGGL(combine_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, yperm, topi,
-                       topw, inv, out, T, (int)d, (int)k);
+  const dim3 grid((unsigned)blocks), block(256);
+  if (act_dtype == SMAUL_DTYPE_BF16) {
+    if (wide) hipLaunchKernelGGL((combine_kernel<true, 16>), grid, block, 0, stream, yperm, topi, topw, inv, out, T, (int)d, (int)k);
+    else hipLaunchKernelGGL((combine_kernel<true, 8>), grid, block, 0, stream, yperm, topi, topw, inv, out, T, (int)d, (int)k);
+  } else {
+    if (wide) hipLaunchKernelGGL((combine_kernel<false, 16>), grid, block, 0, stream, yperm, topi, topw, inv, out, T, (int)d, (int)k);
+    else hipLaunchKernelGGL((combine_kernel<false, 8>), grid, block, 0, stream, yperm, topi, topw, inv, out, T, (int)d, (int)k);
+  }
   return check_launch("combine_kernel");
 }
 

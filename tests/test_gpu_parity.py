@@ -388,6 +388,39 @@ def test_moe_raw_codes_any_flags(T, flags, block_m):
     assert err < 2e-3
 
 
+@pytest.mark.parametrize("T,d,k", [(37, 24, 3), (100, 1040, 2), (5, 2048, 4)])
+def test_combine_entry_direct(T, d, k):
+    """smaul_moe_combine on its own (16 columns per thread, or 8 when d % 16
+    != 0): ascending expert order, fp32 sum from +0 of rounded products,
+    slots with inv < 0 skipped."""
+    from smaulnative_amd import _lib
+    print(f"case combine T={T} d={d} k={k}", flush=True)
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(T * d + k)
+    E = 8
+    topi = torch.stack([torch.randperm(E, generator=gen)[:k] for _ in range(T)]).to(torch.int64)
+    topw = torch.rand(T, k, generator=gen)
+    R = T * k
+    perm = torch.randperm(R, generator=gen).to(torch.int32)
+    inv = perm.reshape(T, k).clone()
+    inv[torch.rand(T, k, generator=gen) < 0.15] = -1
+    yperm = torch.randn(R, d, generator=gen).to(torch.bfloat16)
+    ref = torch.zeros(T, d)
+    for t in range(T):
+        acc = torch.zeros(d)
+        for j in sorted(range(k), key=lambda j: int(topi[t, j])):
+            if inv[t, j] >= 0:
+                acc = acc + yperm[int(inv[t, j])].float() * topw[t, j]
+        ref[t] = acc
+    out = torch.empty(T, d, dtype=torch.bfloat16, device=DEV)
+    yd, ti, tw, iv = yperm.to(DEV), topi.to(DEV), topw.to(DEV), inv.to(DEV)
+    rc = lib.smaul_moe_combine(yd.data_ptr(), 1, ti.data_ptr(), tw.data_ptr(), iv.data_ptr(), out.data_ptr(),
+                               T, d, k, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "moe_combine")
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), ref.to(torch.bfloat16))
+
+
 def test_moe_deterministic_and_empty():
     x, gw, gb, experts = make_moe(77, 700, 256, 640, 8, 2)
     a = gpu_moe(x, gw, gb, experts, 2)
