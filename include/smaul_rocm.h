@@ -124,11 +124,9 @@ int smaul_moe_dispatch(const int64_t* topi, const float* topw, int32_t* counts,
  * max_tiles is an upper bound on tile_off[E] (ceil(T*k/block_m) + E).
  * block_m 16 (chosen for T <= 64, bf16, tile 64, d and h multiples of 128)
  * selects the decode-regime kernels, which stream each expert's weights once
- * for all of its rows.  block_m 256 (bf16, tile 64, at least 256 rows per
- * expert on average) selects the LDS-DMA kernels, which need
- * SMAUL_FLAG_ALIGNED_CODES and 16-byte aligned activations; a caller that
- * cannot promise that passes 128 instead, to the dispatch and both GEMMs
- * (smaul_moe_forward does this itself).
+ * for all of its rows.  block_m 128 with bf16 activations, tile 64,
+ * SMAUL_FLAG_ALIGNED_CODES and 16-byte aligned activations selects the
+ * LDS-DMA kernels (the register-staged ones otherwise, on the same tiles).
  */
 int smaul_moe_block_m(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile,
                       int act_dtype);

@@ -629,7 +629,7 @@ struct DmaGemmCfg {
 };
 
 template <int BM, int BN, int WM, int WN, int NSTAGE, bool SWIGLU, bool CANON, bool REMAP>
-__global__ void __launch_bounds__(WM * WN * 64, (WM * WN) / 4)
+__global__ void __launch_bounds__(WM * WN * 64, 2)
 fp8_gemm_dma_kernel(GemmArgs p) {
   using C = DmaGemmCfg<BM, BN, WM, WN, NSTAGE, SWIGLU>;
   constexpr int NW = C::NW, BNO = C::BNO, TM = C::TM, TN = C::TN, TNO = C::TNO, FM = C::FM, FN = C::FN,
@@ -2626,8 +2626,6 @@ constexpr int DECODE_BM = 16;
 
 bool decode_shape_ok(int64_t d, int64_t h, int64_t tile) { return tile == 64 && d % 128 == 0 && h % 128 == 0; }
 
-// block_m 256 selects the LDS-DMA grouped GEMMs (fp8_gemm_dma_kernel).
-constexpr int DMA_BM = 256;
 bool dma_gemm_enabled();
 
 int pick_block_m(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile, int act_dtype) {
@@ -2635,13 +2633,8 @@ int pick_block_m(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t 
   // rows per expert on average; small segments use the 32-row tile
   const int64_t avg = (T * k + E - 1) / (E > 0 ? E : 1);
   if (avg < 96) return CfgSmall::BM;
-  // LDS-DMA kernels: bf16, 64-wide scale tiles, d a multiple of the down
-  // GEMM's 256 output columns, h of the gate/up GEMM's 128, segments long
-  // enough for 256-row tiles, and activation offsets within 31 bits
-  const int64_t rows_bound = T * k + E * DMA_BM;
-  if (act_dtype == SMAUL_DTYPE_BF16 && tile == 64 && avg >= DMA_BM && d % 256 == 0 && h % 128 == 0 &&
-      rows_bound * (d > h ? d : h) * 2 < ((int64_t)1 << 31) && dma_gemm_enabled())
-    return DMA_BM;
+  // 128-row tiles: the LDS-DMA kernels where they apply (moe_gemm decides),
+  // else the register-staged ones
   return act_dtype == SMAUL_DTYPE_BF16 ? CfgBig::BM : CfgBigF32::BM;
 }
 
@@ -2674,11 +2667,14 @@ int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 // LDS-DMA grouped GEMM shapes: (BM rows, BN staged weight columns, wave
 // grid, pipeline depth).  8 waves (2 per SIMD) and a 3-deep pipeline use
 // 147 KB of LDS: one workgroup per CU.
-struct CfgDmaGU {  // gate+up with the SwiGLU epilogue: 256 rows x 128 outputs
-  static constexpr int BM = 256, BN = 256, WM = 4, WN = 2, NSTAGE = 3;
+// 128-row tiles of 4 waves (each 128 rows x 64 staged columns) with two
+// stage buffers: 68 KB of LDS, so two workgroups share a CU and one's
+// prologue and epilogue overlap the other's main loop.
+struct CfgDmaGU {  // gate+up with the SwiGLU epilogue: 128 rows x 128 outputs
+  static constexpr int BM = 128, BN = 256, WM = 1, WN = 4, NSTAGE = 2;
 };
-struct CfgDmaDown {  // down projection: 256 rows x 256 outputs
-  static constexpr int BM = 256, BN = 256, WM = 4, WN = 2, NSTAGE = 3;
+struct CfgDmaDown {  // down projection: 128 rows x 256 outputs
+  static constexpr int BM = 128, BN = 256, WM = 1, WN = 4, NSTAGE = 2;
 };
 
 template <class CF, bool SWIGLU, bool CANON>
@@ -2692,7 +2688,7 @@ int launch_gemm_dma(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
   return check_launch("fp8_gemm_dma_kernel");
 }
 
-// SMAUL_GEMM=legacy makes smaul_moe_block_m never choose the LDS-DMA kernels
+// SMAUL_GEMM=legacy keeps the grouped GEMMs on the register-staged kernels
 // (for comparisons); anything else lets eligible shapes use them.
 bool dma_gemm_enabled() {
   static const bool on = [] {
@@ -2938,7 +2934,7 @@ static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* 
   if (K % 16 != 0 || !aligned16(act))
     return fail(SMAUL_ERR_UNSUPPORTED, "moe gemm: K must be a multiple of 16 and activations 16-byte aligned");
   const int64_t big_bm = act_dtype == SMAUL_DTYPE_BF16 ? CfgBig::BM : CfgBigF32::BM;
-  if (!(block_m == big_bm || block_m == CfgSmall::BM || block_m == DMA_BM ||
+  if (!(block_m == big_bm || block_m == CfgSmall::BM ||
         (block_m == DECODE_BM && act_dtype == SMAUL_DTYPE_BF16)))
     return fail(SMAUL_ERR_INVALID, "moe gemm: block_m must come from smaul_moe_block_m");
   if (!act || !w1 || !s1 || !out || !seg_off || !tile_off || (swiglu && (!w2 || !s2)))
@@ -2970,15 +2966,13 @@ static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* 
     if (swiglu) return canon ? launch_decode<true, true>(a, stream) : launch_decode<true, false>(a, stream);
     return canon ? launch_decode<false, true>(a, stream) : launch_decode<false, false>(a, stream);
   }
-  if (block_m == DMA_BM) {
-    static_assert(CfgDmaGU::BM == DMA_BM && CfgDmaDown::BM == DMA_BM, "tile_off row tiles");
-    // row indices of x (tokens, < T <= T*k) and of hdn (< T*k) are both
-    // below max_tiles * block_m
-    if (!dma_gemm_ok(a, act_dtype, flags, max_tiles * block_m, swiglu ? CfgDmaGU::BN / 2 : CfgDmaDown::BN))
-      return fail(SMAUL_ERR_INVALID,
-                  "moe gemm: block_m %d needs bf16, tile 64, K %% 64 == 0, N a multiple of %d, 16-byte aligned "
-                  "activations and code buffers (SMAUL_FLAG_ALIGNED_CODES) and offsets below 2^31",
-                  DMA_BM, swiglu ? CfgDmaGU::BN / 2 : CfgDmaDown::BN);
+  // 128-row tiles: the LDS-DMA kernels when the activations are bf16, the
+  // codes promised 16-byte aligned and the shapes fit them (row indices of
+  // x and of hdn are both below max_tiles * block_m); the register-staged
+  // kernels otherwise, on the same tile table
+  static_assert(CfgDmaGU::BM == CfgBig::BM && CfgDmaDown::BM == CfgBig::BM, "one tile table for both kernels");
+  if (block_m == big_bm && dma_gemm_enabled() &&
+      dma_gemm_ok(a, act_dtype, flags, max_tiles * block_m, swiglu ? CfgDmaGU::BN / 2 : CfgDmaDown::BN)) {
     if (swiglu)
       return canon ? launch_gemm_dma<CfgDmaGU, true, true>(a, max_tiles, stream)
                    : launch_gemm_dma<CfgDmaGU, true, false>(a, max_tiles, stream);
@@ -3094,10 +3088,7 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
   ws += align256(R * h * el);
   void* yperm = ws;
 
-  int64_t bm = pick_block_m(T, d, h, E, k, tile, act_dtype);
-  // the LDS-DMA GEMMs need 16-byte aligned code buffers; without that promise
-  // the register-staged kernels (128-row tiles) run instead
-  if (bm == DMA_BM && (!(flags & SMAUL_FLAG_ALIGNED_CODES) || !aligned16(x))) bm = CfgBig::BM;
+  const int64_t bm = pick_block_m(T, d, h, E, k, tile, act_dtype);
   // decode regime: the gate/up kernel dispatches for itself
   const bool fused = bm == DECODE_BM && decode_stream_enabled() && aligned16(x) && h % 16 == 0 &&
                      ds_kbw(d / 64, true) != 0;

@@ -360,9 +360,9 @@ def abi_moe(x, gw, gb, experts, k, tile, flags, code_tensors=None):
     return out.cpu(), topi.cpu(), counts.cpu()
 
 
-@pytest.mark.parametrize("T,flags,block_m", [(1024, 0, 256), (1024, 2, 256), (64, 0, 16)])
+@pytest.mark.parametrize("T,flags,block_m", [(1024, 0, 128), (1024, 2, 128), (64, 0, 16)])
 def test_moe_raw_codes_any_flags(T, flags, block_m):
-    """Raw stored codes (0x7F/0xFF included, no canonical copy).  At 256-row
+    """Raw stored codes (0x7F/0xFF included, no canonical copy).  At 128-row
     tiles without SMAUL_FLAG_ALIGNED_CODES the register-staged kernels run;
     with it the LDS-DMA kernels decode 0x7F/0xFF themselves; T = 64 runs the
     decode kernels on the raw codes."""
