@@ -117,7 +117,9 @@ def cpu_baseline(x, gw, gb, experts, k, target_s=10.0):
 
 
 def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
-    """Config 4: 64 tokens through 24 independent MoE layers, one HIP graph replay per step."""
+    """Config 4: 64 tokens through 24 stacked MoE layers (independent weights, each
+    layer fed the unit-RMS-normalised output of the one before), one HIP graph
+    replay per step."""
     import torch
     dev = torch.device("cuda")
     lay = []
@@ -129,9 +131,14 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
     x0 = (x0.float() * torch.rsqrt(x0.float().pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
 
     def step():
+        # layer l + 1 reads layer l's output after a unit-RMS row norm (Block's
+        # norm around the FFN, model.py:636), so the 24 layers form one chain
         outs = []
+        xl = x0
         for gw, gb, ex in lay:
-            outs.append(be.moe_forward(x0, gw, gb, ex, k, 64))
+            o = be.moe_forward(xl, gw, gb, ex, k, 64)
+            outs.append(o)
+            xl = be.rms_norm(o[0], None, 1e-6)
         return outs
 
     eager = step()
@@ -166,7 +173,7 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
     for c in counts:
         executed = int((c > 0).sum())
         nbytes += executed * expert_bytes + 4 * E * d + 2 * T * d * 2
-    return {"workload": "C4 decode: 64 tokens x 24 MoE layers, d=1024 h=2560 E=8 top-2, HIP graph replay",
+    return {"workload": "C4 decode: 64 tokens x 24 chained MoE layers (unit-RMS norm between layers), d=1024 h=2560 E=8 top-2, HIP graph replay",
             "tokens_per_s": T / dt, "ms_per_step": dt * 1e3, "ms_per_step_eager": dt_eager * 1e3,
             "bytes_per_step": nbytes, "hbm_GBps": nbytes / dt / 1e9,
             "hbm_frac": nbytes / dt / PEAK_HBM_BPS, "graph_matches_eager": ok}

@@ -154,6 +154,17 @@ int smaul_moe_combine(const void* yperm, int act_dtype, const int64_t* topi,
                       int64_t d, int64_t k, hipStream_t stream);
 
 /*
+ * RMSNorm over the rows of x [T, d]: out = cast((x * rsqrt(mean(x^2) + eps)) *
+ * weight) computed in fp32, out in act_dtype (model.py:124-139, RMSNorm.forward;
+ * Block applies it to every MoE output, model.py:636).  weight: fp32 [d], or
+ * NULL for a weight of ones (the unit-RMS normalisation).  eps must be positive
+ * and finite (model.py:127-128).  The row sum of squares is reduced in a
+ * different order than torch's, so results agree to fp32 rounding, not bitwise.
+ */
+int smaul_rms_norm(const void* x, int act_dtype, const float* weight, void* out, int64_t T,
+                   int64_t d, float eps, hipStream_t stream);
+
+/*
  * The whole MoE layer (router -> dispatch -> gate_up -> down -> combine) in
  * one call; SwiFFN_MoE.forward of model.py:557-585.  `workspace` must hold
  * smaul_moe_workspace_size(...) bytes (256-byte aligned).  prob/topi/topw are

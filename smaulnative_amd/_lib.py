@@ -40,6 +40,7 @@ SIGNATURES = {
                                _I64, _I64, _I, _P]),
     "smaul_moe_down": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P]),
     "smaul_moe_combine": (_I, [_P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "smaul_rms_norm": (_I, [_P, _I, _P, _P, _I64, _I64, ctypes.c_float, _P]),
     "smaul_moe_workspace_size": (_I64, [_I64, _I64, _I64, _I64, _I64, _I]),
     "smaul_moe_forward": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P]),

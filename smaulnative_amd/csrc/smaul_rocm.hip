@@ -19,6 +19,7 @@
 #include <stdarg.h>
 
 #include <algorithm>
+#include <cmath>
 #include <stdlib.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -2593,6 +2594,101 @@ combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
 }
 
 // ---------------------------------------------------------------------------
+// RMSNorm over rows: out = cast((x * rsqrt(mean(x^2) + eps)) * weight), fp32
+// ---------------------------------------------------------------------------
+// One wave per row, four rows per workgroup.  VEC: 16-byte loads and stores
+// (d a multiple of the vector width, 16-byte aligned rows); the first NKEEP
+// vectors of each lane stay in registers between the reduction and the scaling
+// pass, anything past them is read again.
+template <bool BF16, bool VEC>
+__global__ void __launch_bounds__(256)
+rms_norm_kernel(const void* __restrict__ x, const float* __restrict__ weight,
+                void* __restrict__ out, int64_t T, int d, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  constexpr int ES = BF16 ? 2 : 4;   // bytes per element
+  constexpr int EPV = 16 / ES;       // elements per 16-byte vector
+  constexpr int NKEEP = 4;
+  const char* row = (const char*)x + t * (int64_t)d * ES;
+  char* orow = (char*)out + t * (int64_t)d * ES;
+  auto unpack = [](const uint4 v, float* f) {
+    if constexpr (BF16) {
+      f[0] = bf2f(v.x & 0xffff); f[1] = bf2f(v.x >> 16); f[2] = bf2f(v.y & 0xffff); f[3] = bf2f(v.y >> 16);
+      f[4] = bf2f(v.z & 0xffff); f[5] = bf2f(v.z >> 16); f[6] = bf2f(v.w & 0xffff); f[7] = bf2f(v.w >> 16);
+    } else {
+      f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
+      f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
+    }
+  };
+  float ss = 0.0f;
+  if constexpr (VEC) {
+    const int nv = d / EPV;
+    uint4 keep[NKEEP];
+#pragma unroll
+    for (int i = 0; i < NKEEP; ++i) {
+      const int v = lane + i * 64;
+      keep[i] = v < nv ? ldg16(row + v * 16) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NKEEP; ++i) {
+      float f[EPV];
+      unpack(keep[i], f);
+#pragma unroll
+      for (int q = 0; q < EPV; ++q) ss = ss + f[q] * f[q];
+    }
+    for (int v = lane + NKEEP * 64; v < nv; v += 64) {
+      float f[EPV];
+      unpack(ldg16(row + v * 16), f);
+#pragma unroll
+      for (int q = 0; q < EPV; ++q) ss = ss + f[q] * f[q];
+    }
+    ss = wave_sum(ss);
+    const float r = 1.0f / __fsqrt_rn(ss / (float)d + eps);
+    auto scale = [&](const uint4 in, int v) {
+      float f[EPV];
+      unpack(in, f);
+      const int c0 = v * EPV;
+#pragma unroll
+      for (int q = 0; q < EPV; ++q) {
+        f[q] = f[q] * r;
+        if (weight) f[q] = f[q] * ldgf(weight + c0 + q);
+      }
+      if constexpr (BF16) {
+        uint4 o;
+        o.x = f2bf(f[0]) | (f2bf(f[1]) << 16);
+        o.y = f2bf(f[2]) | (f2bf(f[3]) << 16);
+        o.z = f2bf(f[4]) | (f2bf(f[5]) << 16);
+        o.w = f2bf(f[6]) | (f2bf(f[7]) << 16);
+        *(uint4*)(orow + v * 16) = o;
+      } else {
+        *(float4*)(orow + v * 16) = make_float4(f[0], f[1], f[2], f[3]);
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < NKEEP; ++i) {
+      const int v = lane + i * 64;
+      if (v < nv) scale(keep[i], v);
+    }
+    for (int v = lane + NKEEP * 64; v < nv; v += 64) scale(ldg16(row + v * 16), v);
+  } else {
+    for (int c = lane; c < d; c += 64) {
+      const float f = BF16 ? bf2f(((const uint16_t*)row)[c]) : ((const float*)row)[c];
+      ss = ss + f * f;
+    }
+    ss = wave_sum(ss);
+    const float r = 1.0f / __fsqrt_rn(ss / (float)d + eps);
+    for (int c = lane; c < d; c += 64) {
+      float f = BF16 ? bf2f(((const uint16_t*)row)[c]) : ((const float*)row)[c];
+      f = f * r;
+      if (weight) f = f * weight[c];
+      if constexpr (BF16) ((uint16_t*)orow)[c] = (uint16_t)f2bf(f);
+      else ((float*)orow)[c] = f;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // code canonicalisation (device repack cache): 0x7F -> 0x7E, 0xFF -> 0xFE
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
@@ -3024,6 +3120,26 @@ int smaul_moe_combine(const void* yperm, int act_dtype, const int64_t* topi, con
     else hipLaunchKernelGGL((combine_kernel<false, 8>), grid, block, 0, stream, yperm, topi, topw, inv, out, T, (int)d, (int)k);
   }
   return check_launch("combine_kernel");
+}
+
+int smaul_rms_norm(const void* x, int act_dtype, const float* weight, void* out, int64_t T,
+                   int64_t d, float eps, hipStream_t stream) {
+  if (!dtype_ok(act_dtype) || T < 0 || d <= 0 || d > INT32_MAX)
+    return fail(SMAUL_ERR_INVALID, "rms_norm: bad arguments");
+  if (!(eps > 0.0f) || !std::isfinite(eps)) return fail(SMAUL_ERR_INVALID, "rms_norm: eps must be positive finite");
+  if (T == 0) return SMAUL_OK;
+  if (!x || !out) return fail(SMAUL_ERR_INVALID, "rms_norm: null pointer");
+  const bool bf = act_dtype == SMAUL_DTYPE_BF16;
+  const bool vec = aligned16(x) && aligned16(out) && d % (bf ? 8 : 4) == 0;
+  const dim3 grid((unsigned)((T + 3) / 4)), block(256);
+  if (bf) {
+    if (vec) hipLaunchKernelGGL((rms_norm_kernel<true, true>), grid, block, 0, stream, x, weight, out, T, (int)d, eps);
+    else hipLaunchKernelGGL((rms_norm_kernel<true, false>), grid, block, 0, stream, x, weight, out, T, (int)d, eps);
+  } else {
+    if (vec) hipLaunchKernelGGL((rms_norm_kernel<false, true>), grid, block, 0, stream, x, weight, out, T, (int)d, eps);
+    else hipLaunchKernelGGL((rms_norm_kernel<false, false>), grid, block, 0, stream, x, weight, out, T, (int)d, eps);
+  }
+  return check_launch("rms_norm_kernel");
 }
 
 // Workspace layout (each piece 256-byte aligned):

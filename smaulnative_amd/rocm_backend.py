@@ -23,6 +23,7 @@ Behaviour differences from the reference CPU backend, all deliberate:
 from __future__ import annotations
 
 import os
+import math
 import threading
 from typing import Sequence
 
@@ -335,6 +336,34 @@ class RocmBackend:
         disp["hdn"] = hdn
         disp["yperm"] = yperm
         return out, prob, topi, topw, disp
+
+    def rms_norm(self, x, weight=None, eps=1e-6):
+        """RMSNorm.forward (model.py:124-139) over the last dim, on the device.
+
+        x: [..., d] bf16 or fp32; weight: [d] (None = ones, the unit-RMS norm).
+        Returns a new tensor of x's dtype and shape.
+        """
+        lib = _lib.load()
+        _need_device("rms_norm", x, weight)
+        if x.dtype not in _ACT:
+            raise RuntimeError(f"rms_norm: x must be float32 or bfloat16, got {x.dtype}")
+        if not math.isfinite(eps) or eps <= 0:
+            raise ValueError(f"RMSNorm eps must be positive finite, got {eps!r}")
+        d = x.shape[-1]
+        x2 = x.reshape(-1, d)
+        x2 = x2 if x2.is_contiguous() else x2.contiguous()
+        w = None
+        if weight is not None:
+            if weight.numel() != d:
+                raise RuntimeError(f"rms_norm: weight must have {d} elements, got {weight.numel()}")
+            w = weight.detach().reshape(d)
+            w = w if (w.dtype == torch.float32 and w.is_contiguous()) else w.float().contiguous()
+        out = torch.empty_like(x2)
+        with torch.cuda.device(x.device):
+            rc = lib.smaul_rms_norm(x2.data_ptr(), _ACT[x.dtype], None if w is None else w.data_ptr(),
+                                    out.data_ptr(), x2.shape[0], d, eps, _stream_handle(x.device))
+        _lib.check(rc, "rms_norm")
+        return out.reshape(x.shape)
 
     def moe_forward(self, x, gate_w, gate_b, experts, top_k, tile):
         """SwiFFN_MoE.forward on the device.

@@ -464,3 +464,42 @@ def test_swiffn_moe_module_on_device():
     st = moe.routing_stats()
     assert sum(st["token_counts"]) == 2 * 50 * 2
     assert rel_l2(y.cpu().float(), ref.out.float()) < 2e-3
+
+
+@pytest.mark.parametrize("T,d,dtype,weighted", [
+    (64, 1024, torch.bfloat16, False),   # the C4 inter-layer norm
+    (37, 1000, torch.bfloat16, True),    # 16-byte vectors, ragged last vector per lane
+    (5, 1001, torch.bfloat16, False),    # d not a multiple of 8: element path
+    (3, 4100, torch.float32, True),      # past the vectors kept in registers
+    (2, 8192, torch.bfloat16, True),
+    (0, 512, torch.bfloat16, False),
+])
+def test_rms_norm(T, d, dtype, weighted):
+    """RMSNorm.forward (model.py:131-139): (x * rsqrt(mean(x^2) + eps)) * weight
+    in fp32, cast to x's dtype.  The row sum is reduced in another order than
+    torch's, so bf16 outputs may differ by one ulp on rounding ties and fp32
+    outputs by a few ulp."""
+    print(f"case rms_norm T={T} d={d} {dtype} weighted={weighted}", flush=True)
+    gen = torch.Generator().manual_seed(T * 7919 + d)
+    x = (torch.randn(T, d, generator=gen) * 3.0).to(dtype)
+    w = (1.0 + 0.1 * torch.randn(d, generator=gen)) if weighted else None
+    eps = 1e-6
+    xf = x.float()
+    ref = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    if w is not None:
+        ref = ref * w
+    got = be().rms_norm(x.to(DEV), None if w is None else w.to(DEV), eps).cpu()
+    assert got.dtype == dtype and got.shape == x.shape
+    if T == 0:
+        return
+    if dtype == torch.bfloat16:
+        exact = ref.to(torch.bfloat16)
+        mism = (got != exact)
+        assert float(mism.float().mean()) < 0.01
+        # a mismatch is one bf16 ulp: the fp32 results sit next to a rounding boundary
+        ulp = (exact.float().abs() * 2.0 ** -7).clamp_min(2.0 ** -133)
+        assert bool(((got.float() - exact.float()).abs() <= ulp * 1.0001).all())
+    else:
+        assert rel_max(got, ref) < 4e-6
+    with pytest.raises(ValueError):
+        be().rms_norm(x.to(DEV), None, 0.0)
