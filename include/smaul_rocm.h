@@ -184,6 +184,24 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
                       int flags, hipStream_t stream);
 
 /*
+ * smaul_moe_forward followed by RMSNorm of its output rows, the norm Block
+ * applies to every FFN output (model.py:636, RMSNorm.forward model.py:124-139):
+ * out as smaul_moe_forward writes it, and norm_out [T, d] (act_dtype) =
+ * smaul_rms_norm(out, norm_w, eps), bit for bit.  With d % 16 == 0 and
+ * d <= 4096 the norm is fused into the combine kernel (one wave per token);
+ * otherwise the two kernels run one after the other.
+ */
+int smaul_moe_forward_norm(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
+                           const uint8_t* const* gate_w8, const float* const* gate_s,
+                           const uint8_t* const* up_w8, const float* const* up_s,
+                           const uint8_t* const* down_w8, const float* const* down_s,
+                           void* out, float* prob, int64_t* topi, float* topw, int32_t* counts,
+                           void* workspace, int64_t workspace_bytes,
+                           int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile,
+                           int flags, const float* norm_w, float eps, void* norm_out,
+                           hipStream_t stream);
+
+/*
  * Host-side self-test of the top-k selection order used by the router (no GPU
  * involved): writes the k indices the router would select for `vals` [n].
  * Exposed only so the CPU test suite can check the order against torch.topk.

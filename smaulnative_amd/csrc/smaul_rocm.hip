@@ -2596,10 +2596,67 @@ combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
 // ---------------------------------------------------------------------------
 // RMSNorm over rows: out = cast((x * rsqrt(mean(x^2) + eps)) * weight), fp32
 // ---------------------------------------------------------------------------
-// One wave per row, four rows per workgroup.  VEC: 16-byte loads and stores
-// (d a multiple of the vector width, 16-byte aligned rows); the first NKEEP
-// vectors of each lane stay in registers between the reduction and the scaling
-// pass, anything past them is read again.
+// One wave per row, four rows per workgroup.  VEC (d a multiple of 16,
+// 16-byte aligned rows): lane l owns the 16-column chunks l, l+64, ...; the row
+// sum of squares adds each chunk left to right, the chunks in order, then the
+// lanes by butterfly (rms_chunk_sumsq, wave_sum).  combine_norm_kernel sums in
+// exactly this order, so the fused MoE output norm and this kernel agree
+// bitwise.  The first RMS_KEEP chunks of a lane stay in registers between the
+// reduction and the scaling pass; chunks past them are read again.
+constexpr int RMS_KEEP = 4;
+
+__device__ __forceinline__ float rms_chunk_sumsq(float ss, const float (&f)[16]) {
+#pragma unroll
+  for (int q = 0; q < 16; ++q) ss = ss + f[q] * f[q];
+  return ss;
+}
+
+// 16 values (bf16 or fp32) from VPC 16-byte vectors
+template <bool BF16>
+__device__ __forceinline__ void rms_unpack(const uint4* v, float (&f)[16]) {
+  if constexpr (BF16) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      f[j * 8 + 0] = bf2f(v[j].x & 0xffff); f[j * 8 + 1] = bf2f(v[j].x >> 16);
+      f[j * 8 + 2] = bf2f(v[j].y & 0xffff); f[j * 8 + 3] = bf2f(v[j].y >> 16);
+      f[j * 8 + 4] = bf2f(v[j].z & 0xffff); f[j * 8 + 5] = bf2f(v[j].z >> 16);
+      f[j * 8 + 6] = bf2f(v[j].w & 0xffff); f[j * 8 + 7] = bf2f(v[j].w >> 16);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f[j * 4 + 0] = __uint_as_float(v[j].x); f[j * 4 + 1] = __uint_as_float(v[j].y);
+      f[j * 4 + 2] = __uint_as_float(v[j].z); f[j * 4 + 3] = __uint_as_float(v[j].w);
+    }
+  }
+}
+
+// (f * r) * weight for 16 columns from c0, cast and stored at dst
+template <bool BF16>
+__device__ __forceinline__ void rms_scale_store(const float (&f)[16], float r, const float* weight, int c0,
+                                                char* dst) {
+  float o[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    o[q] = f[q] * r;
+    if (weight) o[q] = o[q] * ldgf(weight + c0 + q);
+  }
+  if constexpr (BF16) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uint4 w;
+      w.x = f2bf(o[j * 8 + 0]) | (f2bf(o[j * 8 + 1]) << 16);
+      w.y = f2bf(o[j * 8 + 2]) | (f2bf(o[j * 8 + 3]) << 16);
+      w.z = f2bf(o[j * 8 + 4]) | (f2bf(o[j * 8 + 5]) << 16);
+      w.w = f2bf(o[j * 8 + 6]) | (f2bf(o[j * 8 + 7]) << 16);
+      ((uint4*)dst)[j] = w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ((float4*)dst)[j] = make_float4(o[j * 4], o[j * 4 + 1], o[j * 4 + 2], o[j * 4 + 3]);
+  }
+}
+
 template <bool BF16, bool VEC>
 __global__ void __launch_bounds__(256)
 rms_norm_kernel(const void* __restrict__ x, const float* __restrict__ weight,
@@ -2608,69 +2665,52 @@ rms_norm_kernel(const void* __restrict__ x, const float* __restrict__ weight,
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   constexpr int ES = BF16 ? 2 : 4;   // bytes per element
-  constexpr int EPV = 16 / ES;       // elements per 16-byte vector
-  constexpr int NKEEP = 4;
   const char* row = (const char*)x + t * (int64_t)d * ES;
   char* orow = (char*)out + t * (int64_t)d * ES;
-  auto unpack = [](const uint4 v, float* f) {
-    if constexpr (BF16) {
-      f[0] = bf2f(v.x & 0xffff); f[1] = bf2f(v.x >> 16); f[2] = bf2f(v.y & 0xffff); f[3] = bf2f(v.y >> 16);
-      f[4] = bf2f(v.z & 0xffff); f[5] = bf2f(v.z >> 16); f[6] = bf2f(v.w & 0xffff); f[7] = bf2f(v.w >> 16);
-    } else {
-      f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
-      f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
-    }
-  };
   float ss = 0.0f;
   if constexpr (VEC) {
-    const int nv = d / EPV;
-    uint4 keep[NKEEP];
+    constexpr int VPC = BF16 ? 2 : 4;  // 16-byte vectors per 16-column chunk
+    const int nch = d / 16;
+    uint4 keep[RMS_KEEP][VPC];
 #pragma unroll
-    for (int i = 0; i < NKEEP; ++i) {
-      const int v = lane + i * 64;
-      keep[i] = v < nv ? ldg16(row + v * 16) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < RMS_KEEP; ++i) {
+      const int c = lane + i * 64;
+#pragma unroll
+      for (int v = 0; v < VPC; ++v) keep[i][v] = c < nch ? ldg16(row + c * 16 * ES + v * 16) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < NKEEP; ++i) {
-      float f[EPV];
-      unpack(keep[i], f);
-#pragma unroll
-      for (int q = 0; q < EPV; ++q) ss = ss + f[q] * f[q];
+    for (int i = 0; i < RMS_KEEP; ++i) {
+      float f[16];
+      rms_unpack<BF16>(keep[i], f);
+      ss = rms_chunk_sumsq(ss, f);
     }
-    for (int v = lane + NKEEP * 64; v < nv; v += 64) {
-      float f[EPV];
-      unpack(ldg16(row + v * 16), f);
+    for (int c = lane + RMS_KEEP * 64; c < nch; c += 64) {
+      uint4 v[VPC];
 #pragma unroll
-      for (int q = 0; q < EPV; ++q) ss = ss + f[q] * f[q];
+      for (int j = 0; j < VPC; ++j) v[j] = ldg16(row + c * 16 * ES + j * 16);
+      float f[16];
+      rms_unpack<BF16>(v, f);
+      ss = rms_chunk_sumsq(ss, f);
     }
     ss = wave_sum(ss);
     const float r = 1.0f / __fsqrt_rn(ss / (float)d + eps);
-    auto scale = [&](const uint4 in, int v) {
-      float f[EPV];
-      unpack(in, f);
-      const int c0 = v * EPV;
 #pragma unroll
-      for (int q = 0; q < EPV; ++q) {
-        f[q] = f[q] * r;
-        if (weight) f[q] = f[q] * ldgf(weight + c0 + q);
+    for (int i = 0; i < RMS_KEEP; ++i) {
+      const int c = lane + i * 64;
+      if (c < nch) {
+        float f[16];
+        rms_unpack<BF16>(keep[i], f);
+        rms_scale_store<BF16>(f, r, weight, c * 16, orow + c * 16 * ES);
       }
-      if constexpr (BF16) {
-        uint4 o;
-        o.x = f2bf(f[0]) | (f2bf(f[1]) << 16);
-        o.y = f2bf(f[2]) | (f2bf(f[3]) << 16);
-        o.z = f2bf(f[4]) | (f2bf(f[5]) << 16);
-        o.w = f2bf(f[6]) | (f2bf(f[7]) << 16);
-        *(uint4*)(orow + v * 16) = o;
-      } else {
-        *(float4*)(orow + v * 16) = make_float4(f[0], f[1], f[2], f[3]);
-      }
-    };
-#pragma unroll
-    for (int i = 0; i < NKEEP; ++i) {
-      const int v = lane + i * 64;
-      if (v < nv) scale(keep[i], v);
     }
-    for (int v = lane + NKEEP * 64; v < nv; v += 64) scale(ldg16(row + v * 16), v);
+    for (int c = lane + RMS_KEEP * 64; c < nch; c += 64) {
+      uint4 v[VPC];
+#pragma unroll
+      for (int j = 0; j < VPC; ++j) v[j] = ldg16(row + c * 16 * ES + j * 16);
+      float f[16];
+      rms_unpack<BF16>(v, f);
+      rms_scale_store<BF16>(f, r, weight, c * 16, orow + c * 16 * ES);
+    }
   } else {
     for (int c = lane; c < d; c += 64) {
       const float f = BF16 ? bf2f(((const uint16_t*)row)[c]) : ((const float*)row)[c];
@@ -2685,6 +2725,105 @@ rms_norm_kernel(const void* __restrict__ x, const float* __restrict__ weight,
       if constexpr (BF16) ((uint16_t*)orow)[c] = (uint16_t)f2bf(f);
       else ((float*)orow)[c] = f;
     }
+  }
+}
+
+// Combine followed by RMSNorm of each output row (Block's norm of the MoE
+// output, model.py:636, 124-139), one wave per token: lane l owns the
+// 16-column chunks l, l+64, ... (NCH of them, d <= NCH*1024).  Each chunk is
+// combined exactly as combine_kernel does (ascending expert order, fp32 sum
+// from +0 of rounded products), written to out, and its rounded values enter
+// the row sum of squares in rms_norm_kernel's order; then norm_out = cast((v *
+// r) * weight).  Chunks are combined one after another, every slot row load of
+// a chunk in flight together.
+template <bool BF16, int NCH>
+__global__ void __launch_bounds__(256)
+combine_norm_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
+                    const float* __restrict__ topw, const int32_t* __restrict__ inv,
+                    void* __restrict__ out, const float* __restrict__ weight, float eps,
+                    void* __restrict__ norm_out, int64_t T, int d, int k) {
+  static_assert(NCH >= 1 && NCH <= RMS_KEEP, "chunks per lane");
+  constexpr int ES = BF16 ? 2 : 4;
+  constexpr int VPC = BF16 ? 2 : 4;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int nch = d / 16;
+  int ex[8];
+  int rw[8];
+  float wt[8];
+  int n = 0;
+  for (int j = 0; j < k; ++j) {
+    const int pos = inv[t * k + j];
+    if (pos < 0) continue;
+    const int ee = (int)topi[t * k + j];
+    int q = n++;
+    while (q > 0 && ex[q - 1] > ee) {
+      ex[q] = ex[q - 1];
+      rw[q] = rw[q - 1];
+      wt[q] = wt[q - 1];
+      --q;
+    }
+    ex[q] = ee;
+    rw[q] = pos;
+    wt[q] = topw[t * k + j];
+  }
+  float v[NCH][16];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = lane + i * 64;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v[i][q] = 0.0f;
+    if (c < nch) {
+      uint4 yv[8][VPC];
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        if (s < n) {
+          const char* src = (const char*)yperm + ((int64_t)rw[s] * d + c * 16) * ES;
+#pragma unroll
+          for (int j = 0; j < VPC; ++j) yv[s][j] = ldg16(src + j * 16);
+        }
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        if (s < n) {
+          float y[16];
+          rms_unpack<BF16>(yv[s], y);
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            const float pr = y[q] * wt[s];  // rounded product (library built with -ffp-contract=off)
+            v[i][q] = v[i][q] + pr;
+          }
+        }
+      // the row as stored in out (cast to the activation dtype)
+      char* dst = (char*)out + (t * d + c * 16) * ES;
+      if constexpr (BF16) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) v[i][q] = bf2f(f2bf(v[i][q]));
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          uint4 w;
+          w.x = f2bf(v[i][j * 8 + 0]) | (f2bf(v[i][j * 8 + 1]) << 16);
+          w.y = f2bf(v[i][j * 8 + 2]) | (f2bf(v[i][j * 8 + 3]) << 16);
+          w.z = f2bf(v[i][j * 8 + 4]) | (f2bf(v[i][j * 8 + 5]) << 16);
+          w.w = f2bf(v[i][j * 8 + 6]) | (f2bf(v[i][j * 8 + 7]) << 16);
+          ((uint4*)dst)[j] = w;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          ((float4*)dst)[j] = make_float4(v[i][j * 4], v[i][j * 4 + 1], v[i][j * 4 + 2], v[i][j * 4 + 3]);
+      }
+    }
+    ss = rms_chunk_sumsq(ss, v[i]);
+  }
+  // rms_norm_kernel also adds RMS_KEEP - NCH all-zero chunks here: +0 changes nothing
+  ss = wave_sum(ss);
+  const float r = 1.0f / __fsqrt_rn(ss / (float)d + eps);
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = lane + i * 64;
+    if (c < nch) rms_scale_store<BF16>(v[i], r, weight, c * 16, (char*)norm_out + (t * d + c * 16) * ES);
   }
 }
 
@@ -3130,7 +3269,7 @@ int smaul_rms_norm(const void* x, int act_dtype, const float* weight, void* out,
   if (T == 0) return SMAUL_OK;
   if (!x || !out) return fail(SMAUL_ERR_INVALID, "rms_norm: null pointer");
   const bool bf = act_dtype == SMAUL_DTYPE_BF16;
-  const bool vec = aligned16(x) && aligned16(out) && d % (bf ? 8 : 4) == 0;
+  const bool vec = aligned16(x) && aligned16(out) && d % 16 == 0;
   const dim3 grid((unsigned)((T + 3) / 4)), block(256);
   if (bf) {
     if (vec) hipLaunchKernelGGL((rms_norm_kernel<true, true>), grid, block, 0, stream, x, weight, out, T, (int)d, eps);
@@ -3165,13 +3304,43 @@ int64_t smaul_moe_workspace_size(int64_t T, int64_t d, int64_t h, int64_t E, int
   return n;
 }
 
-int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
-                      const uint8_t* const* gate_w8, const float* const* gate_s,
-                      const uint8_t* const* up_w8, const float* const* up_s,
-                      const uint8_t* const* down_w8, const float* const* down_s, void* out,
-                      float* prob, int64_t* topi, float* topw, int32_t* counts, void* workspace,
-                      int64_t workspace_bytes, int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
-                      int64_t tile, int flags, hipStream_t stream) {
+// The RMSNorm that follows the MoE output (smaul_moe_forward_norm)
+struct OutNorm {
+  const float* weight;
+  float eps;
+  void* out;
+};
+
+// The last stage of the layer: the combine, or the combine and the output
+// norm (fused when d % 16 == 0 and d <= 4096, else the two kernels).
+static int finish_combine(const void* yperm, int act_dtype, const int64_t* topi, const float* topw,
+                          const int32_t* inv, void* out, int64_t T, int64_t d, int64_t k, const OutNorm* nrm,
+                          hipStream_t stream) {
+  if (!nrm) return smaul_moe_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, stream);
+  if (d % 16 == 0 && d <= 64 * 16 * RMS_KEEP && aligned16(yperm) && aligned16(out) && aligned16(nrm->out)) {
+    const int nch = (int)((d + 1023) / 1024);
+    const dim3 grid((unsigned)((T + 3) / 4)), block(256);
+    const bool bf = act_dtype == SMAUL_DTYPE_BF16;
+#define SMAUL_CN(BF, N) hipLaunchKernelGGL((combine_norm_kernel<BF, N>), grid, block, 0, stream, yperm, topi, topw, \
+                                           inv, out, nrm->weight, nrm->eps, nrm->out, T, (int)d, (int)k)
+    if (nch == 1) { if (bf) SMAUL_CN(true, 1); else SMAUL_CN(false, 1); }
+    else if (nch == 2) { if (bf) SMAUL_CN(true, 2); else SMAUL_CN(false, 2); }
+    else { if (bf) SMAUL_CN(true, 4); else SMAUL_CN(false, 4); }
+#undef SMAUL_CN
+    return check_launch("combine_norm_kernel");
+  }
+  const int rc = smaul_moe_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, stream);
+  if (rc) return rc;
+  return smaul_rms_norm(out, act_dtype, nrm->weight, nrm->out, T, d, nrm->eps, stream);
+}
+
+static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
+                            const uint8_t* const* gate_w8, const float* const* gate_s,
+                            const uint8_t* const* up_w8, const float* const* up_s,
+                            const uint8_t* const* down_w8, const float* const* down_s, void* out,
+                            float* prob, int64_t* topi, float* topw, int32_t* counts, void* workspace,
+                            int64_t workspace_bytes, int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
+                            int64_t tile, int flags, const OutNorm* nrm, hipStream_t stream) {
   const int64_t need = smaul_moe_workspace_size(T, d, h, E, k, act_dtype);
   if (need < 0) return fail(SMAUL_ERR_INVALID, "moe_forward: bad sizes");
   if (workspace_bytes < need)
@@ -3255,7 +3424,7 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
     rc = smaul_moe_down(hdn, act_dtype, down_w8, down_s, yperm, seg_off, tile_off, max_tiles, E, d, h, tile,
                         bm, flags, stream);
     if (rc) return rc;
-    return smaul_moe_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, stream);
+    return finish_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, nrm, stream);
   }
   if (nb > 1 && T <= 64) {  // one wave dispatches straight from topi/topw
     hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(64), 0, stream, topi, topw, od, T, (int)E, (int)k);
@@ -3272,7 +3441,34 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
   rc = smaul_moe_down(hdn, act_dtype, down_w8, down_s, yperm, seg_off, tile_off, max_tiles, E, d, h, tile,
                       bm, flags, stream);
   if (rc) return rc;
-  return smaul_moe_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, stream);
+  return finish_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, nrm, stream);
+}
+
+int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
+                      const uint8_t* const* gate_w8, const float* const* gate_s,
+                      const uint8_t* const* up_w8, const float* const* up_s,
+                      const uint8_t* const* down_w8, const float* const* down_s, void* out,
+                      float* prob, int64_t* topi, float* topw, int32_t* counts, void* workspace,
+                      int64_t workspace_bytes, int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
+                      int64_t tile, int flags, hipStream_t stream) {
+  return moe_forward_impl(x, act_dtype, gate_w, gate_b, gate_w8, gate_s, up_w8, up_s, down_w8, down_s, out, prob,
+                          topi, topw, counts, workspace, workspace_bytes, T, d, h, E, k, tile, flags, nullptr,
+                          stream);
+}
+
+int smaul_moe_forward_norm(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
+                           const uint8_t* const* gate_w8, const float* const* gate_s,
+                           const uint8_t* const* up_w8, const float* const* up_s,
+                           const uint8_t* const* down_w8, const float* const* down_s, void* out,
+                           float* prob, int64_t* topi, float* topw, int32_t* counts, void* workspace,
+                           int64_t workspace_bytes, int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
+                           int64_t tile, int flags, const float* norm_w, float eps, void* norm_out,
+                           hipStream_t stream) {
+  if (!(eps > 0.0f) || !std::isfinite(eps)) return fail(SMAUL_ERR_INVALID, "moe_forward_norm: eps must be positive finite");
+  if (T > 0 && !norm_out) return fail(SMAUL_ERR_INVALID, "moe_forward_norm: null norm_out");
+  const OutNorm nrm{norm_w, eps, norm_out};
+  return moe_forward_impl(x, act_dtype, gate_w, gate_b, gate_w8, gate_s, up_w8, up_s, down_w8, down_s, out, prob,
+                          topi, topw, counts, workspace, workspace_bytes, T, d, h, E, k, tile, flags, &nrm, stream);
 }
 
 int smaul_fp8_canonicalize(const uint8_t* codes, uint8_t* out, int64_t n, hipStream_t stream) {

@@ -373,6 +373,18 @@ class RocmBackend:
         Returns (out [..., d] x.dtype, prob [..., E] fp32, topi [..., k] int64,
         counts [E] int32 on the device).
         """
+        return self._moe_forward(x, gate_w, gate_b, experts, top_k, tile, None)
+
+    def moe_forward_norm(self, x, gate_w, gate_b, experts, top_k, tile, norm_weight=None, eps=1e-6):
+        """moe_forward followed by RMSNorm of its output (Block's norm of the
+        FFN output, model.py:636), fused into the combine where the shape
+        allows.  Returns moe_forward's tuple plus the normalised output, which
+        equals rms_norm(out, norm_weight, eps) bit for bit."""
+        if not math.isfinite(eps) or eps <= 0:
+            raise ValueError(f"RMSNorm eps must be positive finite, got {eps!r}")
+        return self._moe_forward(x, gate_w, gate_b, experts, top_k, tile, (norm_weight, eps))
+
+    def _moe_forward(self, x, gate_w, gate_b, experts, top_k, tile, norm):
         lib = _lib.load()
         _need_device("moe_forward", x, gate_w)
         if x.dtype not in _ACT:
@@ -405,6 +417,14 @@ class RocmBackend:
         # the dispatch kernel writes every count; no fill, so the call can be graph-captured
         counts = torch.empty(E, dtype=torch.int32, device=dev) if T > 0 else \
             torch.zeros(E, dtype=torch.int32, device=dev)
+        normed = nw = None
+        if norm is not None:
+            normed = torch.empty_like(x2)
+            if norm[0] is not None:
+                if norm[0].numel() != d:
+                    raise RuntimeError(f"moe_forward_norm: weight must have {d} elements, got {norm[0].numel()}")
+                nw = norm[0].detach().reshape(d)
+                nw = nw if (nw.dtype == torch.float32 and nw.is_contiguous()) else nw.float().contiguous()
         if T > 0:
             ws_bytes = lib.smaul_moe_workspace_size(T, d, h, E, top_k, act)
             if ws_bytes < 0:
@@ -412,13 +432,18 @@ class RocmBackend:
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
             tp = table.data_ptr()
             row = E * 8
-            with torch.cuda.device(dev):
-                rc = lib.smaul_moe_forward(
-                    x2.data_ptr(), act, gw.data_ptr(), None if gb is None else gb.data_ptr(),
+            args = [x2.data_ptr(), act, gw.data_ptr(), None if gb is None else gb.data_ptr(),
                     tp, tp + row, tp + 2 * row, tp + 3 * row, tp + 4 * row, tp + 5 * row,
                     out.data_ptr(), prob.data_ptr(), topi.data_ptr(), topw.data_ptr(),
                     counts.data_ptr(), ws.data_ptr(), ws_bytes, T, d, h, E, top_k, tile,
-                    _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES, _stream_handle(dev))
+                    _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES]
+            with torch.cuda.device(dev):
+                if norm is None:
+                    rc = lib.smaul_moe_forward(*args, _stream_handle(dev))
+                else:
+                    rc = lib.smaul_moe_forward_norm(*args, None if nw is None else nw.data_ptr(), norm[1],
+                                                    normed.data_ptr(), _stream_handle(dev))
             _lib.check(rc, "moe_forward")
         lead = x.shape[:-1]
-        return (out.reshape(*lead, d), prob.reshape(*lead, E), topi.reshape(*lead, top_k), counts)
+        res = (out.reshape(*lead, d), prob.reshape(*lead, E), topi.reshape(*lead, top_k), counts)
+        return res if norm is None else res + (normed.reshape(*lead, d),)

@@ -503,3 +503,34 @@ def test_rms_norm(T, d, dtype, weighted):
         assert rel_max(got, ref) < 4e-6
     with pytest.raises(ValueError):
         be().rms_norm(x.to(DEV), None, 0.0)
+
+
+@pytest.mark.parametrize("T,d,h,E,k,dtype,weighted", [
+    (64, 1024, 2560, 8, 2, torch.bfloat16, False),  # C4 layer: self-routed decode, fused norm
+    (40, 2048, 256, 4, 2, torch.bfloat16, True),    # two chunks per lane
+    (300, 256, 640, 8, 2, torch.bfloat16, True),    # prefill path
+    (33, 192, 320, 4, 3, torch.float32, False),     # fp32 activations
+    (5, 4160, 128, 4, 2, torch.bfloat16, True),     # d > 4096: combine, then the norm kernel
+])
+def test_moe_forward_norm(T, d, h, E, k, dtype, weighted):
+    """moe_forward_norm returns moe_forward's outputs unchanged plus
+    rms_norm(out, weight, eps) bit for bit (the fused combine+norm sums the
+    squares in rms_norm_kernel's order)."""
+    print(f"case moe_forward_norm T={T} d={d} h={h} E={E} k={k} {dtype} weighted={weighted}", flush=True)
+    x, gw, gb, experts = make_moe(T * 31 + d, T, d, h, E, k, dtype=dtype)
+    gen = torch.Generator().manual_seed(d)
+    w = (1.0 + 0.1 * torch.randn(d, generator=gen)).to(DEV) if weighted else None
+    dx, dgw, dgb, dex = x.to(DEV), gw.to(DEV), gb.to(DEV), to_dev_experts(experts)
+    ref = be().moe_forward(dx, dgw, dgb, dex, k, 64)
+    got = be().moe_forward_norm(dx, dgw, dgb, dex, k, 64, w, 1e-6)
+    normed = be().rms_norm(ref[0], w, 1e-6)
+    torch.cuda.synchronize()
+    for a, b in zip(ref, got[:4]):
+        assert torch.equal(a.cpu(), b.cpu())
+    assert torch.equal(got[4].cpu(), normed.cpu())
+    # and the norm itself against the fp32 formula
+    xf = ref[0].float().cpu()
+    r = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+    if w is not None:
+        r = r * w.cpu()
+    assert rel_max(got[4].float(), r) < (8e-3 if dtype == torch.bfloat16 else 4e-6)
