@@ -1265,8 +1265,8 @@ __device__ __forceinline__ void dispatch_one_wave(const int* ti, const float* tw
   }
 }
 
-// ---- router building blocks (shared by router_kernel and the decode gate/up
-// kernel that routes for itself; the same code gives the same bits) ---------
+// ---- router building blocks (router_kernel; route_select also backs the
+// tie fallback of the MFMA router) -------------------------------------------
 
 // Router columns per LDS chunk and the lane's 8-column groups per chunk.
 template <int EMAX>
@@ -1478,14 +1478,14 @@ __device__ __forceinline__ void route_select(const float* lg, smaul_topk::Pair* 
 // has at most 8 significant bits), so every product x * wi of a bf16
 // activation is exact in fp32 and v_mfma_f32_16x16x32_bf16 sums them in fp32:
 // the logits carry fp32 accumulation error only, as a scalar fmaf chain does.
-// A pass covers 64 tokens (four MFMA N-tiles of 16) and up to 16 experts (the
-// M rows; rows past E are zero).  K is cut into RK_SLICES fixed slices of
-// KSW 32-wide k-steps; a wave computes whole slices (each with all four token
-// tiles, the three weight terms in separate accumulators) and leaves one
-// partial per (slice, token, expert) in LDS; the logit is the sum of the
-// slices in slice order plus the bias.  Nothing depends on the number of
-// waves, so router_mfma_kernel and the decode gate/up kernel produce the same
-// bits.  The weight terms are made in registers from the lane's own fp32
+// A pass covers 64 tokens (four MFMA N-tiles of 16; one tile, 16 tokens, in
+// the decode step's blocks) and up to 16 experts (the M rows; rows past E are
+// zero).  K is cut into RK_SLICES fixed slices of KSW 32-wide k-steps; a wave
+// computes whole slices (each with all of the block's token tiles, the three
+// weight terms in separate accumulators) and leaves one partial per (slice,
+// token, expert) in LDS; the logit is the sum of the slices in slice order
+// plus the bias.  Nothing depends on the number of waves or on the tokens
+// per block, so every launch shape produces the same bits for a token.  The weight terms are made in registers from the lane's own fp32
 // weights (no LDS staging).
 constexpr int RK_SLICES = 8;
 constexpr int RK_TOK = 64;
@@ -1498,12 +1498,13 @@ __device__ __forceinline__ uint32_t bf16_rne(float f) {
 
 // One K slice of the logits: load() issues every activation and weight load
 // of the slice, compute() waits for them, runs the MFMAs and writes the
-// partials part[(slice * 64 + token) * 16 + expert].  Split so that a caller
+// partials part[(slice * TOK + token) * 16 + expert].  Split so that a caller
 // can issue other loads in between that compute() does not wait for.
 // d <= RK_SLICES * 32 * KSW columns.
-template <int KSW>
+template <int KSW, int NTT = 4>
 struct RouteSlice {
-  uint4 xr[4][KSW];
+  static constexpr int TOK = NTT * 16;  // tokens of the block
+  uint4 xr[NTT][KSW];
   float4 wr[KSW][2];
   int slice;
 
@@ -1519,7 +1520,7 @@ struct RouteSlice {
       const int c = (slice * KSW + i) * 32 + 8 * g;
       const int cc = c < d ? c : 0;  // d % 8 == 0: a group is all in or all out
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
+      for (int tt = 0; tt < NTT; ++tt) {
         const int64_t t = t0 + tt * 16 + n < T ? t0 + tt * 16 + n : T - 1;  // computed, never written
         xr[tt][i] = ldg16(x + t * d + cc);
       }
@@ -1536,13 +1537,13 @@ struct RouteSlice {
       const int c = (slice * KSW + i) * 32 + 8 * g;
       if (c >= d) {
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) xr[tt][i] = make_uint4(0u, 0u, 0u, 0u);
+        for (int tt = 0; tt < NTT; ++tt) xr[tt][i] = make_uint4(0u, 0u, 0u, 0u);
       }
       if (c >= d || n >= E) wr[i][0] = wr[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    f32x4_t acc[4][3];
+    f32x4_t acc[NTT][3];
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
+    for (int tt = 0; tt < NTT; ++tt)
 #pragma unroll
       for (int term = 0; term < 3; ++term) acc[tt][term] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1565,7 +1566,7 @@ struct RouteSlice {
       a[2] = __builtin_bit_cast(bf16x8_t, make_uint4(q2[0] | (q2[1] << 16), q2[2] | (q2[3] << 16),
                                                      q2[4] | (q2[5] << 16), q2[6] | (q2[7] << 16)));
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
+      for (int tt = 0; tt < NTT; ++tt)
 #pragma unroll
         for (int term = 0; term < 3; ++term)
           acc[tt][term] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[term], __builtin_bit_cast(bf16x8_t, xr[tt][i]),
@@ -1573,25 +1574,25 @@ struct RouteSlice {
     }
     // lane holds experts 4g + r of token tt*16 + n
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
+    for (int tt = 0; tt < NTT; ++tt)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        part[(slice * RK_TOK + tt * 16 + n) * 16 + 4 * g + r] = (acc[tt][0][r] + acc[tt][1][r]) + acc[tt][2][r];
+        part[(slice * TOK + tt * 16 + n) * 16 + 4 * g + r] = (acc[tt][0][r] + acc[tt][1][r]) + acc[tt][2][r];
   }
 };
 
 // The sum over slices, in slice order, plus the bias: slog[token][e] for
 // e < E, tokens t0.. below T.  Follows the barrier after the partials; ends
 // with a barrier.
-template <int EMAX>
+template <int EMAX, int TOK = RK_TOK>
 __device__ __forceinline__ void route_reduce(const float* gb, int E, int64_t T, int64_t t0, int nw,
                                              const float* part, float (*slog)[EMAX]) {
-  for (int q = threadIdx.x; q < RK_TOK * EMAX; q += nw * 64) {
+  for (int q = threadIdx.x; q < TOK * EMAX; q += nw * 64) {
     const int tok = q / EMAX, e = q - tok * EMAX;
     if (e < E && t0 + tok < T) {
       float v = part[tok * 16 + e];
 #pragma unroll
-      for (int sl = 1; sl < RK_SLICES; ++sl) v += part[(sl * RK_TOK + tok) * 16 + e];
+      for (int sl = 1; sl < RK_SLICES; ++sl) v += part[(sl * TOK + tok) * 16 + e];
       slog[tok][e] = gb ? v + gb[e] : v;
     }
   }
@@ -1601,17 +1602,17 @@ __device__ __forceinline__ void route_reduce(const float* gb, int E, int64_t T, 
 // Logits of tokens t0 .. t0+63 (rows past T: not written) into slog[token][e]
 // for e < E <= EMAX <= 16, by nw waves of this workgroup (all must call it).
 // part: RK_PART_FLOATS of LDS.  Ends with a barrier.
-template <int KSW, int EMAX>
+template <int KSW, int EMAX, int NTT>
 __device__ __forceinline__ void route_logits(const uint16_t* x, const float* gw, const float* gb, int E, int64_t T,
                                              int64_t t0, int d, int nw, float* part, float (*slog)[EMAX]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int sl = wave; sl < RK_SLICES; sl += nw) {
-    RouteSlice<KSW> rs;
+    RouteSlice<KSW, NTT> rs;
     rs.load(x, gw, E, T, t0, d, sl, lane);
     rs.compute(E, d, lane, part);
   }
   __syncthreads();
-  route_reduce<EMAX>(gb, E, T, t0, nw, part, slog);
+  route_reduce<EMAX, NTT * 16>(gb, E, T, t0, nw, part, slog);
 }
 
 // the k-steps per slice for model width d (0: too wide for the MFMA router)
@@ -2002,45 +2003,30 @@ __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, con
 
 // Inputs of the dispatch that the gate/up kernel performs itself (FUSED):
 // the router's top-k ids and weights of T <= 64 tokens, and where workgroup 0
-// writes the dispatch for the later stages.  With ROUTE the kernel also
-// routes: gw/gb are the router weight and bias, and workgroup 0 writes
-// prob/topi/topw through o.
+// writes the dispatch for the later stages.
 struct DsDispatch {
   const int64_t* topi;
   const float* topw;
   RouteOut o;
   int T, k;
-  const float* gw;
-  const float* gb;
-  int ksw;  // route_ksw(d)
 };
-
-// Expert register width of the routing inside the decode gate/up kernel
-// (E <= 8; waves 0..3 own 16 tokens each).
-constexpr int DS_RT_E = 8;
 
 // FUSED (gate/up only): every workgroup ranks the T <= 64 tokens per expert
 // itself into LDS (one wave, ballot ranks in token order, the same rule as
 // dispatch_one_wave) instead of reading a dispatch written by an earlier
 // kernel; workgroup 0 also writes that dispatch (counts, seg_off, tile_off,
-// perm_row, perm_w, inv) for the down projection and the combine.  ROUTE: the
-// top-k comes from the router's own building blocks run in every workgroup
-// (route_mfma, 16 tokens per wave), bit for bit what router_mfma_kernel
-// computes; otherwise it is read from dd.topi/dd.topw.
-template <bool SWIGLU, bool CANON, int KBW, bool FUSED, bool ROUTE>
+// perm_row, perm_w, inv) for the down projection and the combine.  The
+// top-k is read from dd.topi/dd.topw (the router kernel's output).
+template <bool SWIGLU, bool CANON, int KBW, bool FUSED>
 __global__ void __launch_bounds__(DS_WMAX * 64)
 decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
   constexpr int NH = SWIGLU ? 2 : 1;
   static_assert(!FUSED || SWIGLU, "the fused dispatch feeds the gate/up projection");
-  static_assert(!ROUTE || FUSED, "routing feeds the fused dispatch");
-  // the partial sums of the GEMM; with ROUTE also the routing scratch before it
+  // the partial sums of the GEMM
   constexpr int RED_FLOATS = 2 * DS_WMAX * NH * (DS_ROWS / 16) * 256;
-  constexpr int RT_FLOATS = RK_PART_FLOATS + 64 * DS_RT_E + 64 * DS_RT_E * 2;
-  __shared__ __attribute__((aligned(16))) float red[ROUTE && RT_FLOATS > RED_FLOATS ? RT_FLOATS : RED_FLOATS];
+  __shared__ __attribute__((aligned(16))) float red[RED_FLOATS];
   __shared__ int32_t s_perm[FUSED ? 64 * 8 : 1];
   __shared__ int32_t s_off[FUSED ? MAX_E + 1 : 1];
-  __shared__ int s_ti[ROUTE ? 64 : 1][8];
-  __shared__ float s_tw[ROUTE ? 64 : 1][8];
   const int lane = threadIdx.x & 63;
   const int ctn = (int)(p.N >> 4);
   const int64_t kb0 = (int64_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * KBW;
@@ -2050,30 +2036,6 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
   DsSegs sg;
   if constexpr (FUSED) {
     ds_pointers(p, lane, sg);
-    // With ROUTE, the wave's router loads go out first (waves 0..7 own the
-    // eight K slices; nw == 8 is required), then the ring below, so the
-    // routing waits for its own data only.
-    RouteSlice<4> rs;
-    if constexpr (ROUTE) rs.load((const uint16_t*)p.x, dd.gw, p.E, dd.T, 0, (int)p.K, (int)(threadIdx.x >> 6), lane);
-    if constexpr (ROUTE) {
-      // red is free until the GEMM: the logit partials, the logits [64][8]
-      // and the tie scratch [64][8] live in it
-      constexpr int EM = DS_RT_E;
-      static_assert(RT_FLOATS * 4 <= (int)sizeof(red), "routing scratch must fit");
-      float* part = red;
-      float(*slog)[EM] = (float(*)[EM])(red + RK_PART_FLOATS);
-      smaul_topk::Pair(*spair)[EM] = (smaul_topk::Pair(*)[EM])(red + RK_PART_FLOATS + 64 * EM);
-      static_assert(RK_SLICES == DS_WMAX, "one router slice per wave");
-      rs.compute(p.E, (int)p.K, lane, part);
-      __syncthreads();
-      route_reduce<EM>(dd.gb, p.E, dd.T, 0, nw, part, slog);
-      // EM lanes per token, as in router_mfma_kernel
-      constexpr int TPW = 64 / EM;
-      for (int tl = (int)(threadIdx.x >> 6) * TPW + lane / EM; tl < 64; tl += nw * TPW)
-        route_select_group<EM>(slog[tl], spair[tl], p.E, dd.k, tl, tl < dd.T, dd.o, blockIdx.x == 0, s_ti[tl],
-                               s_tw[tl], nullptr);
-      __syncthreads();
-    }
     if (threadIdx.x < 64) {
       const bool valid = lane < dd.T;
       int ti[8];
@@ -2081,14 +2043,9 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         if (j < dd.k) {
-          if constexpr (ROUTE) {
-            ti[j] = valid ? s_ti[lane][j] : -1;
-            tw[j] = valid ? s_tw[lane][j] : 0.0f;
-          } else {
-            const int64_t v = valid ? dd.topi[lane * dd.k + j] : -1;
-            ti[j] = (v >= 0 && v < p.E) ? (int)v : -1;
-            tw[j] = valid ? dd.topw[lane * dd.k + j] : 0.0f;
-          }
+          const int64_t v = valid ? dd.topi[lane * dd.k + j] : -1;
+          ti[j] = (v >= 0 && v < p.E) ? (int)v : -1;
+          tw[j] = valid ? dd.topw[lane * dd.k + j] : 0.0f;
         }
       const uint64_t sel = valid ? selection_of(ti, tw, p.E, dd.k) : 0ull;
       const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
@@ -2115,21 +2072,6 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
   // two row tiles when any segment has more than 16 rows
   if (__ballot(sg.rows > 16) != 0) ds_body<SWIGLU, CANON, KBW, 2>(p, sg, ridx, u0, u1, ctn, red, nw, ring, prefetched);
   else ds_body<SWIGLU, CANON, KBW, 1>(p, sg, ridx, u0, u1, ctn, red, nw, ring, prefetched);
-}
-
-// The decode gate/up kernel routes for itself when E <= 8, d <= 1024 (4
-// k-steps per router slice) and it has 8 waves (one router slice each).
-// SMAUL_DECODE_ROUTE=0 keeps the router a kernel of its own (A/B timing)
-bool ds_route_enabled() {
-  static const bool on = [] {
-    const char* v = getenv("SMAUL_DECODE_ROUTE");
-    return !(v && strcmp(v, "0") == 0);
-  }();
-  return on;
-}
-
-bool ds_route_ok(int64_t E, int64_t d, int64_t T, int64_t nw) {
-  return ds_route_enabled() && E <= DS_RT_E && route_ksw(d) == 4 && nw == RK_SLICES && T >= 1 && T <= 64;
 }
 
 // K blocks per wave of the streaming decode kernel for K/64 = nkb blocks
@@ -2186,19 +2128,14 @@ int launch_decode_stream(const GemmArgs& a, const DsDispatch* dd, hipStream_t st
   const dim3 grid((unsigned)g), block(nw * 64);
   if constexpr (SWIGLU) {
     if (dd) {
-      if (dd->gw) {
-        if (!ds_route_ok(a.E, a.K, dd->T, nw)) return fail(SMAUL_ERR_INVALID, "decode gate/up: routing shape");
-        hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true, true>), grid, block, 0, stream, a, nw, *dd);
-      } else {
-        hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true, false>), grid, block, 0, stream, a, nw, *dd);
-      }
+      hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true>), grid, block, 0, stream, a, nw, *dd);
       return check_launch("decode_stream_kernel");
     }
   }
   if (kbw == 2) {
-    hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 2, false, false>), grid, block, 0, stream, a, nw, none);
+    hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 2, false>), grid, block, 0, stream, a, nw, none);
   } else {
-    if constexpr (!SWIGLU) hipLaunchKernelGGL((decode_stream_kernel<false, CANON, 5, false, false>), grid, block, 0, stream, a, nw, none);
+    if constexpr (!SWIGLU) hipLaunchKernelGGL((decode_stream_kernel<false, CANON, 5, false>), grid, block, 0, stream, a, nw, none);
   }
   return check_launch("decode_stream_kernel");
 }
@@ -2331,15 +2268,18 @@ router_kernel(const void* __restrict__ x, const float* __restrict__ gw, const fl
 constexpr int ROUTE_MFMA_TPB = RK_TOK;
 constexpr int ROUTE_MFMA_THREADS = 512;
 
-template <int EMAX, bool EXACT, int KSW>
+// NTT token tiles of 16 per block: 4 (ROUTE_MFMA_TPB tokens) in general, 1
+// for the decode step, where a block per 16 tokens shortens each block's
+// loads; the arithmetic per token is the same either way.
+template <int EMAX, bool EXACT, int KSW, int NTT>
 __global__ void __launch_bounds__(ROUTE_MFMA_THREADS)
 router_mfma_kernel(const uint16_t* __restrict__ x, const float* __restrict__ gw, const float* __restrict__ gb,
                    RouteOut o, int64_t T, int d, int E_arg, int k) {
   static_assert(EMAX <= 16, "the MFMA router covers up to 16 experts");
   const int E = EXACT ? EMAX : E_arg;
-  constexpr int TPB = ROUTE_MFMA_TPB;
+  constexpr int TPB = NTT * 16;
   constexpr int NWAVES = ROUTE_MFMA_THREADS / 64;
-  __shared__ __attribute__((aligned(16))) float part[RK_PART_FLOATS];
+  __shared__ __attribute__((aligned(16))) float part[RK_SLICES * TPB * 16];
   __shared__ float slog[TPB][EMAX];
   __shared__ smaul_topk::Pair spair[TPB][EMAX];
   __shared__ int s_ti[TPB][8];
@@ -2348,7 +2288,7 @@ router_mfma_kernel(const uint16_t* __restrict__ x, const float* __restrict__ gw,
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t0 = (int64_t)blockIdx.x * TPB;
   if (tid < EMAX) s_cnt[tid] = 0;
-  route_logits<KSW, EMAX>(x, gw, gb, E, T, t0, d, NWAVES, part, slog);
+  route_logits<KSW, EMAX, NTT>(x, gw, gb, E, T, t0, d, NWAVES, part, slog);
 
   {
     // EMAX lanes per token
@@ -3012,6 +2952,38 @@ static int route_tpb(int64_t E, int64_t d, int x_dtype) {
   return route_mfma_ok(E, d, x_dtype) ? ROUTE_MFMA_TPB : route_tb(E) * ROUTE_WAVES;
 }
 
+// The decode router (T <= 64, bf16, the MFMA router's shapes): one block per
+// 16 tokens, top-k only (no dispatch).
+static int launch_router_small(const void* x, const float* gate_w, const float* gate_b, const RouteOut& o,
+                               int64_t T, int64_t d, int64_t E, int64_t k, hipStream_t stream) {
+  const uint16_t* xb = (const uint16_t*)x;
+  const dim3 grid((unsigned)((T + 15) / 16)), block(ROUTE_MFMA_THREADS);
+  const int ksw = route_ksw(d);
+#define SMAUL_ROUTE_S2(EMAX, EXACT)                                                                            \
+  if (ksw == 4)                                                                                                \
+    hipLaunchKernelGGL((router_mfma_kernel<EMAX, EXACT, 4, 1>), grid, block, 0, stream, xb, gate_w, gate_b, o, T, \
+                       (int)d, (int)E, (int)k);                                                                \
+  else                                                                                                         \
+    hipLaunchKernelGGL((router_mfma_kernel<EMAX, EXACT, 8, 1>), grid, block, 0, stream, xb, gate_w, gate_b, o, T, \
+                       (int)d, (int)E, (int)k);
+#define SMAUL_ROUTE_S(EMAX)     \
+  if (E == EMAX) {              \
+    SMAUL_ROUTE_S2(EMAX, true)  \
+  } else {                      \
+    SMAUL_ROUTE_S2(EMAX, false) \
+  }
+  if (E <= 4) {
+    SMAUL_ROUTE_S(4)
+  } else if (E <= 8) {
+    SMAUL_ROUTE_S(8)
+  } else {
+    SMAUL_ROUTE_S(16)
+  }
+#undef SMAUL_ROUTE_S
+#undef SMAUL_ROUTE_S2
+  return check_launch("router_mfma_kernel");
+}
+
 static int launch_router(const void* x, int x_dtype, const float* gate_w, const float* gate_b,
                          const RouteOut& o, int64_t T, int64_t d, int64_t E, int64_t k,
                          hipStream_t stream) {
@@ -3025,10 +2997,10 @@ static int launch_router(const void* x, int x_dtype, const float* gate_w, const 
     const int ksw = route_ksw(d);
 #define SMAUL_ROUTE_M2(EMAX, EXACT)                                                                          \
   if (ksw == 4)                                                                                              \
-    hipLaunchKernelGGL((router_mfma_kernel<EMAX, EXACT, 4>), grid, block, 0, stream, xb, gate_w, gate_b, o, T, \
+    hipLaunchKernelGGL((router_mfma_kernel<EMAX, EXACT, 4, 4>), grid, block, 0, stream, xb, gate_w, gate_b, o, T, \
                        (int)d, (int)E, (int)k);                                                              \
   else                                                                                                       \
-    hipLaunchKernelGGL((router_mfma_kernel<EMAX, EXACT, 8>), grid, block, 0, stream, xb, gate_w, gate_b, o, T, \
+    hipLaunchKernelGGL((router_mfma_kernel<EMAX, EXACT, 8, 4>), grid, block, 0, stream, xb, gate_w, gate_b, o, T, \
                        (int)d, (int)E, (int)k);
 #define SMAUL_ROUTE_M(EMAX)     \
   if (E == EMAX) {              \
@@ -3391,13 +3363,15 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
   od.perm_w = perm_w;
   od.inv = inv;
   if (nb == 1 && !fused) o = od;  // one router block: it dispatches too
-  // ... and at E == 8 it also routes (no router launch)
-  const bool self_routed =
-      fused && act_dtype == SMAUL_DTYPE_BF16 && ds_route_ok(E, d, T, (d / 64) / ds_kbw(d / 64, true));
-  if (!self_routed) {
+  if (fused && route_mfma_ok(E, d, act_dtype)) {
+    // decode: top-k only, one block per 16 tokens; the gate/up kernel dispatches
+    RouteOut ot = o;
+    ot.blockcnt = nullptr;
+    rc = launch_router_small(x, gate_w, gate_b, ot, T, d, E, k, stream);
+  } else {
     rc = launch_router(x, act_dtype, gate_w, gate_b, o, T, d, E, k, stream);
-    if (rc) return rc;
   }
+  if (rc) return rc;
   const int64_t max_tiles = (R + bm - 1) / bm + E;
   if (fused) {
     GemmArgs a{};
@@ -3416,8 +3390,7 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
     a.seg_off = seg_off;
     a.tile_off = tile_off;
     a.E = (int)E;
-    const DsDispatch dd{topi, topw, od, (int)T, (int)k, self_routed ? gate_w : nullptr,
-                        self_routed ? gate_b : nullptr, route_ksw(d)};
+    const DsDispatch dd{topi, topw, od, (int)T, (int)k};
     rc = (flags & SMAUL_FLAG_CANONICAL_CODES) ? launch_decode_stream<true, true>(a, &dd, stream)
                                               : launch_decode_stream<true, false>(a, &dd, stream);
     if (rc) return rc;

@@ -506,7 +506,7 @@ def test_rms_norm(T, d, dtype, weighted):
 
 
 @pytest.mark.parametrize("T,d,h,E,k,dtype,weighted", [
-    (64, 1024, 2560, 8, 2, torch.bfloat16, False),  # C4 layer: self-routed decode, fused norm
+    (64, 1024, 2560, 8, 2, torch.bfloat16, False),  # C4 layer: decode path, fused norm
     (40, 2048, 256, 4, 2, torch.bfloat16, True),    # two chunks per lane
     (300, 256, 640, 8, 2, torch.bfloat16, True),    # prefill path
     (33, 192, 320, 4, 3, torch.float32, False),     # fp32 activations
