@@ -1,17 +1,26 @@
 // libsmaul_rocm.so -- tiled-FP8 MoE forward for MI355X (gfx950 / CDNA4).
 //
 // Kernels:
-//   fp8_gemm_kernel   grouped (or dense) GEMM over E4M3 codes + per-tile fp32
-//                     scales.  bf16 MFMA (v_mfma_f32_16x16x32_bf16); codes are
-//                     decoded to bf16 once per workgroup while staging to LDS
-//                     (v_cvt_scalef32_pk_bf16_fp8); each output keeps an fp32
-//                     partial per scale tile and adds scale * partial when the
-//                     tile ends, which is exact algebra of
-//                     sum_k x[k] * lut[w[k]] * s[k / tile]  (fp8_cpu.cpp:49-98).
-//                     Optional SwiGLU epilogue (gate and up in one workgroup).
-//   router_kernel     fp32 router GEMV + softmax + top-k + renormalisation.
-//   dispatch_kernel   deterministic per-expert token order (ballot ranks).
-//   combine_kernel    weighted un-permute in ascending expert order.
+//   fp8_gemm_dma_kernel  prefill grouped GEMM (bf16 activations, tile 64):
+//                     128x256 tiles, A rows / E4M3 codes / scales copied to LDS
+//                     by DMA, codes decoded to bf16 in registers
+//                     (v_cvt_scalef32_pk_bf16_fp8), v_mfma_f32_32x32x16_bf16,
+//                     scale * partial added per 64-wide K tile
+//                     (sum_k x[k] * lut[w[k]] * s[k / tile], fp8_cpu.cpp:49-98),
+//                     optional SwiGLU epilogue.
+//   fp8_gemm_kernel   the register-staged grouped / dense GEMM for everything
+//                     else (fp32 activations, tiles 32 and 128*m, short segments).
+//   decode_stream_kernel  T <= 64: units of (segment, 16 columns) streamed
+//                     through a register ring, K split across the waves; the
+//                     gate/up instance dispatches for itself.
+//   decode_gemm_kernel    split-K decode GEMM for shapes the ring cannot take.
+//   router_mfma_kernel    bf16 router logits on the matrix cores (exact three-
+//                     term weight split) + softmax + top-k + renormalisation;
+//   router_kernel     the fp32 router for the other shapes.
+//   dispatch kernels  deterministic per-expert token order (ballot ranks).
+//   combine_kernel    weighted un-permute in ascending expert order;
+//   combine_norm_kernel  the same followed by RMSNorm of each row.
+//   rms_norm_kernel   RMSNorm over rows.
 //
 // Host-side entry points are the extern "C" functions declared in
 // include/smaul_rocm.h.  Nothing here allocates device memory or synchronises.
@@ -1839,12 +1848,10 @@ struct DsRing {
 };
 
 // ridx: logical row -> activation row (SwiGLU only; down reads its rows in
-// place).  prefetched: the ring already holds units u0 .. u0+DS_D-1 (clamped
-// to u1-1).
+// place).
 template <bool SWIGLU, bool CANON, int KBW, int NRT>
 __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, const int32_t* ridx, int u0,
-                                        int u1, int ctn, float* red, int nw, DsRing<SWIGLU, KBW>& ring,
-                                        bool prefetched) {
+                                        int u1, int ctn, float* red, int nw) {
   constexpr int NH = SWIGLU ? 2 : 1;
   const int lane = threadIdx.x & 63;
   const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1852,6 +1859,7 @@ __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, con
   const int64_t kb0 = (int64_t)ks * KBW;
   const f32x4_t z4 = {0.f, 0.f, 0.f, 0.f};
   const int last = u1 - 1;
+  DsRing<SWIGLU, KBW> ring;
 
   // the segment's activation rows, this wave's K slice
   uint4 a0[NRT][KBW], a1[NRT][KBW];
@@ -1887,13 +1895,11 @@ __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, con
   };
 
   // the first unit's codes go out first, then its rows, then the rest of the ring
-  if (!prefetched) ring.fetch(p, sg, ctn, kb0, kq, lane, 0, u0);
+  ring.fetch(p, sg, ctn, kb0, kq, lane, 0, u0);
   int cur_j = u0 / ctn;
   load_a(cur_j);
-  if (!prefetched) {
 #pragma unroll
-    for (int i = 1; i < DS_D; ++i) ring.fetch(p, sg, ctn, kb0, kq, lane, i, min(u0 + i, last));
-  }
+  for (int i = 1; i < DS_D; ++i) ring.fetch(p, sg, ctn, kb0, kq, lane, i, min(u0 + i, last));
 
   const int nthr = nw * 64;
   const int per_buf = nw * NH * NRT * 256;
@@ -2029,10 +2035,6 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
   __shared__ int32_t s_off[FUSED ? MAX_E + 1 : 1];
   const int lane = threadIdx.x & 63;
   const int ctn = (int)(p.N >> 4);
-  const int64_t kb0 = (int64_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * KBW;
-  const int kq = (lane >> 4) * 16;
-  DsRing<SWIGLU, KBW> ring;
-  const bool prefetched = false;
   DsSegs sg;
   if constexpr (FUSED) {
     ds_pointers(p, lane, sg);
@@ -2070,8 +2072,8 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
   const int u1 = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
   if (u0 >= u1) return;  // uniform per workgroup
   // two row tiles when any segment has more than 16 rows
-  if (__ballot(sg.rows > 16) != 0) ds_body<SWIGLU, CANON, KBW, 2>(p, sg, ridx, u0, u1, ctn, red, nw, ring, prefetched);
-  else ds_body<SWIGLU, CANON, KBW, 1>(p, sg, ridx, u0, u1, ctn, red, nw, ring, prefetched);
+  if (__ballot(sg.rows > 16) != 0) ds_body<SWIGLU, CANON, KBW, 2>(p, sg, ridx, u0, u1, ctn, red, nw);
+  else ds_body<SWIGLU, CANON, KBW, 1>(p, sg, ridx, u0, u1, ctn, red, nw);
 }
 
 // K blocks per wave of the streaming decode kernel for K/64 = nkb blocks
