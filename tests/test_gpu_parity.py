@@ -303,8 +303,10 @@ def test_moe_skewed_segments():
 
 @pytest.mark.parametrize("T,d,h", [(900, 512, 1280), (64, 1024, 2560), (5, 256, 640)])
 def test_staged_call_equals_fused_call(T, d, h):
-    """The five stage entries and the single-call layer give identical bits
-    (at decode sizes the single call's gate/up kernel dispatches for itself)."""
+    """The five stage entries and the single-call layer give identical bits.
+    At decode sizes the single call routes with one router block per 16 tokens
+    (the stage entry uses 64-token blocks) and its gate/up kernel dispatches
+    for itself, so this also checks that neither changes a bit."""
     print(f"case staged T={T} d={d} h={h}", flush=True)
     x, gw, gb, experts = make_moe(91, T, d, h, 8, 2)
     b = be()
