@@ -50,6 +50,15 @@ def test_library_validates_without_touching_the_gpu():
     rc = lib.smaul_moe_router(None, 1, None, None, None, None, None, 8, 64, 65, 2, None)
     assert rc == _lib.SMAUL_ERR_INVALID
     assert lib.smaul_moe_workspace_size(16384, 1024, 2560, 8, 2, 1) > 2 * 32768 * 2560
+    # RMSNorm: eps must be positive and finite (model.py:127-128), dtype known
+    rc = lib.smaul_rms_norm(None, 1, None, None, 4, 64, 0.0, None)
+    assert rc == _lib.SMAUL_ERR_INVALID and "eps" in _lib.last_error()
+    rc = lib.smaul_rms_norm(None, 7, None, None, 4, 64, 1e-6, None)
+    assert rc == _lib.SMAUL_ERR_INVALID
+    assert lib.smaul_rms_norm(None, 1, None, None, 0, 64, 1e-6, None) == _lib.SMAUL_OK  # nothing to do
+    rc = lib.smaul_moe_forward_norm(None, 1, None, None, None, None, None, None, None, None, None, None, None,
+                                    None, None, None, 0, 64, 64, 128, 8, 2, 64, 0, None, float("nan"), None, None)
+    assert rc == _lib.SMAUL_ERR_INVALID and "eps" in _lib.last_error()
 
 
 def _host_topk(vals, k):
