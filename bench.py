@@ -130,19 +130,26 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
                      device=dev).to(torch.bfloat16)
     x0 = (x0.float() * torch.rsqrt(x0.float().pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
 
-    def step():
+    def step(chained=True):
         # layer l + 1 reads layer l's output after a unit-RMS row norm (Block's
-        # norm around the FFN, model.py:636), so the 24 layers form one chain
+        # norm around the FFN, model.py:636), so the 24 layers form one chain;
+        # chained: layer l + 1's router runs inside layer l's combine + norm
         outs = []
         xl = x0
-        for gw, gb, ex in lay:
-            o = be.moe_forward_norm(xl, gw, gb, ex, k, 64, None, 1e-6)
+        routing = None
+        for l, (gw, gb, ex) in enumerate(lay):
+            nr = (lay[l + 1][0], lay[l + 1][1], k) if chained and l + 1 < layers else None
+            o = be.moe_forward_norm(xl, gw, gb, ex, k, 64, None, 1e-6, routing=routing, next_router=nr)
             outs.append(o)
             xl = o[4]
+            routing = o[5] if nr is not None else None
         return outs
 
     eager = step()
+    plain = step(False)
     torch.cuda.synchronize()
+    chain_ok = all(torch.equal(a[0], b[0]) and torch.equal(a[4], b[4]) for a, b in zip(eager, plain))
+    del plain
     counts = [o[3].cpu() for o in eager]
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
@@ -173,10 +180,13 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
     for c in counts:
         executed = int((c > 0).sum())
         nbytes += executed * expert_bytes + 4 * E * d + 2 * T * d * 2
-    return {"workload": "C4 decode: 64 tokens x 24 chained MoE layers (unit-RMS norm between layers), d=1024 h=2560 E=8 top-2, HIP graph replay",
+    return {"workload": "C4 decode: 64 tokens x 24 chained MoE layers (unit-RMS norm between layers, each "
+                        "layer's router fused into the previous layer's combine + norm), d=1024 h=2560 E=8 "
+                        "top-2, HIP graph replay",
             "tokens_per_s": T / dt, "ms_per_step": dt * 1e3, "ms_per_step_eager": dt_eager * 1e3,
             "bytes_per_step": nbytes, "hbm_GBps": nbytes / dt / 1e9,
-            "hbm_frac": nbytes / dt / PEAK_HBM_BPS, "graph_matches_eager": ok}
+            "hbm_frac": nbytes / dt / PEAK_HBM_BPS, "graph_matches_eager": ok,
+            "chain_matches_unfused": chain_ok}
 
 
 def read_traffic():

@@ -202,6 +202,35 @@ int smaul_moe_forward_norm(const void* x, int act_dtype, const float* gate_w, co
                            hipStream_t stream);
 
 /*
+ * One layer of a chain of MoE layers (the decode step of a stack of Blocks,
+ * model.py:636 feeding the next layer's router, model.py:558-570):
+ * smaul_moe_forward_norm, plus two ways to move routing across the boundary.
+ *   routed != 0: prob/topi/topw are INPUTS holding this layer's routing of x
+ *     (as smaul_moe_router writes it, e.g. the previous call's next_*); the
+ *     layer runs no router of its own.
+ *   next_gate_w != NULL: after the norm, norm_out is routed with
+ *     next_gate_w [next_E, d] / next_gate_b (may be NULL) and top next_k
+ *     into next_prob [T, next_E], next_topi / next_topw [T, next_k], equal
+ *     bit for bit to smaul_moe_router(norm_out, ...).  For bf16, next_E <= 16
+ *     and d <= 2048 (d % 16 == 0) the router runs inside the combine + norm
+ *     kernel; otherwise it is launched after it.
+ * out, norm_out, counts and (when not routed) prob/topi/topw are written as
+ * by smaul_moe_forward_norm.  No counterpart entry in the reference: its
+ * layers run the norm and the next router as separate calls.
+ */
+int smaul_moe_forward_chain(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
+                            const uint8_t* const* gate_w8, const float* const* gate_s,
+                            const uint8_t* const* up_w8, const float* const* up_s,
+                            const uint8_t* const* down_w8, const float* const* down_s,
+                            void* out, float* prob, int64_t* topi, float* topw, int32_t* counts,
+                            void* workspace, int64_t workspace_bytes,
+                            int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile,
+                            int flags, const float* norm_w, float eps, void* norm_out, int routed,
+                            const float* next_gate_w, const float* next_gate_b, int64_t next_E,
+                            int64_t next_k, float* next_prob, int64_t* next_topi, float* next_topw,
+                            hipStream_t stream);
+
+/*
  * Host-side self-test of the top-k selection order used by the router (no GPU
  * involved): writes the k indices the router would select for `vals` [n].
  * Exposed only so the CPU test suite can check the order against torch.topk.

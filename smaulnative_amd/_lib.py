@@ -46,6 +46,9 @@ SIGNATURES = {
                                _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P]),
     "smaul_moe_forward_norm": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                     _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, ctypes.c_float, _P, _P]),
+    "smaul_moe_forward_chain": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                     _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, ctypes.c_float, _P, _I,
+                                     _P, _P, _I64, _I64, _P, _P, _P, _P]),
     "smaul_selftest_topk": (_I, [_P, _I64, _I64, _P]),
 }
 

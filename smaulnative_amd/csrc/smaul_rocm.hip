@@ -19,7 +19,9 @@
 //   router_kernel     the fp32 router for the other shapes.
 //   dispatch kernels  deterministic per-expert token order (ballot ranks).
 //   combine_kernel    weighted un-permute in ascending expert order;
-//   combine_norm_kernel  the same followed by RMSNorm of each row.
+//   combine_norm_kernel  the same followed by RMSNorm of each row;
+//   combine_norm_route_kernel  and then the next layer's router on the
+//                     normed rows (a chain of layers).
 //   rms_norm_kernel   RMSNorm over rows.
 //
 // Host-side entry points are the extern "C" functions declared in
@@ -1539,6 +1541,35 @@ struct RouteSlice {
     }
   }
 
+  // load() in two parts: the weights alone, and the activations from a
+  // [tokens][d] bf16 copy in LDS (rows at and past nvalid read row nvalid-1,
+  // as load() does past T)
+  __device__ __forceinline__ void load_w(const float* gw, int E, int d, int sl, int lane) {
+    slice = sl;
+    const int n = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < KSW; ++i) {
+      const int c = (slice * KSW + i) * 32 + 8 * g;
+      const int cc = c < d ? c : 0;
+      const int64_t wrow = n < E ? n : 0;
+      wr[i][0] = *(const float4*)(gw + wrow * d + cc);
+      wr[i][1] = *(const float4*)(gw + wrow * d + cc + 4);
+    }
+  }
+  __device__ __forceinline__ void load_x_lds(const uint16_t* sx, int d, int nvalid, int lane) {
+    const int n = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < KSW; ++i) {
+      const int c = (slice * KSW + i) * 32 + 8 * g;
+      const int cc = c < d ? c : 0;
+#pragma unroll
+      for (int tt = 0; tt < NTT; ++tt) {
+        const int t = tt * 16 + n < nvalid ? tt * 16 + n : nvalid - 1;
+        xr[tt][i] = *(const uint4*)(sx + t * d + cc);
+      }
+    }
+  }
+
   __device__ __forceinline__ void compute(int E, int d, int lane, float* part) {
     const int n = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -2448,6 +2479,51 @@ dispatch_small_kernel(const int64_t* __restrict__ topi, const float* __restrict_
 // ---------------------------------------------------------------------------
 // combine: out[t] = cast(sum over ascending expert id of y * w), fp32, no FMA
 // ---------------------------------------------------------------------------
+// The dispatched slots of token t (inv >= 0) as (yperm row, weight) in
+// ascending expert id, the summation order of the combine; returns their
+// count.  Every inv/topi/topw read of the token is issued before the first is
+// used, and the slots are ordered by an odd-even transposition sort over
+// fixed register indices (dispatched experts of a token are distinct).
+__device__ __forceinline__ int combine_slots(const int64_t* topi, const float* topw, const int32_t* inv, int64_t t,
+                                             int k, int (&rw)[8], float (&wt)[8]) {
+  int pos[8], key[8];
+  int64_t ti[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (j < k) {
+      pos[j] = inv[t * k + j];
+      ti[j] = topi[t * k + j];
+      wt[j] = topw[t * k + j];
+    }
+  int n = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const bool live = j < k && pos[j] >= 0;
+    key[j] = live ? (int)ti[j] : 0x7fffffff;
+    rw[j] = live ? pos[j] : 0;
+    n += live ? 1 : 0;
+  }
+#pragma unroll
+  for (int pass = 0; pass < 8; ++pass) {
+    if (pass >= k) break;  // k passes sort k keys
+#pragma unroll
+    for (int i = pass & 1; i + 1 < 8; i += 2) {
+      if (i + 1 >= k) break;
+      if (key[i] > key[i + 1]) {
+        const int tk = key[i], tr = rw[i];
+        const float tw = wt[i];
+        key[i] = key[i + 1];
+        rw[i] = rw[i + 1];
+        wt[i] = wt[i + 1];
+        key[i + 1] = tk;
+        rw[i + 1] = tr;
+        wt[i + 1] = tw;
+      }
+    }
+  }
+  return n;
+}
+
 template <bool BF16, int CW>
 __global__ void __launch_bounds__(256)
 combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
@@ -2462,26 +2538,9 @@ combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
   const int64_t t = gidx / cpt;
   if (t >= T) return;
   const int c0 = (int)(gidx % cpt) * CW;
-  // gather (expert, row, weight) of dispatched slots, sort by expert id
-  int ex[8];
   int rw[8];
   float wt[8];
-  int n = 0;
-  for (int j = 0; j < k; ++j) {
-    const int pos = inv[t * k + j];
-    if (pos < 0) continue;
-    const int ee = (int)topi[t * k + j];
-    int q = n++;
-    while (q > 0 && ex[q - 1] > ee) {
-      ex[q] = ex[q - 1];
-      rw[q] = rw[q - 1];
-      wt[q] = wt[q - 1];
-      --q;
-    }
-    ex[q] = ee;
-    rw[q] = pos;
-    wt[q] = topw[t * k + j];
-  }
+  const int n = combine_slots(topi, topw, inv, t, k, rw, wt);
   uint4 yv[8][NV];
 #pragma unroll
   for (int s = 0; s < 8; ++s)
@@ -2576,12 +2635,16 @@ __device__ __forceinline__ void rms_unpack(const uint4* v, float (&f)[16]) {
 // (f * r) * weight for 16 columns from c0, cast and stored at dst
 template <bool BF16>
 __device__ __forceinline__ void rms_scale_store(const float (&f)[16], float r, const float* weight, int c0,
-                                                char* dst) {
+                                                char* dst, char* lds_dst = nullptr) {
   float o[16];
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    o[q] = f[q] * r;
-    if (weight) o[q] = o[q] * ldgf(weight + c0 + q);
+  for (int q = 0; q < 16; ++q) o[q] = f[q] * r;
+  if (weight) {  // all 16 loads in flight before the first product
+    float wv[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) wv[q] = ldgf(weight + c0 + q);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) o[q] = o[q] * wv[q];
   }
   if constexpr (BF16) {
 #pragma unroll
@@ -2591,7 +2654,8 @@ __device__ __forceinline__ void rms_scale_store(const float (&f)[16], float r, c
       w.y = f2bf(o[j * 8 + 2]) | (f2bf(o[j * 8 + 3]) << 16);
       w.z = f2bf(o[j * 8 + 4]) | (f2bf(o[j * 8 + 5]) << 16);
       w.w = f2bf(o[j * 8 + 6]) | (f2bf(o[j * 8 + 7]) << 16);
-      ((uint4*)dst)[j] = w;
+      if (dst) ((uint4*)dst)[j] = w;
+      if (lds_dst) ((uint4*)lds_dst)[j] = w;
     }
   } else {
 #pragma unroll
@@ -2679,93 +2743,188 @@ rms_norm_kernel(const void* __restrict__ x, const float* __restrict__ weight,
 // r) * weight).  Chunks are combined one after another, every slot row load of
 // a chunk in flight together.
 template <bool BF16, int NCH>
+struct CombineNormRow {
+  static_assert(NCH >= 1 && NCH <= RMS_KEEP, "chunks per lane");
+  static constexpr int ES = BF16 ? 2 : 4;
+  static constexpr int VPC = BF16 ? 2 : 4;
+  float v[NCH][16];  // the combined row as stored in out (rounded to the dtype)
+  float r;           // 1 / rms
+
+  // the combine of the chunks and the row's 1/rms; no store
+  __device__ __forceinline__ void compute(const void* yperm, const int64_t* topi, const float* topw,
+                                          const int32_t* inv, float eps, int64_t t, int d, int k, int lane) {
+    const int nch = d / 16;
+    int rw[8];
+    float wt[8];
+    const int n = combine_slots(topi, topw, inv, t, k, rw, wt);
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = lane + i * 64;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) v[i][q] = 0.0f;
+      if (c < nch) {
+        uint4 yv[8][VPC];
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+          if (s < n) {
+            const char* src = (const char*)yperm + ((int64_t)rw[s] * d + c * 16) * ES;
+#pragma unroll
+            for (int j = 0; j < VPC; ++j) yv[s][j] = ldg16(src + j * 16);
+          }
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+          if (s < n) {
+            float y[16];
+            rms_unpack<BF16>(yv[s], y);
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+              const float pr = y[q] * wt[s];  // rounded product (library built with -ffp-contract=off)
+              v[i][q] = v[i][q] + pr;
+            }
+          }
+        if constexpr (BF16) {
+#pragma unroll
+          for (int q = 0; q < 16; ++q) v[i][q] = bf2f(f2bf(v[i][q]));
+        }
+      }
+      ss = rms_chunk_sumsq(ss, v[i]);
+    }
+    // rms_norm_kernel also adds RMS_KEEP - NCH all-zero chunks here: +0 changes nothing
+    ss = wave_sum(ss);
+    r = 1.0f / __fsqrt_rn(ss / (float)d + eps);
+  }
+
+  // the normalised row to LDS only (lds_row: d values of the dtype)
+  __device__ __forceinline__ void to_lds(const float* weight, int d, int lane, char* lds_row) const {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = lane + i * 64;
+      if (c < d / 16) rms_scale_store<BF16>(v[i], r, weight, c * 16, nullptr, lds_row + c * 16 * ES);
+    }
+  }
+
+  // out and norm_out of token t
+  __device__ __forceinline__ void store(void* out, const float* weight, void* norm_out, int64_t t, int d,
+                                        int lane) const {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = lane + i * 64;
+      if (c < d / 16) {
+        rms_scale_store<BF16>(v[i], r, weight, c * 16, (char*)norm_out + (t * d + c * 16) * ES);
+        char* dst = (char*)out + (t * d + c * 16) * ES;
+        if constexpr (BF16) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            uint4 w;
+            w.x = f2bf(v[i][j * 8 + 0]) | (f2bf(v[i][j * 8 + 1]) << 16);
+            w.y = f2bf(v[i][j * 8 + 2]) | (f2bf(v[i][j * 8 + 3]) << 16);
+            w.z = f2bf(v[i][j * 8 + 4]) | (f2bf(v[i][j * 8 + 5]) << 16);
+            w.w = f2bf(v[i][j * 8 + 6]) | (f2bf(v[i][j * 8 + 7]) << 16);
+            ((uint4*)dst)[j] = w;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            ((float4*)dst)[j] = make_float4(v[i][j * 4], v[i][j * 4 + 1], v[i][j * 4 + 2], v[i][j * 4 + 3]);
+        }
+      }
+    }
+  }
+};
+
+template <bool BF16, int NCH>
 __global__ void __launch_bounds__(256)
 combine_norm_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
                     const float* __restrict__ topw, const int32_t* __restrict__ inv,
                     void* __restrict__ out, const float* __restrict__ weight, float eps,
                     void* __restrict__ norm_out, int64_t T, int d, int k) {
-  static_assert(NCH >= 1 && NCH <= RMS_KEEP, "chunks per lane");
-  constexpr int ES = BF16 ? 2 : 4;
-  constexpr int VPC = BF16 ? 2 : 4;
-  const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  const int nch = d / 16;
-  int ex[8];
-  int rw[8];
-  float wt[8];
-  int n = 0;
-  for (int j = 0; j < k; ++j) {
-    const int pos = inv[t * k + j];
-    if (pos < 0) continue;
-    const int ee = (int)topi[t * k + j];
-    int q = n++;
-    while (q > 0 && ex[q - 1] > ee) {
-      ex[q] = ex[q - 1];
-      rw[q] = rw[q - 1];
-      wt[q] = wt[q - 1];
-      --q;
-    }
-    ex[q] = ee;
-    rw[q] = pos;
-    wt[q] = topw[t * k + j];
+  CombineNormRow<BF16, NCH> cn;
+  cn.compute(yperm, topi, topw, inv, eps, t, d, k, threadIdx.x & 63);
+  cn.store(out, weight, norm_out, t, d, threadIdx.x & 63);
+}
+
+// The combine and output norm of 16 tokens (one wave each, combine_norm_row)
+// followed by the next layer's router on the normed rows: the logits, softmax
+// and top-k of router_mfma_kernel for these 16 tokens (RouteSlice over the
+// same K slices, route_reduce, route_select_group), so the per-token
+// arithmetic, and the bits, are those of routing norm_out in a kernel of its
+// own.  The normed rows reach the router through LDS (a copy beside the
+// norm_out stores) and the bias stays in a register.  Writes the next layer's
+// prob/topi/topw (no counts: the next gate/up kernel or dispatch builds its
+// dispatch from the top-k).
+constexpr int CNR_TOK = 16;
+constexpr int CNR_DMAX = 2048;  // the MFMA router's widest d
+
+// Workgroup barrier for LDS data only: waits for this wave's LDS accesses,
+// not for its global stores (__syncthreads waits for those too).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+template <int NCH, int EMAX, bool EXACT, int KSW>
+__global__ void __launch_bounds__(CNR_TOK * 64)
+combine_norm_route_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
+                          const float* __restrict__ topw, const int32_t* __restrict__ inv, void* __restrict__ out,
+                          const float* __restrict__ weight, float eps, void* norm_out, int64_t T, int d, int k,
+                          const float* __restrict__ ngw, const float* __restrict__ ngb, RouteOut no, int nE,
+                          int nk) {
+  static_assert(EMAX <= 16, "the MFMA router covers up to 16 experts");
+  constexpr int NWAVES = CNR_TOK;
+  __shared__ __attribute__((aligned(16))) float part[RK_SLICES * CNR_TOK * 16];
+  __shared__ float slog[CNR_TOK][EMAX];
+  __shared__ smaul_topk::Pair spair[CNR_TOK][EMAX];
+  __shared__ int s_ti[CNR_TOK][8];
+  __shared__ float s_tw[CNR_TOK][8];
+  __shared__ __attribute__((aligned(16))) uint16_t sx[CNR_TOK * CNR_DMAX];
+  static_assert(NWAVES >= RK_SLICES, "one K slice per router wave");
+  static_assert(CNR_TOK * EMAX <= RK_SLICES * 64, "the bias-adding threads are router-wave threads");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int E = EXACT ? EMAX : nE;
+  const int64_t t0 = (int64_t)blockIdx.x * CNR_TOK;
+  const int nvalid = (int)min<int64_t>(CNR_TOK, T - t0);
+  // The combine and norm first, the normed row to LDS only.  The router
+  // weights and bias are loaded after the barrier: a CU returns reads in
+  // issue order, so cold weights issued before the combine's slot reads
+  // would hold those up.  The global stores of out / norm_out go out after
+  // the routing MFMAs, so that the wait for the weights does not also wait
+  // for them.
+  // (At KSW = 8 the row held through the routing would spill: stored first.)
+  constexpr bool LATE_STORE = KSW == 4;
+  CombineNormRow<true, NCH> cn;
+  const bool mine = wave < nvalid;  // uniform per wave
+  if (mine) {
+    cn.compute(yperm, topi, topw, inv, eps, t0 + wave, d, k, lane);
+    cn.to_lds(weight, d, lane, (char*)(sx + wave * d));
+    if (!LATE_STORE) cn.store(out, weight, norm_out, t0 + wave, d, lane);
   }
-  float v[NCH][16];
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < NCH; ++i) {
-    const int c = lane + i * 64;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) v[i][q] = 0.0f;
-    if (c < nch) {
-      uint4 yv[8][VPC];
-#pragma unroll
-      for (int s = 0; s < 8; ++s)
-        if (s < n) {
-          const char* src = (const char*)yperm + ((int64_t)rw[s] * d + c * 16) * ES;
-#pragma unroll
-          for (int j = 0; j < VPC; ++j) yv[s][j] = ldg16(src + j * 16);
-        }
-#pragma unroll
-      for (int s = 0; s < 8; ++s)
-        if (s < n) {
-          float y[16];
-          rms_unpack<BF16>(yv[s], y);
-#pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            const float pr = y[q] * wt[s];  // rounded product (library built with -ffp-contract=off)
-            v[i][q] = v[i][q] + pr;
-          }
-        }
-      // the row as stored in out (cast to the activation dtype)
-      char* dst = (char*)out + (t * d + c * 16) * ES;
-      if constexpr (BF16) {
-#pragma unroll
-        for (int q = 0; q < 16; ++q) v[i][q] = bf2f(f2bf(v[i][q]));
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          uint4 w;
-          w.x = f2bf(v[i][j * 8 + 0]) | (f2bf(v[i][j * 8 + 1]) << 16);
-          w.y = f2bf(v[i][j * 8 + 2]) | (f2bf(v[i][j * 8 + 3]) << 16);
-          w.z = f2bf(v[i][j * 8 + 4]) | (f2bf(v[i][j * 8 + 5]) << 16);
-          w.w = f2bf(v[i][j * 8 + 6]) | (f2bf(v[i][j * 8 + 7]) << 16);
-          ((uint4*)dst)[j] = w;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          ((float4*)dst)[j] = make_float4(v[i][j * 4], v[i][j * 4 + 1], v[i][j * 4 + 2], v[i][j * 4 + 3]);
-      }
-    }
-    ss = rms_chunk_sumsq(ss, v[i]);
+  lds_barrier();
+  // route_reduce's thread q = tok * EMAX + e adds bias[e]
+  const int re = (int)(threadIdx.x % EMAX);
+  float bias = 0.0f;
+  if (wave < RK_SLICES) {  // uniform per wave
+    RouteSlice<KSW, 1> rs;
+    rs.load_w(ngw, E, d, wave, lane);
+    if (threadIdx.x < (unsigned)(CNR_TOK * EMAX) && re < E && ngb) bias = ngb[re];
+    rs.load_x_lds(sx, d, nvalid, lane);
+    rs.compute(E, d, lane, part);
   }
-  // rms_norm_kernel also adds RMS_KEEP - NCH all-zero chunks here: +0 changes nothing
-  ss = wave_sum(ss);
-  const float r = 1.0f / __fsqrt_rn(ss / (float)d + eps);
+  if (LATE_STORE && mine) cn.store(out, weight, norm_out, t0 + wave, d, lane);
+  lds_barrier();
+  // route_reduce with the bias from a register (the same sums, in slice order)
+  if (threadIdx.x < (unsigned)(CNR_TOK * EMAX)) {
+    const int tok = (int)threadIdx.x / EMAX;
+    if (re < E && t0 + tok < T) {
+      float v = part[tok * 16 + re];
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) {
-    const int c = lane + i * 64;
-    if (c < nch) rms_scale_store<BF16>(v[i], r, weight, c * 16, (char*)norm_out + (t * d + c * 16) * ES);
+      for (int sl = 1; sl < RK_SLICES; ++sl) v += part[(sl * CNR_TOK + tok) * 16 + re];
+      slog[tok][re] = ngb ? v + bias : v;
+    }
+  }
+  lds_barrier();
+  constexpr int TPW = 64 / EMAX;
+  for (int tl = wave * TPW + (lane / EMAX); tl < CNR_TOK; tl += NWAVES * TPW) {
+    const int64_t t = t0 + tl;
+    route_select_group<EMAX>(slog[tl], spair[tl], E, nk, t, t < T, no, true, s_ti[tl], s_tw[tl], nullptr);
   }
 }
 
@@ -3285,13 +3444,68 @@ struct OutNorm {
   void* out;
 };
 
+// The next layer's router, run on the normed output (smaul_moe_forward_chain)
+struct NextRoute {
+  const float* gate_w;
+  const float* gate_b;
+  int64_t E, k;
+  float* prob;
+  int64_t* topi;
+  float* topw;
+};
+
+// combine + norm + the next layer's MFMA router in one kernel (bf16, d <= 2048)
+static int launch_combine_norm_route(const void* yperm, const int64_t* topi, const float* topw, const int32_t* inv,
+                                     void* out, const OutNorm& nrm, const NextRoute& nr, int64_t T, int64_t d,
+                                     int64_t k, hipStream_t stream) {
+  RouteOut no{};
+  no.prob = nr.prob;
+  no.topi = nr.topi;
+  no.topw = nr.topw;
+  const dim3 grid((unsigned)((T + CNR_TOK - 1) / CNR_TOK)), block(CNR_TOK * 64);
+  const int E = (int)nr.E;
+#define SMAUL_CNR2(NCH, KSW, EMAX, EXACT)                                                                         \
+  hipLaunchKernelGGL((combine_norm_route_kernel<NCH, EMAX, EXACT, KSW>), grid, block, 0, stream, yperm, topi, topw, \
+                     inv, out, nrm.weight, nrm.eps, nrm.out, T, (int)d, (int)k, nr.gate_w, nr.gate_b, no, E,       \
+                     (int)nr.k)
+#define SMAUL_CNR1(NCH, KSW)                                                 \
+  if (E <= 4) {                                                              \
+    if (E == 4) SMAUL_CNR2(NCH, KSW, 4, true); else SMAUL_CNR2(NCH, KSW, 4, false);   \
+  } else if (E <= 8) {                                                       \
+    if (E == 8) SMAUL_CNR2(NCH, KSW, 8, true); else SMAUL_CNR2(NCH, KSW, 8, false);   \
+  } else {                                                                   \
+    if (E == 16) SMAUL_CNR2(NCH, KSW, 16, true); else SMAUL_CNR2(NCH, KSW, 16, false); \
+  }
+  if (route_ksw(d) == 4) {
+    SMAUL_CNR1(1, 4)
+  } else {
+    SMAUL_CNR1(2, 8)
+  }
+#undef SMAUL_CNR1
+#undef SMAUL_CNR2
+  return check_launch("combine_norm_route_kernel");
+}
+
 // The last stage of the layer: the combine, or the combine and the output
-// norm (fused when d % 16 == 0 and d <= 4096, else the two kernels).
+// norm (fused when d % 16 == 0 and d <= 4096, else the two kernels), and the
+// next layer's router on the normed rows when nr is given (fused into the
+// same kernel for bf16 activations and the MFMA router's shapes, else
+// smaul_moe_router on norm_out).
 static int finish_combine(const void* yperm, int act_dtype, const int64_t* topi, const float* topw,
                           const int32_t* inv, void* out, int64_t T, int64_t d, int64_t k, const OutNorm* nrm,
-                          hipStream_t stream) {
+                          const NextRoute* nr, hipStream_t stream) {
   if (!nrm) return smaul_moe_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, stream);
-  if (d % 16 == 0 && d <= 64 * 16 * RMS_KEEP && aligned16(yperm) && aligned16(out) && aligned16(nrm->out)) {
+  const bool fuse_norm =
+      d % 16 == 0 && d <= 64 * 16 * RMS_KEEP && aligned16(yperm) && aligned16(out) && aligned16(nrm->out);
+  if (nr) {
+    if (fuse_norm && route_mfma_ok(nr->E, d, act_dtype) && aligned16(nr->gate_w))
+      return launch_combine_norm_route(yperm, topi, topw, inv, out, *nrm, *nr, T, d, k, stream);
+    const int rc = finish_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, nrm, nullptr, stream);
+    if (rc) return rc;
+    return smaul_moe_router(nrm->out, act_dtype, nr->gate_w, nr->gate_b, nr->prob, nr->topi, nr->topw, T, d, nr->E,
+                            nr->k, stream);
+  }
+  if (fuse_norm) {
     const int nch = (int)((d + 1023) / 1024);
     const dim3 grid((unsigned)((T + 3) / 4)), block(256);
     const bool bf = act_dtype == SMAUL_DTYPE_BF16;
@@ -3314,7 +3528,8 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
                             const uint8_t* const* down_w8, const float* const* down_s, void* out,
                             float* prob, int64_t* topi, float* topw, int32_t* counts, void* workspace,
                             int64_t workspace_bytes, int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
-                            int64_t tile, int flags, const OutNorm* nrm, hipStream_t stream) {
+                            int64_t tile, int flags, const OutNorm* nrm, bool routed, const NextRoute* nr,
+                            hipStream_t stream) {
   const int64_t need = smaul_moe_workspace_size(T, d, h, E, k, act_dtype);
   if (need < 0) return fail(SMAUL_ERR_INVALID, "moe_forward: bad sizes");
   if (workspace_bytes < need)
@@ -3365,7 +3580,9 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
   od.perm_w = perm_w;
   od.inv = inv;
   if (nb == 1 && !fused) o = od;  // one router block: it dispatches too
-  if (fused && route_mfma_ok(E, d, act_dtype)) {
+  if (routed) {
+    // prob/topi/topw came with the call (the previous layer's fused router)
+  } else if (fused && route_mfma_ok(E, d, act_dtype)) {
     // decode: top-k only, one block per 16 tokens; the gate/up kernel dispatches
     RouteOut ot = o;
     ot.blockcnt = nullptr;
@@ -3399,9 +3616,18 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
     rc = smaul_moe_down(hdn, act_dtype, down_w8, down_s, yperm, seg_off, tile_off, max_tiles, E, d, h, tile,
                         bm, flags, stream);
     if (rc) return rc;
-    return finish_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, nrm, stream);
+    return finish_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, nrm, nr, stream);
   }
-  if (nb > 1 && T <= 64) {  // one wave dispatches straight from topi/topw
+  if (routed && T > 64) {  // the dispatch from the given top-k, as smaul_moe_dispatch
+    const int64_t nbd = (T + DISPATCH_TPB - 1) / DISPATCH_TPB;  // <= nb: blockcnt/blockoff fit
+    hipLaunchKernelGGL(block_count_kernel, dim3((unsigned)nbd), dim3(64), 0, stream, topi, topw, blockcnt, T,
+                       (int)E, (int)k, DISPATCH_TPB);
+    rc = check_launch("block_count_kernel");
+    if (rc) return rc;
+    rc = launch_scan_scatter(topi, topw, blockcnt, blockoff, counts, seg_off, tile_off, perm_row, perm_w, inv,
+                             T, E, k, bm, DISPATCH_TPB, stream);
+    if (rc) return rc;
+  } else if ((nb > 1 || routed) && T <= 64) {  // one wave dispatches straight from topi/topw
     hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(64), 0, stream, topi, topw, od, T, (int)E, (int)k);
     rc = check_launch("dispatch_small_kernel");
     if (rc) return rc;
@@ -3416,7 +3642,7 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
   rc = smaul_moe_down(hdn, act_dtype, down_w8, down_s, yperm, seg_off, tile_off, max_tiles, E, d, h, tile,
                       bm, flags, stream);
   if (rc) return rc;
-  return finish_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, nrm, stream);
+  return finish_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, nrm, nr, stream);
 }
 
 int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
@@ -3428,7 +3654,7 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
                       int64_t tile, int flags, hipStream_t stream) {
   return moe_forward_impl(x, act_dtype, gate_w, gate_b, gate_w8, gate_s, up_w8, up_s, down_w8, down_s, out, prob,
                           topi, topw, counts, workspace, workspace_bytes, T, d, h, E, k, tile, flags, nullptr,
-                          stream);
+                          false, nullptr, stream);
 }
 
 int smaul_moe_forward_norm(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
@@ -3443,7 +3669,35 @@ int smaul_moe_forward_norm(const void* x, int act_dtype, const float* gate_w, co
   if (T > 0 && !norm_out) return fail(SMAUL_ERR_INVALID, "moe_forward_norm: null norm_out");
   const OutNorm nrm{norm_w, eps, norm_out};
   return moe_forward_impl(x, act_dtype, gate_w, gate_b, gate_w8, gate_s, up_w8, up_s, down_w8, down_s, out, prob,
-                          topi, topw, counts, workspace, workspace_bytes, T, d, h, E, k, tile, flags, &nrm, stream);
+                          topi, topw, counts, workspace, workspace_bytes, T, d, h, E, k, tile, flags, &nrm, false,
+                          nullptr, stream);
+}
+
+int smaul_moe_forward_chain(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
+                            const uint8_t* const* gate_w8, const float* const* gate_s,
+                            const uint8_t* const* up_w8, const float* const* up_s,
+                            const uint8_t* const* down_w8, const float* const* down_s, void* out,
+                            float* prob, int64_t* topi, float* topw, int32_t* counts, void* workspace,
+                            int64_t workspace_bytes, int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
+                            int64_t tile, int flags, const float* norm_w, float eps, void* norm_out, int routed,
+                            const float* next_gate_w, const float* next_gate_b, int64_t next_E, int64_t next_k,
+                            float* next_prob, int64_t* next_topi, float* next_topw, hipStream_t stream) {
+  if (!(eps > 0.0f) || !std::isfinite(eps)) return fail(SMAUL_ERR_INVALID, "moe_forward_chain: eps must be positive finite");
+  if (T > 0 && !norm_out) return fail(SMAUL_ERR_INVALID, "moe_forward_chain: null norm_out");
+  if (T > 0 && routed && (!prob || !topi || !topw))
+    return fail(SMAUL_ERR_INVALID, "moe_forward_chain: routed needs prob, topi and topw");
+  NextRoute nr{next_gate_w, next_gate_b, next_E, next_k, next_prob, next_topi, next_topw};
+  if (next_gate_w) {
+    // the next router reads norm_out: same rows, width and dtype as x
+    int rc = check_router_args(norm_out, act_dtype, next_gate_w, T, d, next_E, next_k);
+    if (rc) return rc;
+    if (T > 0 && (!next_prob || !next_topi || !next_topw))
+      return fail(SMAUL_ERR_INVALID, "moe_forward_chain: null next-router output");
+  }
+  const OutNorm nrm{norm_w, eps, norm_out};
+  return moe_forward_impl(x, act_dtype, gate_w, gate_b, gate_w8, gate_s, up_w8, up_s, down_w8, down_s, out, prob,
+                          topi, topw, counts, workspace, workspace_bytes, T, d, h, E, k, tile, flags, &nrm,
+                          routed != 0, next_gate_w ? &nr : nullptr, stream);
 }
 
 int smaul_fp8_canonicalize(const uint8_t* codes, uint8_t* out, int64_t n, hipStream_t stream) {

@@ -375,16 +375,28 @@ class RocmBackend:
         """
         return self._moe_forward(x, gate_w, gate_b, experts, top_k, tile, None)
 
-    def moe_forward_norm(self, x, gate_w, gate_b, experts, top_k, tile, norm_weight=None, eps=1e-6):
+    def moe_forward_norm(self, x, gate_w, gate_b, experts, top_k, tile, norm_weight=None, eps=1e-6,
+                         routing=None, next_router=None):
         """moe_forward followed by RMSNorm of its output (Block's norm of the
         FFN output, model.py:636), fused into the combine where the shape
         allows.  Returns moe_forward's tuple plus the normalised output, which
-        equals rms_norm(out, norm_weight, eps) bit for bit."""
+        equals rms_norm(out, norm_weight, eps) bit for bit.
+
+        For a chain of layers (each layer's normalised output is the next
+        layer's input, model.py:636 into the next router, model.py:558-570):
+        - routing=(prob, topi, topw): this layer's routing of x, computed
+          before (moe_router's outputs, or the previous call's next routing);
+          the layer runs no router and returns prob/topi as given.
+        - next_router=(gate_w, gate_b, top_k): the next layer's router; the
+          normalised output is routed with it (inside the combine kernel
+          where the shape allows) and (prob, topi, topw) is appended to the
+          returned tuple, equal bit for bit to moe_router(normed, ...)."""
         if not math.isfinite(eps) or eps <= 0:
             raise ValueError(f"RMSNorm eps must be positive finite, got {eps!r}")
-        return self._moe_forward(x, gate_w, gate_b, experts, top_k, tile, (norm_weight, eps))
+        return self._moe_forward(x, gate_w, gate_b, experts, top_k, tile, (norm_weight, eps), routing,
+                                 next_router)
 
-    def _moe_forward(self, x, gate_w, gate_b, experts, top_k, tile, norm):
+    def _moe_forward(self, x, gate_w, gate_b, experts, top_k, tile, norm, routing=None, next_router=None):
         lib = _lib.load()
         _need_device("moe_forward", x, gate_w)
         if x.dtype not in _ACT:
@@ -411,9 +423,34 @@ class RocmBackend:
             gb = gb if (gb.dtype == torch.float32 and gb.is_contiguous()) else gb.float().contiguous()
         act = _ACT[x.dtype]
         out = torch.empty_like(x2)
-        prob = torch.empty(T, E, dtype=torch.float32, device=dev)
-        topi = torch.empty(T, top_k, dtype=torch.int64, device=dev)
-        topw = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+        if routing is None:
+            prob = torch.empty(T, E, dtype=torch.float32, device=dev)
+            topi = torch.empty(T, top_k, dtype=torch.int64, device=dev)
+            topw = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+        else:
+            prob, topi, topw = routing
+            _need_device("moe_forward", x, prob, topi, topw)
+            for name, t, dt, shape in (("prob", prob, torch.float32, (T, E)), ("topi", topi, torch.int64, (T, top_k)),
+                                       ("topw", topw, torch.float32, (T, top_k))):
+                if t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous():
+                    raise RuntimeError(f"moe_forward: routing {name} must be contiguous {dt} {list(shape)}, "
+                                       f"got {t.dtype} {list(t.shape)}")
+        nxt = None
+        if next_router is not None:
+            ngw, ngb, nk = next_router
+            _need_device("moe_forward", x, ngw, ngb)
+            nE = ngw.shape[0]
+            if ngw.dim() != 2 or ngw.shape[1] != d:
+                raise RuntimeError(f"moe_forward: next gate weight must be [E, {d}], got {tuple(ngw.shape)}")
+            if not 1 <= nk <= nE:
+                raise ValueError(f"next top_k must be in [1, {nE}], got {nk}")
+            ngw = ngw.detach()
+            ngw = ngw if (ngw.dtype == torch.float32 and ngw.is_contiguous()) else ngw.float().contiguous()
+            if ngb is not None:
+                ngb = ngb.detach()
+                ngb = ngb if (ngb.dtype == torch.float32 and ngb.is_contiguous()) else ngb.float().contiguous()
+            nxt = (ngw, ngb, nE, nk, torch.empty(T, nE, dtype=torch.float32, device=dev),
+                   torch.empty(T, nk, dtype=torch.int64, device=dev), torch.empty(T, nk, dtype=torch.float32, device=dev))
         # the dispatch kernel writes every count; no fill, so the call can be graph-captured
         counts = torch.empty(E, dtype=torch.int32, device=dev) if T > 0 else \
             torch.zeros(E, dtype=torch.int32, device=dev)
@@ -440,10 +477,25 @@ class RocmBackend:
             with torch.cuda.device(dev):
                 if norm is None:
                     rc = lib.smaul_moe_forward(*args, _stream_handle(dev))
-                else:
+                elif routing is None and nxt is None:
                     rc = lib.smaul_moe_forward_norm(*args, None if nw is None else nw.data_ptr(), norm[1],
                                                     normed.data_ptr(), _stream_handle(dev))
+                else:
+                    nargs = [None] * 7 if nxt is None else \
+                        [nxt[0].data_ptr(), None if nxt[1] is None else nxt[1].data_ptr(), nxt[2], nxt[3],
+                         nxt[4].data_ptr(), nxt[5].data_ptr(), nxt[6].data_ptr()]
+                    if nxt is None:
+                        nargs[2] = nargs[3] = 0
+                    rc = lib.smaul_moe_forward_chain(*args, None if nw is None else nw.data_ptr(), norm[1],
+                                                     normed.data_ptr(), int(routing is not None), *nargs,
+                                                     _stream_handle(dev))
             _lib.check(rc, "moe_forward")
         lead = x.shape[:-1]
         res = (out.reshape(*lead, d), prob.reshape(*lead, E), topi.reshape(*lead, top_k), counts)
-        return res if norm is None else res + (normed.reshape(*lead, d),)
+        if norm is None:
+            return res
+        res = res + (normed.reshape(*lead, d),)
+        if nxt is not None:
+            res = res + ((nxt[4].reshape(*lead, nxt[2]), nxt[5].reshape(*lead, nxt[3]),
+                          nxt[6].reshape(*lead, nxt[3])),)
+        return res

@@ -59,6 +59,17 @@ def test_library_validates_without_touching_the_gpu():
     rc = lib.smaul_moe_forward_norm(None, 1, None, None, None, None, None, None, None, None, None, None, None,
                                     None, None, None, 0, 64, 64, 128, 8, 2, 64, 0, None, float("nan"), None, None)
     assert rc == _lib.SMAUL_ERR_INVALID and "eps" in _lib.last_error()
+    # the chained layer: eps, a routed call without its routing, the next router's sizes
+    head = [None, 1, None, None, None, None, None, None, None, None, None, None, None, None, None, None]
+    rc = lib.smaul_moe_forward_chain(*head, 0, 4, 64, 128, 8, 2, 64, 0, None, 0.0, None, 0,
+                                     None, None, 0, 0, None, None, None, None)
+    assert rc == _lib.SMAUL_ERR_INVALID and "eps" in _lib.last_error()
+    rc = lib.smaul_moe_forward_chain(*head, 0, 4, 64, 128, 8, 2, 64, 0, None, 1e-6, 16, 1,
+                                     None, None, 0, 0, None, None, None, None)
+    assert rc == _lib.SMAUL_ERR_INVALID and "routed" in _lib.last_error()
+    rc = lib.smaul_moe_forward_chain(*head, 0, 4, 64, 128, 8, 2, 64, 0, None, 1e-6, 16, 0,
+                                     16, None, 65, 2, None, None, None, None)
+    assert rc == _lib.SMAUL_ERR_INVALID and "router" in _lib.last_error()
 
 
 def _host_topk(vals, k):

@@ -536,3 +536,41 @@ def test_moe_forward_norm(T, d, h, E, k, dtype, weighted):
     if w is not None:
         r = r * w.cpu()
     assert rel_max(got[4].float(), r) < (8e-3 if dtype == torch.bfloat16 else 4e-6)
+
+
+@pytest.mark.parametrize("T,d,h,E,k,nE,nk,dtype", [
+    (64, 1024, 2560, 8, 2, 8, 2, torch.bfloat16),   # C4 layer: decode path, router fused into the combine
+    (40, 2048, 256, 4, 2, 16, 4, torch.bfloat16),   # two chunks per lane, 16 next experts
+    (300, 256, 640, 8, 2, 6, 2, torch.bfloat16),    # prefill path, ragged last 16-token block, E < EMAX
+    (33, 192, 320, 4, 3, 4, 3, torch.float32),      # fp32: the next router runs as its own kernel
+    (5, 4160, 128, 4, 2, 4, 2, torch.bfloat16),     # d > 4096: combine, norm, router kernels
+])
+def test_moe_forward_chain(T, d, h, E, k, nE, nk, dtype):
+    """Two chained layers: layer A routes its normalised output with layer B's
+    router (next_router), layer B takes that routing (routing=).  Every output
+    equals the unchained calls bit for bit: A's outputs those of
+    moe_forward_norm, the next routing moe_router(normed), B's outputs those
+    of moe_forward_norm on A's normalised output."""
+    print(f"case moe_forward_chain T={T} d={d} h={h} E={E} k={k} nE={nE} nk={nk} {dtype}", flush=True)
+    x, gwa, gba, exa = make_moe(T * 37 + d, T, d, h, E, k, dtype=dtype)
+    _, gwb, gbb, exb = make_moe(T * 41 + h, 1, d, h, nE, nk, dtype=dtype)
+    gen = torch.Generator().manual_seed(d + 1)
+    w = (1.0 + 0.1 * torch.randn(d, generator=gen)).to(DEV)
+    dx = x.to(DEV)
+    dgwa, dgba, dexa = gwa.to(DEV), gba.to(DEV), to_dev_experts(exa)
+    dgwb, dgbb, dexb = gwb.to(DEV), gbb.to(DEV), to_dev_experts(exb)
+    ref_a = be().moe_forward_norm(dx, dgwa, dgba, dexa, k, 64, w, 1e-6)
+    got_a = be().moe_forward_norm(dx, dgwa, dgba, dexa, k, 64, w, 1e-6, next_router=(dgwb, dgbb, nk))
+    ref_r = be().moe_router(ref_a[4], dgwb, dgbb, nk)
+    torch.cuda.synchronize()
+    for a, b in zip(ref_a, got_a[:5]):
+        assert torch.equal(a.cpu(), b.cpu())
+    assert len(got_a) == 6
+    for a, b in zip(ref_r, got_a[5]):
+        assert torch.equal(a.cpu(), b.cpu())
+    ref_b = be().moe_forward_norm(got_a[4], dgwb, dgbb, dexb, nk, 64, w, 1e-6)
+    got_b = be().moe_forward_norm(got_a[4], dgwb, dgbb, dexb, nk, 64, w, 1e-6, routing=got_a[5])
+    torch.cuda.synchronize()
+    assert len(got_b) == 5
+    for a, b in zip(ref_b, got_b):
+        assert torch.equal(a.cpu(), b.cpu())
