@@ -2632,7 +2632,8 @@ __device__ __forceinline__ void rms_unpack(const uint4* v, float (&f)[16]) {
   }
 }
 
-// (f * r) * weight for 16 columns from c0, cast and stored at dst
+// (f * r) * weight for 16 columns from c0, cast and stored at dst and/or
+// lds_dst (either may be null)
 template <bool BF16>
 __device__ __forceinline__ void rms_scale_store(const float (&f)[16], float r, const float* weight, int c0,
                                                 char* dst, char* lds_dst = nullptr) {
@@ -2659,7 +2660,11 @@ __device__ __forceinline__ void rms_scale_store(const float (&f)[16], float r, c
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ((float4*)dst)[j] = make_float4(o[j * 4], o[j * 4 + 1], o[j * 4 + 2], o[j * 4 + 3]);
+    for (int j = 0; j < 4; ++j) {
+      const float4 w = make_float4(o[j * 4], o[j * 4 + 1], o[j * 4 + 2], o[j * 4 + 3]);
+      if (dst) ((float4*)dst)[j] = w;
+      if (lds_dst) ((float4*)lds_dst)[j] = w;
+    }
   }
 }
 
