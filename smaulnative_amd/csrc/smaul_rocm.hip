@@ -17,7 +17,8 @@
 //   router_mfma_kernel    bf16 router logits on the matrix cores (exact three-
 //                     term weight split) + softmax + top-k + renormalisation;
 //   router_kernel     the fp32 router for the other shapes.
-//   dispatch kernels  deterministic per-expert token order (ballot ranks).
+//   dispatch kernels  deterministic per-expert token order (ballot ranks);
+//                     for E <= 16 the scan runs inside the scatter's blocks.
 //   combine_kernel    weighted un-permute in ascending expert order;
 //   combine_norm_kernel  the same followed by RMSNorm of each row;
 //   combine_norm_route_kernel  and then the next layer's router on the
@@ -2459,6 +2460,107 @@ dispatch_scatter_kernel(const int64_t* __restrict__ topi, const float* __restric
   }
 }
 
+// Scan and scatter in one launch (E <= EMAX <= 16): every block sums the
+// per-block expert counts of all blocks itself, its own prefix and the totals
+// (integer sums: the offsets of dispatch_scan_kernel), block 0 writes counts,
+// seg_off and tile_off, and the scatter follows as in dispatch_scatter_kernel.
+// The count reads are issued with the token's top-k reads, so the scan costs
+// no round trip of its own.
+constexpr int SCAN_FUSED_CHUNKS = 4;  // count reads unrolled for up to 4 * 64 blocks
+template <int EMAX>
+__global__ void __launch_bounds__(64)
+dispatch_scan_scatter_kernel(const int64_t* __restrict__ topi, const float* __restrict__ topw,
+                             const int32_t* __restrict__ blockcnt, int32_t* __restrict__ counts,
+                             int32_t* __restrict__ seg_off_out, int32_t* __restrict__ tile_off,
+                             int32_t* __restrict__ perm_row, float* __restrict__ perm_w, int32_t* __restrict__ inv,
+                             int64_t T, int E, int k, int tpb, int64_t nb, int block_m) {
+  const int lane = threadIdx.x;
+  const int64_t t = (int64_t)blockIdx.x * tpb + lane;
+  const bool valid = lane < tpb && t < T;
+  int ti[8];
+  float tw[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (j < k) {
+      const int64_t v = valid ? topi[t * k + j] : -1;
+      ti[j] = (v >= 0 && v < E) ? (int)v : -1;
+      tw[j] = valid ? topw[t * k + j] : 0.0f;
+    }
+  int before[EMAX], total[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) before[e] = total[e] = 0;
+  auto add_block = [&](int64_t b, int v, int e) {
+    total[e] += v;
+    if (b < (int64_t)blockIdx.x) before[e] += v;
+  };
+  int cv[SCAN_FUSED_CHUNKS][EMAX];
+#pragma unroll
+  for (int c = 0; c < SCAN_FUSED_CHUNKS; ++c) {
+    const int64_t b = c * 64 + lane;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) cv[c][e] = (e < E && b < nb) ? blockcnt[b * E + e] : 0;
+  }
+#pragma unroll
+  for (int c = 0; c < SCAN_FUSED_CHUNKS; ++c)
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) add_block(c * 64 + lane, cv[c][e], e);
+  for (int64_t b = SCAN_FUSED_CHUNKS * 64 + lane; b < nb; b += 64)
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+      if (e < E) add_block(b, blockcnt[b * E + e], e);
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e)
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      before[e] += __shfl_xor(before[e], o, 64);
+      total[e] += __shfl_xor(total[e], o, 64);
+    }
+  int segoff[EMAX];
+  int base = 0, tbase = 0;
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e)
+    if (e < E) {
+      segoff[e] = base;
+      if (blockIdx.x == 0 && lane == 0) {
+        counts[e] = total[e];
+        seg_off_out[e] = base;
+        tile_off[e] = tbase;
+      }
+      base += total[e];
+      tbase += (total[e] + block_m - 1) / block_m;
+    }
+  if (blockIdx.x == 0 && lane == 0) {
+    seg_off_out[E] = base;
+    tile_off[E] = tbase;
+  }
+  const uint64_t sel = valid ? selection_of(ti, tw, E, k) : 0ull;
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    if (e >= E) break;
+    const uint64_t b = __ballot((sel >> e) & 1ull);
+    if ((sel >> e) & 1ull) {
+      const int pos = segoff[e] + before[e] + __popcll(b & lt);
+      perm_row[pos] = (int32_t)t;
+      for (int j = 0; j < k; ++j)
+        if (ti[j] == e && tw[j] > 0.0f) {
+          perm_w[pos] = tw[j];
+          inv[t * k + j] = pos;
+          break;
+        }
+    }
+  }
+  if (valid) {
+    uint64_t seen = 0;
+    for (int j = 0; j < k; ++j) {
+      const int ee = ti[j];
+      const bool ok = tw[j] > 0.0f && ee >= 0 && ee < E && !((seen >> ee) & 1ull);
+      if (ok) seen |= 1ull << ee;
+      else inv[t * k + j] = -1;
+    }
+  }
+}
+
 // Dispatch of at most 64 tokens in one wave, straight from the router outputs
 // (the decode regime: one launch instead of block counts, scan and scatter).
 __global__ void __launch_bounds__(64)
@@ -3253,6 +3355,16 @@ static int launch_scan_scatter(const int64_t* topi, const float* topw, int32_t* 
                                int32_t* perm_row, float* perm_w, int32_t* inv, int64_t T, int64_t E,
                                int64_t k, int64_t block_m, int64_t tpb, hipStream_t stream) {
   const int64_t nb = (T + tpb - 1) / tpb;
+  if (E <= 16 && nb <= 65535) {  // one launch
+#define SMAUL_SCS(EMAX)                                                                                         \
+  hipLaunchKernelGGL((dispatch_scan_scatter_kernel<EMAX>), dim3((unsigned)nb), dim3(64), 0, stream, topi, topw, \
+                     blockcnt, counts, seg_off, tile_off, perm_row, perm_w, inv, T, (int)E, (int)k, (int)tpb, nb, \
+                     (int)block_m)
+    if (E <= 8) SMAUL_SCS(8);
+    else SMAUL_SCS(16);
+#undef SMAUL_SCS
+    return check_launch("dispatch_scan_scatter_kernel");
+  }
   hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(SCAN_THREADS), 0, stream, blockcnt, blockoff, counts,
                      seg_off, tile_off, nb, (int)E, (int)block_m);
   int rc = check_launch("dispatch_scan_kernel");
