@@ -390,7 +390,8 @@ def test_moe_raw_codes_any_flags(T, flags, block_m):
     assert err < 2e-3
 
 
-@pytest.mark.parametrize("T,d,k", [(37, 24, 3), (100, 1040, 2), (5, 2048, 4)])
+@pytest.mark.parametrize("T,d,k", [(37, 24, 3), (100, 1040, 2), (5, 2048, 4),
+                                   (29, 64, 8), (50, 128, 7)])  # every slot order of the sorting network
 def test_combine_entry_direct(T, d, k):
     """smaul_moe_combine on its own (16 columns per thread, or 8 when d % 16
     != 0): ascending expert order, fp32 sum from +0 of rounded products,
