@@ -545,6 +545,7 @@ def test_moe_forward_norm(T, d, h, E, k, dtype, weighted):
     (300, 256, 640, 8, 2, 6, 2, torch.bfloat16),    # prefill path, ragged last 16-token block, E < EMAX
     (33, 192, 320, 4, 3, 4, 3, torch.float32),      # fp32: the next router runs as its own kernel
     (5, 4160, 128, 4, 2, 4, 2, torch.bfloat16),     # d > 4096: combine, norm, router kernels
+    (7, 512, 384, 4, 2, 8, 3, torch.bfloat16),      # one partial 16-token block, fused router
 ])
 def test_moe_forward_chain(T, d, h, E, k, nE, nk, dtype):
     """Two chained layers: layer A routes its normalised output with layer B's
