@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """MoE-layer benchmark on one MI355X (BASELINE.json metric).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--no-c5] [--no-c2]
 
 Headline (``value``): tokens/s of one SmaulMoE layer at config 3 -- prefill,
 T=16384 tokens, d=1024, expert hidden h=2560, E=8 experts, top-2, tile 64,
@@ -10,14 +10,20 @@ bf16 activations, router bias N(0, 0.5).  A step is one full layer forward
 combine) over inputs already resident in HBM.
 
 Extra objects on the same JSON line:
-- ``roofline``: the dominant kernel (the gate/up grouped GEMM), algorithmic
-  FLOPs per launch / its mean duration from HIP events on the launch stream,
-  against the bf16 dense MFMA peak;
+- ``roofline``: the dominant kernel (the gate/up grouped GEMM): algorithmic
+  FLOPs per launch / its mean duration, from HIP events recorded on the
+  stream it is launched on, around each launch inside a full layer;
+  ``traffic`` is the calibrated HBM bytes per launch read from the committed
+  rocprofv3 summary profiles/gate_up_c3_traffic.txt (not measured in this run);
 - ``cpu_baseline``: the reference CPU path on this host's cores -- the
   reference's own fp8_cpu.cpp (built under oracle/_ref) inside the torch MoE
-  loop of model.py:557-585 -- on a bounded sample of the same tokens;
+  loop of model.py:557-585 -- on bounded samples of the config-3 and config-5
+  tokens, at the process's affinity core count and at the reference default
+  max(1, cpu_count // 2) threads (kernel/compute.py:86), median of 3 runs;
 - ``decode``: config 4 (64 tokens x 24 MoE layers), one step replayed as a HIP
-  graph, with achieved HBM bytes/s against the 8 TB/s peak.
+  graph, with achieved HBM bytes/s against the 8 TB/s peak;
+- ``c5``: config 5 (the large skewed layer, T=65536 d=2048 h=5120 E=16);
+- ``c2``: config 2 (one dense SwiGLU FFN, 4096 x 512 -> 2 x 1280 -> 512).
 Only one GPU is measured: ``--gpus`` above 1 exits with a message.
 """
 from __future__ import annotations
@@ -25,6 +31,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -38,6 +45,11 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def quantized(w):
+    from smaulnative_amd.fp8_tile import quantize_tiles
+    return quantize_tiles(w, 64)
+
+
 def make_layer(seed, T, d, h, E, bias_std, device, gen_device="cpu"):
     """Config-3 style synthetic layer: x, router W/b, E experts as tiled E4M3.
 
@@ -45,7 +57,6 @@ def make_layer(seed, T, d, h, E, bias_std, device, gen_device="cpu"):
     gate, up and down weights, each N(0, 0.02).
     """
     import torch
-    from smaulnative_amd.fp8_tile import quantize_tiles
     gen = torch.Generator(device=gen_device).manual_seed(seed)
     x = torch.randn(T, d, generator=gen, device=gen_device)
     gw = torch.randn(E, d, generator=gen, device=gen_device) * 0.02
@@ -54,13 +65,35 @@ def make_layer(seed, T, d, h, E, bias_std, device, gen_device="cpu"):
     for _ in range(E):
         parts = []
         for (o, i) in ((h, d), (h, d), (d, h)):
-            w8, sc = quantize_tiles(torch.randn(o, i, generator=gen, device=gen_device) * 0.02, 64)
-            parts += [w8, sc]
+            parts += list(quantized(torch.randn(o, i, generator=gen, device=gen_device) * 0.02))
         experts.append(tuple(parts))
     return x.to(torch.bfloat16), gw, gb, experts
 
 
-def time_prefill(be, xd, gwd, gbd, exd, k, steps, warmup):
+def make_c5():
+    """Config 5: x and router W from the committed seed, the bisection-set skew
+    bias (tests/golden/c5_skew.json), experts drawn and quantized on the device."""
+    import torch
+    cfg = json.load(open(os.path.join(HERE, "tests", "golden", "c5_skew.json")))
+    T, d, h, E = 65536, 2048, 5120, 16
+    gen = torch.Generator().manual_seed(cfg["seed"])
+    x = torch.randn(T, d, generator=gen).to(torch.bfloat16)
+    gw = torch.randn(E, d, generator=gen) * 0.02
+    gb = torch.zeros(E)
+    gb[0] = cfg["beta_hi"]
+    for e in (13, 14, 15):
+        gb[e] = -cfg["beta_lo"]
+    gdev = torch.Generator(device="cuda").manual_seed(cfg["seed"])
+    experts = []
+    for _ in range(E):
+        parts = []
+        for (o, i) in ((h, d), (h, d), (d, h)):
+            parts += list(quantized(torch.randn(o, i, generator=gdev, device="cuda") * 0.02))
+        experts.append(tuple(parts))
+    return x, gw, gb, experts
+
+
+def time_layer(be, xd, gwd, gbd, exd, k, steps, warmup):
     import torch
     for _ in range(warmup):
         be.moe_forward(xd, gwd, gbd, exd, k, 64)
@@ -73,53 +106,151 @@ def time_prefill(be, xd, gwd, gbd, exd, k, steps, warmup):
     return (t1 - t0) / steps, out
 
 
-def time_stages(be, xd, gwd, gbd, exd, k, steps):
+def time_stages(be, xd, gwd, gbd, exd, k, steps, warmup=2):
     """Mean per-stage device time from HIP events on the launch stream."""
     import torch
     names = ["router", "dispatch", "gate_up", "down", "combine"]
     acc = [0.0] * 5
-    for it in range(steps + 2):
+    for it in range(steps + warmup):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
         be.moe_stages(xd, gwd, gbd, exd, k, 64, events=ev)
         torch.cuda.synchronize()
-        if it >= 2:
+        if it >= warmup:
             for i in range(5):
                 acc[i] += ev[i].elapsed_time(ev[i + 1])
     return {n: a / steps for n, a in zip(names, acc)}
 
 
-def cpu_baseline(x, gw, gb, experts, k, target_s=10.0):
-    """Reference CPU path on a bounded token sample (tokens are independent)."""
+def layer_flops(T, d, h, E, k):
+    R = T * k
+    return {"router": 2.0 * T * d * E, "gate_up": 2.0 * R * d * (2 * h), "down": 2.0 * R * h * d}
+
+
+def c5_bench(be, steps, warmup):
+    """Config 5: one layer of T=65536 d=2048 h=5120 E=16 top-2 with the skewed router."""
+    import torch
+    T, d, h, E, k = 65536, 2048, 5120, 16, 2
+    x, gw, gb, exd = make_c5()
+    xd, gwd, gbd = x.to("cuda"), gw.to("cuda"), gb.to("cuda")
+    sec, out = time_layer(be, xd, gwd, gbd, exd, k, steps, warmup)
+    counts = out[3].cpu().tolist()
+    stages = time_stages(be, xd, gwd, gbd, exd, k, max(3, steps // 2))
+    fl = layer_flops(T, d, h, E, k)
+    tot = sum(fl.values())
+    res = {"workload": "C5 skewed MoE layer: T=65536 d=2048 h=5120 E=16 top-2 tile 64, bf16, router bias "
+                       "+beta_hi on expert 0 and -beta_lo on experts 13-15 (tests/golden/c5_skew.json)",
+           "tokens_per_s": T / sec, "ms_per_step": sec * 1e3, "layer_tflops": tot / sec / 1e12,
+           "layer_mfma_frac": tot / sec / PEAK_BF16_FLOPS, "expert_token_counts": counts,
+           "share_e0": counts[0] / (T * k), "stages_ms": stages,
+           "gate_up_mfma_frac": fl["gate_up"] / (stages["gate_up"] * 1e-3) / PEAK_BF16_FLOPS,
+           "down_mfma_frac": fl["down"] / (stages["down"] * 1e-3) / PEAK_BF16_FLOPS}
+    cpu_inputs = (x, gw, gb, exd)
+    return res, cpu_inputs
+
+
+def c2_bench(be, steps, warmup):
+    """Config 2: one dense SwiGLU FFN, 4096 x 512 -> 2 x 1280 (gate+up, one launch) -> 512."""
+    import torch
+    rows, d, h = 4096, 512, 1280
+    gen = torch.Generator().manual_seed(1234 + 1)
+    x = torch.randn(rows, d, generator=gen).to(torch.bfloat16).to("cuda")
+    bufs = []
+    for (o, i) in ((h, d), (h, d), (d, h)):
+        bufs += [t.to("cuda") for t in quantized(torch.randn(o, i, generator=gen) * 0.02)]
+    bufs = tuple(bufs)
+    for _ in range(warmup):
+        be.swiffn_forward(x, bufs, 64)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = max(steps, 50)
+    ev0.record(stream)
+    for _ in range(n):
+        be.swiffn_forward(x, bufs, 64)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / n
+    flops = 6.0 * rows * d * h
+    return {"workload": "C2 dense SwiGLU FFN: 4096 x 512 -> 2 x 1280 (fused gate+up) -> 512, bf16, tile 64",
+            "tokens_per_s": rows / (ms * 1e-3), "ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+            "mfma_frac": flops / (ms * 1e-3) / PEAK_BF16_FLOPS, "flops_per_step": flops,
+            "timing": f"HIP events around {n} back-to-back calls on the launch stream"}
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def cpu_time_moe(x, gw, gb, experts, k, threads, target_s, max_tokens):
+    """Median of 3 timed passes of the reference CPU path over the first n tokens,
+    n sized so that one pass takes about target_s (benchmark.py:51-59 method)."""
     import torch
     import oracle
-    cores = oracle.default_threads()
-    torch.set_num_threads(cores)
-    os.environ["OMP_NUM_THREADS"] = str(cores)
+    torch.set_num_threads(threads)
+    os.environ["OMP_NUM_THREADS"] = str(threads)
     ref = oracle.ref_module()
     gemm = oracle.fp8_forward_ref if ref is not None else (
-        lambda xx, w, s, i, o, t: oracle.fp8_forward(xx, w, s, i, o, t, threads=cores))
+        lambda xx, w, s, i, o, t: oracle.fp8_forward(xx, w, s, i, o, t, threads=threads))
     kind = "reference" if ref is not None else "port"
     ow = [oracle.ExpertWeights(*e) for e in experts]
-    oracle.moe_forward(x[:64], gw, gb, ow, k, 64, gemm=gemm)  # warm-up
-    n = 512
+    n = 64
     t0 = time.perf_counter()
-    oracle.moe_forward(x[:n], gw, gb, ow, k, 64, gemm=gemm)
+    oracle.moe_forward(x[:n], gw, gb, ow, k, 64, gemm=gemm)  # warm-up and size probe
     dt = time.perf_counter() - t0
-    if dt < target_s / 4 and n < x.shape[0]:
-        n = int(min(x.shape[0], max(n, n * target_s / max(dt, 1e-3))))
+    n = int(min(max_tokens, max(n, n * target_s / max(dt, 1e-4))))
+    runs = []
+    for _ in range(3):
         t0 = time.perf_counter()
         oracle.moe_forward(x[:n], gw, gb, ow, k, 64, gemm=gemm)
-        dt = time.perf_counter() - t0
-    what = ("reference kernel/fp8_cpu.cpp (oracle/_ref) in the model.py:557-585 torch MoE loop"
-            if kind == "reference" else "C restatement of fp8_cpu.cpp in the model.py:557-585 MoE loop")
-    return {"value": n / dt, "unit": "tokens/s", "cores": cores, "kind": kind,
-            "sample": f"first {n} of the config-3 tokens, one pass, {dt:.2f} s; {what}"}
+        runs.append(time.perf_counter() - t0)
+    med = statistics.median(runs)
+    return {"tokens_per_s": n / med, "tokens": n, "median_s": med, "threads": threads}, kind
+
+
+def cpu_baseline(c3_inputs, c5_inputs, k, target_s=2.5):
+    """The reference CPU path on this host, config 3 (headline) and config 5 samples."""
+    import torch
+    import oracle
+    aff = oracle.default_threads()
+    dflt = max(1, (os.cpu_count() or 2) // 2)
+    x, gw, gb, experts = c3_inputs
+    main, kind = cpu_time_moe(x, gw, gb, experts, k, aff, target_s, x.shape[0])
+    res = {"value": main["tokens_per_s"], "unit": "tokens/s", "cores": aff, "kind": kind,
+           "sample": f"first {main['tokens']} of the config-3 tokens, median of 3 passes of "
+                     f"{main['median_s']:.2f} s; "
+                     + ("reference kernel/fp8_cpu.cpp (oracle/_ref)" if kind == "reference"
+                        else "C restatement of fp8_cpu.cpp") + " in the model.py:557-585 torch MoE loop",
+           "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count()}
+    if dflt != aff:
+        alt, _ = cpu_time_moe(x, gw, gb, experts, k, dflt, target_s, x.shape[0])
+        res["at_reference_default_threads"] = alt
+    else:
+        res["at_reference_default_threads"] = dict(main)
+    if c5_inputs is not None:
+        x5, gw5, gb5, ex5 = c5_inputs
+        ex5 = [tuple(t.cpu() for t in e) for e in ex5]
+        c5 = {}
+        for th in sorted({aff, dflt}):
+            r, _ = cpu_time_moe(x5, gw5, gb5, ex5, k, th, target_s, x5.shape[0])
+            c5[str(th)] = r
+        res["c5"] = c5
+    torch.set_num_threads(aff)
+    return res
 
 
 def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
     """Config 4: 64 tokens through 24 stacked MoE layers (independent weights, each
     layer fed the unit-RMS-normalised output of the one before), one HIP graph
-    replay per step."""
+    replay per step.  Timed twice: chained (each layer's router inside the
+    previous layer's combine + norm kernel) and unchained (every layer routes
+    its own input with a router kernel)."""
     import torch
     dev = torch.device("cuda")
     lay = []
@@ -131,9 +262,8 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
     x0 = (x0.float() * torch.rsqrt(x0.float().pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
 
     def step(chained=True):
-        # layer l + 1 reads layer l's output after a unit-RMS row norm (Block's
-        # norm around the FFN, model.py:636), so the 24 layers form one chain;
-        # chained: layer l + 1's router runs inside layer l's combine + norm
+        # layer l + 1 reads layer l's output after a unit-RMS row norm (a stand-in
+        # for the norms of the Block around its FFN), so the 24 layers form one chain
         outs = []
         xl = x0
         routing = None
@@ -151,25 +281,29 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
     chain_ok = all(torch.equal(a[0], b[0]) and torch.equal(a[4], b[4]) for a, b in zip(eager, plain))
     del plain
     counts = [o[3].cpu() for o in eager]
-    g = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        step()  # warm the caches of the capture stream
+
+    def graph_time(chained):
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step(chained)  # warm the caches of the capture stream
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                gouts = step(chained)
         torch.cuda.synchronize()
-        with torch.cuda.graph(g, stream=s):
-            gouts = step()
-    torch.cuda.synchronize()
-    for _ in range(max(1, warmup)):
-        g.replay()
-    torch.cuda.synchronize()
-    ok = all(torch.equal(a[0], b[0]) for a, b in zip(eager, gouts))
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        g.replay()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / steps
-    # eager (no graph) for reference
+        for _ in range(max(1, warmup)):
+            g.replay()
+        torch.cuda.synchronize()
+        ok = all(torch.equal(a[0], b[0]) for a, b in zip(eager, gouts))
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps, ok
+
+    dt, ok = graph_time(True)
+    dt_plain, ok_plain = graph_time(False)
     t0 = time.perf_counter()
     for _ in range(max(1, steps // 4)):
         step()
@@ -181,12 +315,14 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
         executed = int((c > 0).sum())
         nbytes += executed * expert_bytes + 4 * E * d + 2 * T * d * 2
     return {"workload": "C4 decode: 64 tokens x 24 chained MoE layers (unit-RMS norm between layers, each "
-                        "layer's router fused into the previous layer's combine + norm), d=1024 h=2560 E=8 "
-                        "top-2, HIP graph replay",
+                        "layer's router fused into the previous layer's combine + norm -- a fusion this "
+                        "harness allows because it feeds the norm output straight to the next layer), "
+                        "d=1024 h=2560 E=8 top-2, HIP graph replay",
             "tokens_per_s": T / dt, "ms_per_step": dt * 1e3, "ms_per_step_eager": dt_eager * 1e3,
+            "ms_per_step_unchained": dt_plain * 1e3,
             "bytes_per_step": nbytes, "hbm_GBps": nbytes / dt / 1e9,
-            "hbm_frac": nbytes / dt / PEAK_HBM_BPS, "graph_matches_eager": ok,
-            "chain_matches_unfused": chain_ok}
+            "hbm_frac": nbytes / dt / PEAK_HBM_BPS, "hbm_frac_unchained": nbytes / dt_plain / PEAK_HBM_BPS,
+            "graph_matches_eager": ok and ok_plain, "chain_matches_unfused": chain_ok}
 
 
 def read_traffic():
@@ -210,6 +346,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-c5", action="store_true")
+    ap.add_argument("--no-c2", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 3 device-to-device copies of BYTES (calibrates rocprofv3 "
                          "FETCH_SIZE/WRITE_SIZE against a kernel of known traffic), then exit")
@@ -244,20 +382,21 @@ def main():
     exd = [tuple(t.to(dev) for t in e) for e in experts]
 
     log("bench: timing prefill layer")
-    sec, out = time_prefill(be, xd, gwd, gbd, exd, k, args.steps, args.warmup)
+    sec, out = time_layer(be, xd, gwd, gbd, exd, k, args.steps, args.warmup)
     counts = out[3].cpu().tolist()
-    stages = time_stages(be, xd, gwd, gbd, exd, k, max(3, args.steps // 2))
+    n_stage = max(3, args.steps // 2)
+    stages = time_stages(be, xd, gwd, gbd, exd, k, n_stage)
     log("bench: stages ms", {kk: round(v, 4) for kk, v in stages.items()})
-    R = T * k
-    flops_router = 2.0 * T * d * E
-    flops_gate_up = 2.0 * R * d * (2 * h)
-    flops_down = 2.0 * R * h * d
-    total_flops = flops_router + flops_gate_up + flops_down
+    fl = layer_flops(T, d, h, E, k)
+    total_flops = sum(fl.values())
     gu_s = stages["gate_up"] * 1e-3
     roof = {"kernel": "fp8_gemm_dma_kernel (gate_up, SwiGLU epilogue)", "bound": "mfma",
-            "achieved": flops_gate_up / gu_s / 1e12, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
-            "frac": flops_gate_up / gu_s / PEAK_BF16_FLOPS, "traffic": read_traffic(),
-            "flops_per_launch": flops_gate_up, "mean_launch_ms": stages["gate_up"]}
+            "achieved": fl["gate_up"] / gu_s / 1e12, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
+            "frac": fl["gate_up"] / gu_s / PEAK_BF16_FLOPS, "traffic": read_traffic(),
+            "flops_per_launch": fl["gate_up"], "mean_launch_ms": stages["gate_up"],
+            "timing": f"HIP events on the launch stream around the gate_up launch of {n_stage} full layers "
+                      "(after 2 untimed layers), mean",
+            "traffic_source": "profiles/gate_up_c3_traffic.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)"}
     res = {
         "metric": METRIC,
         "value": T / sec,
@@ -280,16 +419,29 @@ def main():
         "stages_ms": stages,
         "roofline": roof,
     }
+    c5_inputs = None
+    if not args.no_c5:
+        log("bench: config 5")
+        try:
+            res["c5"], c5_inputs = c5_bench(be, max(5, args.steps // 2), 2)
+        except Exception as exc:  # report, keep the headline
+            res["c5"] = {"error": f"{type(exc).__name__}: {exc}"}
+    if not args.no_c2:
+        log("bench: config 2")
+        try:
+            res["c2"] = c2_bench(be, args.steps, args.warmup)
+        except Exception as exc:
+            res["c2"] = {"error": f"{type(exc).__name__}: {exc}"}
     if not args.no_decode:
         log("bench: decode (config 4)")
         try:
             res["decode"] = decode_bench(be, max(5, args.steps), args.warmup)
-        except Exception as exc:  # report, keep the headline
+        except Exception as exc:
             res["decode"] = {"error": f"{type(exc).__name__}: {exc}"}
     if not args.no_cpu:
         log("bench: CPU baseline")
         try:
-            res["cpu_baseline"] = cpu_baseline(x, gw, gb, experts, k)
+            res["cpu_baseline"] = cpu_baseline((x, gw, gb, experts), c5_inputs, k)
         except Exception as exc:
             res["cpu_baseline"] = {"error": f"{type(exc).__name__}: {exc}"}
     print(json.dumps(res), flush=True)

@@ -154,6 +154,25 @@ int smaul_moe_combine(const void* yperm, int act_dtype, const int64_t* topi,
                       int64_t d, int64_t k, hipStream_t stream);
 
 /*
+ * Dense SwiGLU FFN over every row: out = cast(cast(silu(cast(x . Wg^T)) *
+ * cast(x . Wu^T)) . Wd^T), cast to act_dtype at each point (a no-op for
+ * fp32) -- SwiFFN.forward, model.py:289-290, with its three FP8Linear
+ * forwards (kernel/fp8_tile.py:237-239, 163-170).  One launch computes gate
+ * and up together with the SwiGLU epilogue into the workspace (hdn [rows, h]),
+ * a second the down projection into out.  x: act_dtype [rows, d]; gate/up
+ * codes uint8 [h, d] with fp32 scales [h, ceil(d/tile)]; down codes [d, h],
+ * scales [d, ceil(h/tile)]; out: act_dtype [rows, d].  x, codes, out and the
+ * workspace 16-byte aligned; d and h multiples of 16.  `workspace` holds
+ * smaul_swiffn_workspace_size(rows, h, act_dtype) bytes.
+ */
+int64_t smaul_swiffn_workspace_size(int64_t rows, int64_t h, int act_dtype);
+
+int smaul_swiffn_forward(const void* x, int act_dtype, const uint8_t* gate_w8, const float* gate_s,
+                         const uint8_t* up_w8, const float* up_s, const uint8_t* down_w8, const float* down_s,
+                         void* out, void* workspace, int64_t workspace_bytes, int64_t rows, int64_t d, int64_t h,
+                         int64_t tile, int flags, hipStream_t stream);
+
+/*
  * RMSNorm over the rows of x [T, d]: out = cast((x * rsqrt(mean(x^2) + eps)) *
  * weight) computed in fp32, out in act_dtype (model.py:124-139, RMSNorm.forward;
  * Block applies it to every MoE output, model.py:636).  weight: fp32 [d], or

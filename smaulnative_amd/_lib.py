@@ -49,6 +49,8 @@ SIGNATURES = {
     "smaul_moe_forward_chain": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                      _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, ctypes.c_float, _P, _I,
                                      _P, _P, _I64, _I64, _P, _P, _P, _P]),
+    "smaul_swiffn_workspace_size": (_I64, [_I64, _I64, _I]),
+    "smaul_swiffn_forward": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P]),
     "smaul_selftest_topk": (_I, [_P, _I64, _I64, _P]),
 }
 

@@ -175,10 +175,7 @@ struct GemmCfg {
   static_assert(B_CH >= 1 && (BNB * 4) % NT == 0, "B staging split");
 };
 
-#ifndef SMAUL_GROUP_M
-#define SMAUL_GROUP_M 8
-#endif
-constexpr int GROUP_M = SMAUL_GROUP_M;
+constexpr int GROUP_M = 8;
 
 template <int BM, int BNB, int WM, int WN, int MT, bool REMAP, bool SWIGLU, int NSPLIT, bool OUT_BF16,
           int KMODE, bool CANON, bool VEC>
@@ -892,33 +889,14 @@ fp8_gemm_dma_kernel(GemmArgs p) {
 }
 
 // Launch configurations: (rows, staged weight rows, wave grid) per workgroup.
-#ifndef SMAUL_BIG_BM
-#define SMAUL_BIG_BM 128
-#endif
-#ifndef SMAUL_BIG_BNB
-#define SMAUL_BIG_BNB 128
-#endif
-#ifndef SMAUL_BIG_WM
-#define SMAUL_BIG_WM 2
-#endif
-#ifndef SMAUL_BIG_WN
-#define SMAUL_BIG_WN 2
-#endif
-#ifndef SMAUL_BIG_MT
-#define SMAUL_BIG_MT 32
-#endif
-#ifndef SMAUL_REMAP
-#define SMAUL_REMAP 1
-#endif
 struct CfgBig {
-  static constexpr int BM = SMAUL_BIG_BM, BNB = SMAUL_BIG_BNB, WM = SMAUL_BIG_WM, WN = SMAUL_BIG_WN;
-  static constexpr int MT = SMAUL_BIG_MT;
-  static constexpr bool REMAP = SMAUL_REMAP;
+  static constexpr int BM = 128, BNB = 128, WM = 2, WN = 2, MT = 32;
+  static constexpr bool REMAP = true;
 };
 // fp32 activations stage two bf16 planes of A, so they keep a 128-row tile
 struct CfgBigF32 {
   static constexpr int BM = 128, BNB = 128, WM = 2, WN = 2, MT = 16;
-  static constexpr bool REMAP = SMAUL_REMAP;
+  static constexpr bool REMAP = true;
 };
 struct CfgSmall {
   static constexpr int BM = 32, BNB = 128, WM = 1, WN = 4, MT = 16;
@@ -2122,15 +2100,6 @@ int ds_kbw(int64_t nkb, bool swiglu) {
   return 0;
 }
 
-// SMAUL_DECODE=split runs decode_gemm_kernel for every decode GEMM (A/B timing)
-bool decode_stream_enabled() {
-  static const bool on = [] {
-    const char* v = getenv("SMAUL_DECODE");
-    return !(v && strcmp(v, "split") == 0);
-  }();
-  return on;
-}
-
 // compute units of the current device (cached per device)
 int cu_count() {
   static int cached[64] = {0};
@@ -2177,7 +2146,7 @@ int launch_decode_stream(const GemmArgs& a, const DsDispatch* dd, hipStream_t st
 template <bool SWIGLU, bool CANON>
 int launch_decode(const GemmArgs& a, hipStream_t stream) {
   if (SWIGLU != (a.row_idx != nullptr)) return fail(SMAUL_ERR_INVALID, "decode gemm: row gather mismatch");
-  if (decode_stream_enabled()) {
+  {
     const int rc = launch_decode_stream<SWIGLU, CANON>(a, nullptr, stream);
     if (rc != 1) return rc;
   }
@@ -2465,7 +2434,8 @@ dispatch_scatter_kernel(const int64_t* __restrict__ topi, const float* __restric
 // (integer sums: the offsets of dispatch_scan_kernel), block 0 writes counts,
 // seg_off and tile_off, and the scatter follows as in dispatch_scatter_kernel.
 // The count reads are issued with the token's top-k reads, so the scan costs
-// no round trip of its own.
+// no round trip of its own.  Launched only for nb <= SCAN_FUSED_CHUNKS * 64
+// blocks (the unrolled count reads cover every block).
 constexpr int SCAN_FUSED_CHUNKS = 4;  // count reads unrolled for up to 4 * 64 blocks
 template <int EMAX>
 __global__ void __launch_bounds__(64)
@@ -2504,10 +2474,6 @@ dispatch_scan_scatter_kernel(const int64_t* __restrict__ topi, const float* __re
   for (int c = 0; c < SCAN_FUSED_CHUNKS; ++c)
 #pragma unroll
     for (int e = 0; e < EMAX; ++e) add_block(c * 64 + lane, cv[c][e], e);
-  for (int64_t b = SCAN_FUSED_CHUNKS * 64 + lane; b < nb; b += 64)
-#pragma unroll
-    for (int e = 0; e < EMAX; ++e)
-      if (e < E) add_block(b, blockcnt[b * E + e], e);
 #pragma unroll
   for (int e = 0; e < EMAX; ++e)
 #pragma unroll
@@ -2537,17 +2503,18 @@ dispatch_scan_scatter_kernel(const int64_t* __restrict__ topi, const float* __re
   const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
   for (int e = 0; e < EMAX; ++e) {
-    if (e >= E) break;
-    const uint64_t b = __ballot((sel >> e) & 1ull);
-    if ((sel >> e) & 1ull) {
-      const int pos = segoff[e] + before[e] + __popcll(b & lt);
-      perm_row[pos] = (int32_t)t;
-      for (int j = 0; j < k; ++j)
-        if (ti[j] == e && tw[j] > 0.0f) {
-          perm_w[pos] = tw[j];
-          inv[t * k + j] = pos;
-          break;
-        }
+    if (e < E) {  // uniform: every lane takes part in the ballot
+      const uint64_t b = __ballot((sel >> e) & 1ull);
+      if ((sel >> e) & 1ull) {
+        const int pos = segoff[e] + before[e] + __popcll(b & lt);
+        perm_row[pos] = (int32_t)t;
+        for (int j = 0; j < k; ++j)
+          if (ti[j] == e && tw[j] > 0.0f) {
+            perm_w[pos] = tw[j];
+            inv[t * k + j] = pos;
+            break;
+          }
+      }
     }
   }
   if (valid) {
@@ -3069,7 +3036,6 @@ constexpr int DECODE_BM = 16;
 
 bool decode_shape_ok(int64_t d, int64_t h, int64_t tile) { return tile == 64 && d % 128 == 0 && h % 128 == 0; }
 
-bool dma_gemm_enabled();
 
 int pick_block_m(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile, int act_dtype) {
   if (T <= 64 && act_dtype == SMAUL_DTYPE_BF16 && decode_shape_ok(d, h, tile)) return DECODE_BM;
@@ -3129,16 +3095,6 @@ int launch_gemm_dma(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
   hipLaunchKernelGGL((fp8_gemm_dma_kernel<CF::BM, CF::BN, CF::WM, CF::WN, CF::NSTAGE, SWIGLU, CANON, true>),
                      dim3((unsigned)n_tiles, (unsigned)m_tiles), dim3(CF::WM * CF::WN * 64), 0, stream, a);
   return check_launch("fp8_gemm_dma_kernel");
-}
-
-// SMAUL_GEMM=legacy keeps the grouped GEMMs on the register-staged kernels
-// (for comparisons); anything else lets eligible shapes use them.
-bool dma_gemm_enabled() {
-  static const bool on = [] {
-    const char* v = getenv("SMAUL_GEMM");
-    return !(v && strcmp(v, "legacy") == 0);
-  }();
-  return on;
 }
 
 // The LDS-DMA kernel needs bf16 activations, 64-wide scale tiles, K a
@@ -3355,7 +3311,10 @@ static int launch_scan_scatter(const int64_t* topi, const float* topw, int32_t* 
                                int32_t* perm_row, float* perm_w, int32_t* inv, int64_t T, int64_t E,
                                int64_t k, int64_t block_m, int64_t tpb, hipStream_t stream) {
   const int64_t nb = (T + tpb - 1) / tpb;
-  if (E <= 16 && nb <= 65535) {  // one launch
+  // One launch while every block can sum all block counts from its unrolled
+  // reads (nb <= 256); past that each block would re-read nb * E counts, a
+  // cost growing with nb^2, so the scan runs once in its own kernel.
+  if (E <= 16 && nb <= SCAN_FUSED_CHUNKS * 64) {
 #define SMAUL_SCS(EMAX)                                                                                         \
   hipLaunchKernelGGL((dispatch_scan_scatter_kernel<EMAX>), dim3((unsigned)nb), dim3(64), 0, stream, topi, topw, \
                      blockcnt, counts, seg_off, tile_off, perm_row, perm_w, inv, T, (int)E, (int)k, (int)tpb, nb, \
@@ -3456,7 +3415,7 @@ static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* 
   // x and of hdn are both below max_tiles * block_m); the register-staged
   // kernels otherwise, on the same tile table
   static_assert(CfgDmaGU::BM == CfgBig::BM && CfgDmaDown::BM == CfgBig::BM, "one tile table for both kernels");
-  if (block_m == big_bm && dma_gemm_enabled() &&
+  if (block_m == big_bm &&
       dma_gemm_ok(a, act_dtype, flags, max_tiles * block_m, swiglu ? CfgDmaGU::BN / 2 : CfgDmaDown::BN)) {
     if (swiglu)
       return canon ? launch_gemm_dma<CfgDmaGU, true, true>(a, max_tiles, stream)
@@ -3486,6 +3445,82 @@ int smaul_moe_down(const void* hdn, int act_dtype, const uint8_t* const* down_w,
                    int64_t tile, int64_t block_m, int flags, hipStream_t stream) {
   return moe_gemm(false, hdn, act_dtype, nullptr, down_w, down_s, nullptr, nullptr, yperm, seg_off,
                   tile_off, max_tiles, E, h, d, tile, block_m, flags, stream);
+}
+
+// Dense SwiGLU FFN (one expert, every row): the grouped kernels in their
+// dense form (no segment table, no row gather).  gate and up run as one
+// launch with the SwiGLU epilogue into hdn (the workspace), then down writes
+// out directly.
+int64_t smaul_swiffn_workspace_size(int64_t rows, int64_t h, int act_dtype) {
+  if (rows < 0 || h <= 0 || !dtype_ok(act_dtype)) return -1;
+  return align256(rows * h * (act_dtype == SMAUL_DTYPE_BF16 ? 2 : 4));
+}
+
+static int dense_gemm(bool swiglu, const void* act, int act_dtype, const uint8_t* w1, const float* s1,
+                      const uint8_t* w2, const float* s2, void* out, int64_t rows, int64_t K, int64_t N,
+                      int64_t tile, int flags, hipStream_t stream) {
+  GemmArgs a{};
+  a.x = act;
+  a.row_idx = nullptr;
+  a.ldx = K;
+  a.w = w1;
+  a.s = s1;
+  a.w2 = w2;
+  a.s2 = s2;
+  a.y = out;
+  a.ldy = N;
+  a.K = K;
+  a.N = N;
+  a.nt = (K + tile - 1) / tile;
+  a.tile = tile;
+  a.seg_off = nullptr;
+  a.tile_off = nullptr;
+  a.R = rows;
+  a.E = 1;
+  const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
+  const int64_t bno = swiglu ? CfgDmaGU::BN / 2 : CfgDmaDown::BN;
+  if (dma_gemm_ok(a, act_dtype, flags | SMAUL_FLAG_ALIGNED_CODES, rows, bno)) {
+    const int64_t mt = (rows + CfgBig::BM - 1) / CfgBig::BM;
+    if (swiglu)
+      return canon ? launch_gemm_dma<CfgDmaGU, true, true>(a, mt, stream)
+                   : launch_gemm_dma<CfgDmaGU, true, false>(a, mt, stream);
+    return canon ? launch_gemm_dma<CfgDmaDown, false, true>(a, mt, stream)
+                 : launch_gemm_dma<CfgDmaDown, false, false>(a, mt, stream);
+  }
+  const bool small = rows <= 64;
+  if (act_dtype == SMAUL_DTYPE_BF16) {
+    const int64_t mt = (rows + (small ? CfgSmall::BM : CfgBig::BM) - 1) / (small ? CfgSmall::BM : CfgBig::BM);
+    return small ? gemm_dispatch_moe<CfgSmall, CfgSmall>(a, swiglu, act_dtype, mt, canon, stream)
+                 : gemm_dispatch_moe<CfgBig, CfgBigF32>(a, swiglu, act_dtype, mt, canon, stream);
+  }
+  const int64_t mt = (rows + (small ? CfgSmall::BM : CfgBigF32::BM) - 1) / (small ? CfgSmall::BM : CfgBigF32::BM);
+  return small ? gemm_dispatch_moe<CfgSmall, CfgSmall>(a, swiglu, act_dtype, mt, canon, stream)
+               : gemm_dispatch_moe<CfgBig, CfgBigF32>(a, swiglu, act_dtype, mt, canon, stream);
+}
+
+int smaul_swiffn_forward(const void* x, int act_dtype, const uint8_t* gate_w8, const float* gate_s,
+                         const uint8_t* up_w8, const float* up_s, const uint8_t* down_w8, const float* down_s,
+                         void* out, void* workspace, int64_t workspace_bytes, int64_t rows, int64_t d, int64_t h,
+                         int64_t tile, int flags, hipStream_t stream) {
+  if (!dtype_ok(act_dtype)) return fail(SMAUL_ERR_INVALID, "swiffn: activation dtype must be f32|bf16");
+  if (rows < 0 || d <= 0 || h <= 0 || tile <= 0)
+    return fail(SMAUL_ERR_INVALID, "swiffn: need rows >= 0 and positive d, h, tile");
+  if (kmode_of(tile) < 0) return fail(SMAUL_ERR_UNSUPPORTED, "swiffn: tile must be 32 or a multiple of 64");
+  if (d % 16 != 0 || h % 16 != 0) return fail(SMAUL_ERR_UNSUPPORTED, "swiffn: d and h must be multiples of 16");
+  const int64_t need = smaul_swiffn_workspace_size(rows, h, act_dtype);
+  if (workspace_bytes < need) return fail(SMAUL_ERR_INVALID, "swiffn: workspace %lld < %lld bytes",
+                                          (long long)workspace_bytes, (long long)need);
+  if (rows == 0) return SMAUL_OK;
+  if (!x || !gate_w8 || !gate_s || !up_w8 || !up_s || !down_w8 || !down_s || !out || !workspace)
+    return fail(SMAUL_ERR_INVALID, "swiffn: null pointer");
+  if (!aligned16(x) || !aligned16(out) || !aligned16(workspace) || !aligned16(gate_w8) || !aligned16(up_w8) ||
+      !aligned16(down_w8))
+    return fail(SMAUL_ERR_UNSUPPORTED, "swiffn: x, codes, out and workspace must be 16-byte aligned");
+  if (rows * (h > d ? h : d) > 2147483647LL) return fail(SMAUL_ERR_UNSUPPORTED, "swiffn: rows * width exceeds int32");
+  int rc = dense_gemm(true, x, act_dtype, gate_w8, gate_s, up_w8, up_s, workspace, rows, d, h, tile, flags, stream);
+  if (rc) return rc;
+  return dense_gemm(false, workspace, act_dtype, down_w8, down_s, nullptr, nullptr, out, rows, h, d, tile, flags,
+                    stream);
 }
 
 int smaul_moe_combine(const void* yperm, int act_dtype, const int64_t* topi, const float* topw,
@@ -3681,7 +3716,7 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
 
   const int64_t bm = pick_block_m(T, d, h, E, k, tile, act_dtype);
   // decode regime: the gate/up kernel dispatches for itself
-  const bool fused = bm == DECODE_BM && decode_stream_enabled() && aligned16(x) && h % 16 == 0 &&
+  const bool fused = bm == DECODE_BM && aligned16(x) && h % 16 == 0 &&
                      ds_kbw(d / 64, true) != 0;
   RouteOut o{};
   o.prob = prob;

@@ -63,6 +63,10 @@ class SwiFFN(nn.Module):
         self.down = FP8Linear(h, cfg.d_model, cfg.tile)
 
     def forward(self, x):
+        be = get_backend()
+        if hasattr(be, "swiffn_forward") and not (torch.is_grad_enabled() and self.training):
+            xf = x if x.is_floating_point() else x.float()
+            return be.swiffn_forward(xf, self.buffers6(), self.gate.tile)
         odt = x.dtype if x.is_floating_point() else torch.float32
         return self.down((F.silu(self.gate(x).float()) * self.up(x).float()).to(odt))
 

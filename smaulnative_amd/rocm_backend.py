@@ -22,9 +22,10 @@ Behaviour differences from the reference CPU backend, all deliberate:
 """
 from __future__ import annotations
 
-import os
 import math
+import os
 import threading
+import weakref
 from typing import Sequence
 
 import torch
@@ -36,6 +37,12 @@ _ACT = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
 
 def _stream_handle(device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def _call_weak(method_ref, *args):
+    m = method_ref()
+    if m is not None:
+        m(*args)
 
 
 def _need_device(name: str, *tensors):
@@ -155,23 +162,25 @@ class RocmBackend:
         raise NotImplementedError("rocm backend: sparse_grad_v is not implemented")
 
     # ---- MoE (model.py:557-585) -------------------------------------------
-    def _expert_table(self, experts: Sequence[Sequence[torch.Tensor]], device, d, h, tile):
-        """Device int64 [6, E] table of the experts' buffer addresses (a repack cache).
+    def _expert_entry(self, experts: Sequence[Sequence[torch.Tensor]], device, d, h, tile):
+        """The repack cache entry of a set of experts: ``table``, a device int64
+        [6, E] table of the experts' buffer addresses, and ``ptrs``, the same
+        addresses as host ints.
 
         Rows: gate codes, gate scales, up codes, up scales, down codes, down
         scales.  The code rows point at *canonical copies* of the ``w8``
         buffers (0x7F/0xFF rewritten to 0x7E/0xFE, the same +-448 values) so
         the GEMMs can use the hardware E4M3 converter directly; the stored
-        ``w8`` buffers are never modified.  Non-fp32 scales (a model cast to
-        bf16) are widened into cached copies.
+        ``w8`` buffers are never modified.  fp32 contiguous scales are used in
+        place; other scales (a model cast to bf16) are widened into copies.
 
-        The cache is keyed on the buffers' addresses.  When a buffer's
-        ``_version`` changes (requant, ``copy_``), the copies are refreshed in
-        place on the current stream, so the table -- and any HIP graph that
-        captured it -- keeps pointing at valid, current data.  Entries whose
-        source buffers have been freed are dropped.
+        The cache is keyed on the buffers' addresses and holds only weak
+        references to them.  When a buffer's ``_version`` changes (requant,
+        ``copy_``), the copies are refreshed in place on the current stream,
+        so the table -- and any HIP graph that captured it -- keeps pointing
+        at valid, current data.  When any of the buffers is freed, its entry
+        (and the copies it owns, one byte per weight) is dropped at once.
         """
-        import weakref
         lib = _lib.load()
         flat = []
         for ex in experts:
@@ -180,12 +189,13 @@ class RocmBackend:
             flat.extend(ex)
         key = (str(device), d, h, tile, tuple(t.data_ptr() for t in flat))
         versions = tuple(t._version for t in flat)
-        ent = self._ptr_cache.get(key)
-        if ent is not None and all(r() is not None for r in ent["refs"]):
+        with self._lock:
+            ent = self._ptr_cache.get(key)
+        if ent is not None and all(r() is t for r, t in zip(ent["refs"], flat)):
             if ent["versions"] != versions:
                 self._refresh(ent, flat, lib, device)
                 ent["versions"] = versions
-            return ent["table"]
+            return ent
         nt_d = (d + tile - 1) // tile
         nt_h = (h + tile - 1) // tile
         shapes = [(h, d), (h, nt_d), (h, d), (h, nt_d), (d, h), (d, nt_h)]
@@ -204,20 +214,27 @@ class RocmBackend:
         self._refresh(ent, flat, lib, device)
         E = len(experts)
         rows = [[0] * E for _ in range(6)]
-        for n in range(len(flat)):
+        for n, t in enumerate(flat):
             e, idx = divmod(n, 6)
-            rows[idx][e] = ent["copies"][n].data_ptr()
+            src = ent["copies"][n]
+            rows[idx][e] = (src if src is not None else t).data_ptr()
+        ent["ptrs"] = rows
         ent["table"] = torch.tensor(rows, dtype=torch.int64).to(device)
         with self._lock:
-            dead = [k for k, v in self._ptr_cache.items() if any(r() is None for r in v["refs"])]
-            for k in dead:
-                del self._ptr_cache[k]
             self._ptr_cache[key] = ent
-        return ent["table"]
+        evict = weakref.WeakMethod(self._evict)
+        for t in flat:
+            weakref.finalize(t, _call_weak, evict, key, ent)
+        return ent
+
+    def _evict(self, key, ent):
+        with self._lock:
+            if self._ptr_cache.get(key) is ent:
+                del self._ptr_cache[key]
 
     @staticmethod
     def _refresh(ent, flat, lib, device):
-        """(Re)write the cached canonical codes and fp32 scales from the source buffers."""
+        """(Re)write the cached canonical codes and widened scales from the source buffers."""
         stream = _stream_handle(device)
         for n, t in enumerate(flat):
             if n % 2 == 0:
@@ -226,21 +243,58 @@ class RocmBackend:
                 with torch.cuda.device(device):
                     rc = lib.smaul_fp8_canonicalize(src.data_ptr(), dst.data_ptr(), src.numel(), stream)
                 _lib.check(rc, "fp8_canonicalize")
-            else:
-                if t.dtype == torch.float32 and t.is_contiguous():
-                    ent["copies"][n] = t
+            elif not (t.dtype == torch.float32 and t.is_contiguous()):
+                w = t.float().contiguous().reshape(-1)
+                if ent["copies"][n] is None:
+                    ent["copies"][n] = w
                 else:
-                    w = t.float().contiguous()
-                    if ent["copies"][n] is None or ent["copies"][n] is t:
-                        ent["copies"][n] = w
-                    else:
-                        ent["copies"][n].copy_(w.reshape(ent["copies"][n].shape))
+                    ent["copies"][n].copy_(w)
+
+    def swiffn_forward(self, x, buffers, tile):
+        """SwiFFN.forward (model.py:289-290) on the device: one fused gate+up
+        launch with the SwiGLU epilogue, then the down projection.
+
+        x: [..., d] bf16 or fp32; buffers: (gate_w8, gate_sc, up_w8, up_sc,
+        down_w8, down_sc) as FP8Linear stores them.  Returns a new tensor of
+        x's dtype and shape, rounded at the points of the reference module
+        (each FP8Linear output and the SwiGLU product cast to x.dtype).
+        """
+        lib = _lib.load()
+        _need_device("swiffn_forward", x, *buffers)
+        if x.dtype not in _ACT:
+            raise RuntimeError(f"swiffn_forward: x must be float32 or bfloat16, got {x.dtype}")
+        if tile <= 0:
+            raise ValueError(f"tile must be > 0, got {tile}")
+        d = x.shape[-1]
+        h = buffers[0].shape[0]
+        x2 = x.reshape(-1, d)
+        x2 = x2 if x2.is_contiguous() else x2.contiguous()
+        rows = x2.shape[0]
+        dev = x.device
+        ptrs = self._expert_entry([buffers], dev, d, h, tile)["ptrs"]
+        out = torch.empty_like(x2)
+        ws_bytes = lib.smaul_swiffn_workspace_size(rows, h, _ACT[x.dtype])
+        ws = torch.empty(max(1, ws_bytes), dtype=torch.uint8, device=dev)
+        with torch.cuda.device(dev):
+            rc = lib.smaul_swiffn_forward(x2.data_ptr(), _ACT[x.dtype], *[ptrs[i][0] for i in range(6)],
+                                          out.data_ptr(), ws.data_ptr(), ws_bytes, rows, d, h, tile,
+                                          _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES, _stream_handle(dev))
+        _lib.check(rc, "swiffn_forward")
+        return out.reshape(x.shape)
 
     def moe_router(self, x2, gate_w, gate_b, top_k):
         """Router stage alone: (prob [T,E] fp32, topi [T,k] int64, topw [T,k] fp32)."""
         lib = _lib.load()
+        _need_device("moe_router", x2, gate_w, gate_b)
+        if x2.dtype not in _ACT or x2.dim() != 2:
+            raise RuntimeError(f"moe_router: x must be 2-D float32 or bfloat16, got {x2.dtype} {tuple(x2.shape)}")
         T, d = x2.shape
         E = gate_w.shape[0]
+        if gate_w.dim() != 2 or gate_w.shape[1] != d:
+            raise RuntimeError(f"moe_router: gate weight must be [E, {d}], got {tuple(gate_w.shape)}")
+        if gate_b is not None and gate_b.numel() != E:
+            raise RuntimeError(f"moe_router: gate bias must have {E} elements, got {gate_b.numel()}")
+        x2 = x2 if x2.is_contiguous() else x2.contiguous()
         prob = torch.empty(T, E, dtype=torch.float32, device=x2.device)
         topi = torch.empty(T, top_k, dtype=torch.int64, device=x2.device)
         topw = torch.empty(T, top_k, dtype=torch.float32, device=x2.device)
@@ -257,6 +311,11 @@ class RocmBackend:
     def moe_dispatch(self, topi, topw, num_experts, block_m=None):
         """Dispatch stage alone: dict of counts/seg_off/tile_off/perm_row/perm_w/inv."""
         lib = _lib.load()
+        _need_device("moe_dispatch", topi, topw)
+        if topi.dtype != torch.int64 or topw.dtype != torch.float32 or topi.dim() != 2 or \
+                tuple(topw.shape) != tuple(topi.shape):
+            raise RuntimeError(f"moe_dispatch: topi int64 [T, k] and topw float32 [T, k] expected, got "
+                               f"{topi.dtype} {tuple(topi.shape)} / {topw.dtype} {tuple(topw.shape)}")
         T, k = topi.shape
         E = int(num_experts)
         if block_m is None:
@@ -293,12 +352,16 @@ class RocmBackend:
         Returns (out [T,d], prob, topi, topw, dispatch dict).
         """
         lib = _lib.load()
+        _need_device("moe_stages", x2, gate_w, gate_b)
+        if x2.dtype not in _ACT or x2.dim() != 2:
+            raise RuntimeError(f"moe_stages: x must be 2-D float32 or bfloat16, got {x2.dtype} {tuple(x2.shape)}")
+        x2 = x2 if x2.is_contiguous() else x2.contiguous()
         T, d = x2.shape
         E = len(experts)
         h = experts[0][0].shape[0]
         dev = x2.device
         act = _ACT[x2.dtype]
-        table = self._expert_table(experts, dev, d, h, tile)
+        table = self._expert_entry(experts, dev, d, h, tile)["table"]
         gw = gate_w.detach().float().contiguous()
         gb = None if gate_b is None else gate_b.detach().float().contiguous()
         R = T * top_k
@@ -398,13 +461,15 @@ class RocmBackend:
 
     def _moe_forward(self, x, gate_w, gate_b, experts, top_k, tile, norm, routing=None, next_router=None):
         lib = _lib.load()
-        _need_device("moe_forward", x, gate_w)
+        _need_device("moe_forward", x, gate_w, gate_b, None if norm is None else norm[0])
         if x.dtype not in _ACT:
             raise RuntimeError(f"moe_forward: x must be float32 or bfloat16, got {x.dtype}")
         d = x.shape[-1]
         E = len(experts)
         if gate_w.dim() != 2 or tuple(gate_w.shape) != (E, d):
             raise RuntimeError(f"moe_forward: gate weight must be [{E}, {d}], got {tuple(gate_w.shape)}")
+        if gate_b is not None and gate_b.numel() != E:
+            raise RuntimeError(f"moe_forward: gate bias must have {E} elements, got {gate_b.numel()}")
         if not 1 <= top_k <= E:
             raise ValueError(f"top_k must be in [1, {E}], got {top_k}")
         if tile <= 0:
@@ -414,7 +479,7 @@ class RocmBackend:
         x2 = x2 if x2.is_contiguous() else x2.contiguous()
         T = x2.shape[0]
         dev = x.device
-        table = self._expert_table(experts, dev, d, h, tile)
+        table = self._expert_entry(experts, dev, d, h, tile)["table"]
         gw = gate_w.detach()
         gw = gw if (gw.dtype == torch.float32 and gw.is_contiguous()) else gw.float().contiguous()
         gb = None

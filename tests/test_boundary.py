@@ -148,3 +148,19 @@ def test_fp8linear_and_moe_modules_on_cpu():
         moe(torch.randn(1, 4, 64))
     aux = moe.balance_loss(torch.full((8, 4), 0.25))
     assert abs(float(aux) - 1.0) < 1e-6
+
+
+def test_staged_entries_need_device_tensors():
+    """Every backend entry that hands pointers to the library checks that its
+    tensors live on a HIP device first: a host pointer never reaches a kernel."""
+    be = get_backend("rocm")
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    gw = torch.zeros(4, 64)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        be.moe_router(x, gw, None, 2)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        be.moe_dispatch(torch.zeros(4, 2, dtype=torch.int64), torch.zeros(4, 2), 4)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        be.moe_stages(x, gw, None, [()] * 4, 2, 64)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        be.moe_forward(x, gw, torch.zeros(4), [()] * 4, 2, 64)

@@ -123,23 +123,57 @@ def test_fp8_linear_special_codes():
 
 
 def test_c2_dense_swiglu_pair_full_size():
-    """Config 2: 4096 x 512 -> 2 x 1280 (gate, up), then 1280 -> 512, bf16 x."""
+    """Config 2: 4096 x 512 -> 2 x 1280 (gate and up in one launch with the
+    SwiGLU epilogue), then 1280 -> 512, bf16 x, through the fused entry."""
     gen = torch.Generator().manual_seed(1236)
     rows, d, h = 4096, 512, 1280
     x = torch.randn(rows, d, generator=gen).to(torch.bfloat16)
     ex = oracle.make_expert(d, h, gen)
-    b = be()
-    xd = x.to(DEV)
-    g = b.fp8_forward(xd, ex.gate_w.to(DEV), ex.gate_s.to(DEV), d, h, 64).to(torch.bfloat16)
-    u = b.fp8_forward(xd, ex.up_w.to(DEV), ex.up_s.to(DEV), d, h, 64).to(torch.bfloat16)
-    hd = (torch.nn.functional.silu(g.float()) * u.float()).to(torch.bfloat16)
-    y = b.fp8_forward(hd, ex.down_w.to(DEV), ex.down_s.to(DEV), h, d, 64).to(torch.bfloat16)
-    # oracle on the first 512 rows (rows are independent)
-    ref = oracle.swiffn_forward(x[:512], ex)
-    assert rel_l2(y[:512].float(), ref.float()) < 2e-3
-    # the whole output against an fp32 torch reference of the same math
-    Wg = oracle.decode_full(ex.gate_w, ex.gate_s).to(DEV)
-    assert rel_l2(g.float(), (xd.float() @ Wg.T)) < 4e-3  # only g's bf16 rounding
+    bufs = tuple(t.to(DEV) for t in (ex.gate_w, ex.gate_s, ex.up_w, ex.up_s, ex.down_w, ex.down_s))
+    y = be().swiffn_forward(x.to(DEV), bufs, 64).cpu()
+    assert y.dtype == torch.bfloat16 and y.shape == x.shape
+    # the oracle (model.py:289-290 with the reference GEMM) on every 8th row
+    idx = torch.arange(0, rows, 8)
+    ref = oracle.swiffn_forward(x[idx], ex)
+    err = rel_l2(y[idx].float(), ref.float())
+    print(f"rel_l2={err:.3e}")
+    assert err < 2e-3
+
+
+@pytest.mark.parametrize("rows,d,h,dtype,tile", [
+    (37, 256, 640, torch.bfloat16, 64),     # small row count: 32-row register-staged tiles
+    (300, 192, 320, torch.bfloat16, 64),    # d not a multiple of 256: register-staged down
+    (300, 256, 640, torch.float32, 64),     # fp32 activations (hi+lo split), no rounding points
+    (129, 256, 512, torch.bfloat16, 32),
+    (200, 256, 384, torch.bfloat16, 128),
+    (1, 512, 1280, torch.bfloat16, 64),
+])
+def test_swiffn_dense_vs_oracle(rows, d, h, dtype, tile):
+    print(f"case swiffn rows={rows} d={d} h={h} {dtype} tile={tile}", flush=True)
+    gen = torch.Generator().manual_seed(rows * 13 + d + h)
+    x = torch.randn(rows, d, generator=gen).to(dtype)
+    ex = oracle.make_expert(d, h, gen, tile)
+    bufs = tuple(t.to(DEV) for t in (ex.gate_w, ex.gate_s, ex.up_w, ex.up_s, ex.down_w, ex.down_s))
+    y = be().swiffn_forward(x.to(DEV), bufs, tile).cpu()
+    ref = oracle.swiffn_forward(x, ex, tile)
+    assert y.dtype == dtype
+    err = rel_l2(y.float(), ref.float())
+    print(f"rel_l2={err:.3e}")
+    assert err < (2e-3 if dtype == torch.bfloat16 else 1e-5)
+
+
+def test_swiffn_module_on_device():
+    """SwiFFN.forward (model.py:289-290) runs the fused entry on the device."""
+    from smaulnative_amd import MoEConfig, SwiFFN
+    torch.manual_seed(1)
+    ffn = SwiFFN(MoEConfig(d_model=256, ffn_mult=2.5)).eval()
+    ex = oracle.ExpertWeights(*[t.clone() for t in ffn.buffers6()])
+    x = torch.randn(3, 40, 256).to(torch.bfloat16)
+    ref = oracle.swiffn_forward(x, ex)
+    with torch.no_grad():
+        y = ffn.to(DEV)(x.to(DEV)).cpu()
+    assert y.shape == x.shape and y.dtype == torch.bfloat16
+    assert rel_l2(y.float(), ref.float()) < 2e-3
 
 
 # --------------------------------------------------------------------------
@@ -161,14 +195,10 @@ def test_router_matches_oracle(T, d, E, k, dtype):
     prob, topi, topw = prob.cpu(), topi.cpu(), topw.cpu()
     assert rel_max(prob, prob_r) < 1e-5
     diff = (topi != topi_r).any(1)
-    if diff.any():
-        # a flip is only acceptable at a near-tie of the reference probabilities
-        m = route_margin(prob_r, topi_r, k)[diff]
-        print(f"routing flips: {int(diff.sum())} of {T}, margins {m.tolist()}")
-        assert float(m.abs().max()) < 1e-6
-    assert int(diff.sum()) <= max(1, T // 10000)
-    same = ~diff
-    assert rel_max(topw[same], topw_r[same]) < 1e-5
+    if diff.any():  # printed so that a near-tie flip is diagnosable; none is accepted
+        print(f"routing flips: {int(diff.sum())} of {T}, margins {route_margin(prob_r, topi_r, k)[diff].tolist()}")
+    assert torch.equal(topi, topi_r)
+    assert rel_max(topw, topw_r) < 1e-5
 
 
 def test_dispatch_permutation_bit_exact():
@@ -202,6 +232,66 @@ def test_dispatch_permutation_bit_exact():
     bm = disp["block_m"]
     tiles = disp["tile_off"].cpu().tolist()
     assert tiles == [sum((c + bm - 1) // bm for c in counts[:e]) for e in range(E + 1)]
+
+
+@pytest.mark.parametrize("T,E,k", [(20000, 8, 2), (20000, 16, 3), (70000, 4, 1)])
+def test_dispatch_many_blocks_bit_exact(T, E, k):
+    """Past 256 router blocks the dispatch scan runs as its own kernel: the
+    permutation, counts and inverse map still follow the brute-force order."""
+    print(f"case dispatch T={T} E={E} k={k}", flush=True)
+    gen = torch.Generator().manual_seed(T + E)
+    topi = torch.stack([torch.randperm(E, generator=gen)[:k] for _ in range(T)]).to(torch.int64)
+    topw = torch.rand(T, k, generator=gen)
+    topw[torch.rand(T, k, generator=gen) < 0.05] = 0.0  # w == 0: not dispatched (model.py:576)
+    disp = be().moe_dispatch(topi.to(DEV), topw.to(DEV), E, 128)
+    torch.cuda.synchronize()
+    counts = disp["counts"].cpu().tolist()
+    seg = disp["seg_off"].cpu().tolist()
+    perm = disp["perm_row"].cpu()
+    pw = disp["perm_w"].cpu()
+    inv = disp["inv"].cpu().reshape(T, k)
+    for e in range(E):
+        w_e = torch.where(topi == e, topw, torch.zeros_like(topw)).sum(-1)
+        toks = torch.nonzero(w_e > 0).flatten()
+        assert counts[e] == toks.numel() and seg[e + 1] - seg[e] == toks.numel()
+        assert torch.equal(perm[seg[e]:seg[e + 1]].long(), toks)
+        assert torch.equal(pw[seg[e]:seg[e + 1]], w_e[toks])
+    live = topw > 0
+    assert bool((inv[~live] == -1).all())
+    pos = inv[live].long()
+    assert torch.equal(perm[pos].long(), torch.arange(T).unsqueeze(1).expand(T, k)[live])
+
+
+def test_moe_fp32_many_router_blocks():
+    """fp32 activations at E = 16 route 16 tokens per block: T = 4500 gives 282
+    blocks, past the fused scan + scatter kernel's 256."""
+    print("case moe fp32 T=4500 E=16", flush=True)
+    T, d, h, E, k = 4500, 128, 256, 16, 2
+    x, gw, gb, experts = make_moe(4500, T, d, h, E, k, dtype=torch.float32)
+    ref = oracle.moe_forward(x, gw, gb, experts, k)
+    out, prob, topi, counts = gpu_moe(x, gw, gb, experts, k)
+    assert torch.equal(topi, ref.topi)
+    assert counts.tolist() == ref.counts
+    assert rel_l2(out, ref.out) < 1e-5
+
+
+def test_host_tensors_rejected_before_launch():
+    """A bias, norm weight or routing tensor left on the host raises in Python;
+    no host pointer reaches a kernel."""
+    x, gw, gb, experts = make_moe(3, 64, 128, 256, 4, 2)
+    b = be()
+    xd, gwd, exd = x.to(DEV), gw.to(DEV), to_dev_experts(experts)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        b.moe_forward(xd, gwd, gb, exd, 2, 64)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        b.moe_forward_norm(xd, gwd, gb.to(DEV), exd, 2, 64, torch.ones(128), 1e-6)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        b.moe_router(xd, gwd, gb, 2)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        b.moe_stages(xd, gwd, gb, exd, 2, 64)
+    prob, topi, topw = b.moe_router(xd, gwd, gb.to(DEV), 2)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        b.moe_dispatch(topi, topw.cpu(), 4)
 
 
 # --------------------------------------------------------------------------
@@ -242,15 +332,11 @@ def test_moe_vs_oracle(T, d, h, E, k, dtype, tile):
     ref = oracle.moe_forward(x, gw, gb, experts, k, tile)
     out, prob, topi, counts = gpu_moe(x, gw, gb, experts, k, tile)
     diff = (topi.reshape(-1, k) != ref.topi.reshape(-1, k)).any(1)
-    if diff.any():
-        m = route_margin(ref.prob, ref.topi, k)[diff]
-        print(f"routing flips at near-ties: {int(diff.sum())}, margins {m.tolist()}")
-        assert float(m.abs().max()) < 1e-6
-    else:
-        assert counts.tolist() == ref.counts
-    same = ~diff
-    o, r = out.reshape(-1, d)[same].float(), ref.out.reshape(-1, d)[same].float()
-    err = rel_l2(o, r)
+    if diff.any():  # printed so that a near-tie flip is diagnosable; none is accepted
+        print(f"routing flips: {int(diff.sum())}, margins {route_margin(ref.prob, ref.topi, k)[diff].tolist()}")
+    assert torch.equal(topi.reshape(-1, k), ref.topi.reshape(-1, k))
+    assert counts.tolist() == ref.counts
+    err = rel_l2(out.float(), ref.out.float())
     print(f"rel_l2={err:.3e}")
     assert err < (2e-3 if dtype == torch.bfloat16 else 1e-5)
 
@@ -434,12 +520,18 @@ def test_moe_deterministic_and_empty():
     assert out.shape == (0, 256) and counts.tolist() == [0] * 8
 
 
-def test_moe_full_config3_sampled_tokens():
-    """Config 3 at full size; the oracle re-runs a sample of tokens (tokens are independent)."""
+def test_moe_full_config3():
+    """Config 3 at full size: the routing of all 16384 tokens and the per-expert
+    counts bit-exact against the oracle router (model.py:558-570, 577); the
+    output of a token sample against the oracle's expert loop (tokens are
+    independent)."""
     T, d, h, E, k = 16384, 1024, 2560, 8, 2
     x, gw, gb, experts = make_moe(1236, T, d, h, E, k)
     out, prob, topi, counts = gpu_moe(x, gw, gb, experts, k)
-    assert int(counts.sum()) == T * k
+    prob_r, topi_r, topw_r = oracle.route(x, gw, gb, k)
+    assert torch.equal(topi, topi_r)
+    assert counts.tolist() == [int(((topi_r == e) & (topw_r > 0)).any(-1).sum()) for e in range(E)]
+    assert rel_max(prob, prob_r) < 1e-5
     idx = torch.arange(0, T, 61)
     ref = oracle.moe_forward(x[idx], gw, gb, experts, k)
     assert torch.equal(topi[idx], ref.topi)
