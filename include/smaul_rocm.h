@@ -203,6 +203,29 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
                       int flags, hipStream_t stream);
 
 /*
+ * smaul_moe_forward without a workspace argument: the layer's workspace is a
+ * static device array inside the library (SMAUL_NOALLOC_SCRATCH_BYTES, one per
+ * GPU, held until the process ends), so the call allocates nothing -- no
+ * hipMalloc, no hipFree, no allocating library routine.  No counterpart in
+ * the reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  Results
+ * are bit-identical to smaul_moe_forward.  Layers whose
+ * smaul_moe_workspace_size exceeds SMAUL_NOALLOC_SCRATCH_BYTES are rejected
+ * with SMAUL_ERR_UNSUPPORTED (64 MiB: e.g. up to ~4600 tokens at d=1024,
+ * h=2560, top-2, bf16; the 64-token decode step needs ~1 MB).  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (two streams,
+ * two threads) race and must be serialised by the caller.
+ */
+#define SMAUL_NOALLOC_SCRATCH_BYTES (64ll << 20)
+
+int smaul_moe_forward_noalloc(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
+                              const uint8_t* const* gate_w8, const float* const* gate_s,
+                              const uint8_t* const* up_w8, const float* const* up_s,
+                              const uint8_t* const* down_w8, const float* const* down_s, void* out,
+                              float* prob, int64_t* topi, float* topw, int32_t* counts, int64_t T, int64_t d,
+                              int64_t h, int64_t E, int64_t k, int64_t tile, int flags, hipStream_t stream);
+
+/*
  * smaul_moe_forward followed by RMSNorm of its output rows, the norm Block
  * applies to every FFN output (model.py:636, RMSNorm.forward model.py:124-139):
  * out as smaul_moe_forward writes it, and norm_out [T, d] (act_dtype) =

@@ -44,6 +44,8 @@ SIGNATURES = {
     "smaul_moe_workspace_size": (_I64, [_I64, _I64, _I64, _I64, _I64, _I]),
     "smaul_moe_forward": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P]),
+    "smaul_moe_forward_noalloc": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                       _I64, _I64, _I64, _I64, _I64, _I64, _I, _P]),
     "smaul_moe_forward_norm": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                     _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, ctypes.c_float, _P, _P]),
     "smaul_moe_forward_chain": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,

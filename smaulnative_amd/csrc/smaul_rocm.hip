@@ -31,6 +31,7 @@
 #include <stdarg.h>
 
 #include <algorithm>
+#include <mutex>
 #include <cmath>
 #include <stdlib.h>
 #include <stdint.h>
@@ -3110,6 +3111,39 @@ bool dma_gemm_ok(const GemmArgs& a, int act_dtype, int flags, int64_t x_rows, in
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Static scratch for smaul_moe_forward_noalloc: a fixed device array per GPU,
+// held from the library's first call on that GPU until the process ends.  In
+// host code `scratch` names a host-side stand-in, never the device memory:
+// the device address comes from hipGetSymbolAddress, once per device, with
+// that device current, and only that address is handed to kernels.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) char scratch[SMAUL_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address (looked up on the first call per device).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(SMAUL_ERR_HIP, "noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(SMAUL_ERR_UNSUPPORTED, "noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(SMAUL_ERR_HIP, "noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SMAUL_OK;
+}
+}  // namespace
+
 // ===========================================================================
 // C ABI
 // ===========================================================================
@@ -3807,6 +3841,29 @@ int smaul_moe_forward(const void* x, int act_dtype, const float* gate_w, const f
   return moe_forward_impl(x, act_dtype, gate_w, gate_b, gate_w8, gate_s, up_w8, up_s, down_w8, down_s, out, prob,
                           topi, topw, counts, workspace, workspace_bytes, T, d, h, E, k, tile, flags, nullptr,
                           false, nullptr, stream);
+}
+
+int smaul_moe_forward_noalloc(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
+                              const uint8_t* const* gate_w8, const float* const* gate_s,
+                              const uint8_t* const* up_w8, const float* const* up_s,
+                              const uint8_t* const* down_w8, const float* const* down_s, void* out,
+                              float* prob, int64_t* topi, float* topw, int32_t* counts, int64_t T, int64_t d,
+                              int64_t h, int64_t E, int64_t k, int64_t tile, int flags, hipStream_t stream) {
+  const int64_t need = smaul_moe_workspace_size(T, d, h, E, k, act_dtype);
+  if (need < 0) return fail(SMAUL_ERR_INVALID, "moe_forward_noalloc: bad sizes");
+  if (need > (int64_t)SMAUL_NOALLOC_SCRATCH_BYTES)
+    return fail(SMAUL_ERR_UNSUPPORTED,
+                "moe_forward_noalloc: the layer needs %lld bytes of workspace, more than the %lld-byte static "
+                "scratch; use smaul_moe_forward with a workspace",
+                (long long)need, (long long)SMAUL_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc) return rc;
+  // Nothing in the workspace has to start at zero: every stage writes what
+  // the next one reads (counts, offsets, tables, hdn, yperm) in this call.
+  return moe_forward_impl(x, act_dtype, gate_w, gate_b, gate_w8, gate_s, up_w8, up_s, down_w8, down_s, out, prob,
+                          topi, topw, counts, ws, (int64_t)SMAUL_NOALLOC_SCRATCH_BYTES, T, d, h, E, k, tile, flags,
+                          nullptr, false, nullptr, stream);
 }
 
 int smaul_moe_forward_norm(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
