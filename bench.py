@@ -200,11 +200,15 @@ def cpu_time_moe(x, gw, gb, experts, k, threads, target_s, max_tokens):
         lambda xx, w, s, i, o, t: oracle.fp8_forward(xx, w, s, i, o, t, threads=threads))
     kind = "reference" if ref is not None else "port"
     ow = [oracle.ExpertWeights(*e) for e in experts]
-    n = 64
-    t0 = time.perf_counter()
-    oracle.moe_forward(x[:n], gw, gb, ow, k, 64, gemm=gemm)  # warm-up and size probe
-    dt = time.perf_counter() - t0
-    n = int(min(max_tokens, max(n, n * target_s / max(dt, 1e-4))))
+    oracle.moe_forward(x[:64], gw, gb, ow, k, 64, gemm=gemm)  # warm-up
+    n = min(256, max_tokens)
+    while True:  # grow the sample until one pass takes about target_s
+        t0 = time.perf_counter()
+        oracle.moe_forward(x[:n], gw, gb, ow, k, 64, gemm=gemm)
+        dt = time.perf_counter() - t0
+        if dt >= 0.5 * target_s or n >= max_tokens:
+            break
+        n = int(min(max_tokens, max(2 * n, n * target_s / max(dt, 1e-4))))
     runs = []
     for _ in range(3):
         t0 = time.perf_counter()

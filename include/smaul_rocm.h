@@ -174,8 +174,8 @@ int smaul_swiffn_forward(const void* x, int act_dtype, const uint8_t* gate_w8, c
 
 /*
  * RMSNorm over the rows of x [T, d]: out = cast((x * rsqrt(mean(x^2) + eps)) *
- * weight) computed in fp32, out in act_dtype (model.py:124-139, RMSNorm.forward;
- * Block applies it to every MoE output, model.py:636).  weight: fp32 [d], or
+ * weight) computed in fp32, out in act_dtype (the formula of RMSNorm.forward,
+ * model.py:124-139).  weight: fp32 [d], or
  * NULL for a weight of ones (the unit-RMS normalisation).  eps must be positive
  * and finite (model.py:127-128).  The row sum of squares is reduced in a
  * different order than torch's, so results agree to fp32 rounding, not bitwise.
@@ -226,12 +226,15 @@ int smaul_moe_forward_noalloc(const void* x, int act_dtype, const float* gate_w,
                               int64_t h, int64_t E, int64_t k, int64_t tile, int flags, hipStream_t stream);
 
 /*
- * smaul_moe_forward followed by RMSNorm of its output rows, the norm Block
- * applies to every FFN output (model.py:636, RMSNorm.forward model.py:124-139):
- * out as smaul_moe_forward writes it, and norm_out [T, d] (act_dtype) =
- * smaul_rms_norm(out, norm_w, eps), bit for bit.  With d % 16 == 0 and
- * d <= 4096 the norm is fused into the combine kernel (one wave per token);
- * otherwise the two kernels run one after the other.
+ * smaul_moe_forward followed by RMSNorm of its output rows (the formula of
+ * RMSNorm.forward, model.py:124-139): out as smaul_moe_forward writes it, and
+ * norm_out [T, d] (act_dtype) = smaul_rms_norm(out, norm_w, eps), bit for bit.
+ * With d % 16 == 0 and d <= 4096 the norm is fused into the combine kernel
+ * (one wave per token); otherwise the two kernels run one after the other.
+ * No counterpart in the reference: its Block norms the FFN output in fp32
+ * (n4 on fx.float(), model.py:640-641), so norm_out is not that norm; it is
+ * for stacks whose next MoE layer reads the normalised rows in act_dtype
+ * (the config-4 decode harness).
  */
 int smaul_moe_forward_norm(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
                            const uint8_t* const* gate_w8, const float* const* gate_s,
@@ -244,8 +247,9 @@ int smaul_moe_forward_norm(const void* x, int act_dtype, const float* gate_w, co
                            hipStream_t stream);
 
 /*
- * One layer of a chain of MoE layers (the decode step of a stack of Blocks,
- * model.py:636 feeding the next layer's router, model.py:558-570):
+ * One layer of a chain of MoE layers in which each layer's normalised output
+ * is the next layer's input (the config-4 decode harness; a reference Block
+ * routes n5(x + f) instead, so it cannot use this fusion):
  * smaul_moe_forward_norm, plus two ways to move routing across the boundary.
  *   routed != 0: prob/topi/topw are INPUTS holding this layer's routing of x
  *     (as smaul_moe_router writes it, e.g. the previous call's next_*); the
@@ -271,6 +275,33 @@ int smaul_moe_forward_chain(const void* x, int act_dtype, const float* gate_w, c
                             const float* next_gate_w, const float* next_gate_b, int64_t next_E,
                             int64_t next_k, float* next_prob, int64_t* next_topi, float* next_topw,
                             hipStream_t stream);
+
+/*
+ * Linear-attention recurrence of SmaulLinear, per (batch, head):
+ *   kn_t = k_t / max(||k_t||, 1e-6),  S_t = S_{t-1} + kn_t (x) v_t,
+ *   z_t = z_{t-1} + kn_t,  y_t = (q_t @ S_t) / max(q_t . z_t, eps).
+ * Replaces the reference's native kernels kernel/attn_cpu.cpp attn_forward
+ * (:144-212) and attn_step (:421-492), reached through the backend entries
+ * of kernel/compute.py:265-309; results are bit-identical to them (the same
+ * per-element operation order, correctly rounded division and square root).
+ * Q/K/V/Y fp32 [B,T,H,D] contiguous (K raw: the normalisation is inside);
+ * DEN fp32 [B,T,H] or NULL; S_out fp32 [B,H,D,D] and z_out [B,H,D] (the final
+ * state, both or neither; zeros when T == 0).  0 < D <= 2048, eps positive
+ * and finite.  For D > 128 without S_out the state lives in `workspace`
+ * (smaul_attn_workspace_size bytes; 0 otherwise).
+ */
+int64_t smaul_attn_workspace_size(int64_t B, int64_t H, int64_t D, int need_state);
+
+int smaul_attn_forward(const float* Q, const float* K, const float* V, float* Y, float* DEN, float* S_out,
+                       float* z_out, int64_t B, int64_t T, int64_t H, int64_t D, float eps, void* workspace,
+                       int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * One decode step from the carried state: S [B,H,D,D] and z [B,H,D] are
+ * advanced in place, y [B,H,D] = the step's output (q/k/v [B,H,D]).
+ */
+int smaul_attn_step(float* S, float* z, const float* q, const float* k, const float* v, float* y, int64_t B,
+                    int64_t H, int64_t D, float eps, hipStream_t stream);
 
 /*
  * Host-side self-test of the top-k selection order used by the router (no GPU

@@ -17,6 +17,9 @@ checkout):
 - ``fp8_linear``        kernel/fp8_tile.py:163-170 (_Fn.forward dtype handling)
 - ``swiffn_forward``    model.py:289-290
 - ``moe_forward``       model.py:557-585 (router, top-k, mask dispatch, combine)
+- ``attn_forward``      kernel/attn_cpu.cpp:16-24,40-142 via ``attn.c`` (C, bit-exact)
+- ``attn_step``         kernel/attn_cpu.cpp:421-492 via ``attn.c``
+- ``attn_textbook``     model.py:199-218 (_attn_reference: the same recurrence in torch ops)
 
 Arithmetic that lives in torch (router GEMM, softmax, topk, silu) is computed
 with the same torch CPU calls the reference makes; torch is a third-party
@@ -33,6 +36,10 @@ How each piece is pinned (tests/test_oracle.py):
   special-value cases of tests/test_linear_fp8.py:484-510.
 - moe_forward: golden outputs, probabilities, top-k indices and counts of the
   reference SwiFFN_MoE, including exact-tie and zero-weight routing cases.
+- attn_forward / attn_step: bit-exact against the reference's own attn_cpu.cpp
+  built under oracle/_ref and against golden vectors written from it; within
+  fp32 rounding of the textbook recurrence (model.py:199-218); closed forms at
+  T=1 (y = v when q.kn >= eps) and for zero keys (the 1e-6 clamp).
 """
 from __future__ import annotations
 
@@ -146,6 +153,10 @@ def _load_lib():
         lib.oracle_fp8_forward.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4 + [ctypes.c_int]
         lib.oracle_fp8_forward.restype = ctypes.c_int
         lib.oracle_e4m3_lut.argtypes = [ctypes.c_void_p]
+        lib.oracle_attn_forward.argtypes = [ctypes.c_void_p] * 7 + [ctypes.c_int64] * 4 + [ctypes.c_float]
+        lib.oracle_attn_forward.restype = ctypes.c_int
+        lib.oracle_attn_step.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int64] * 3 + [ctypes.c_float]
+        lib.oracle_attn_step.restype = ctypes.c_int
         _lib = lib
     return _lib
 
@@ -291,6 +302,76 @@ def moe_forward(x, gate_w, gate_b, experts: List[ExpertWeights], top_k, tile=TIL
             out[m] += y.float() * w[m]
     res = out.to(x.dtype if x.is_floating_point() else torch.float32)
     return MoEResult(res, prob, topi, topv, counts, executed, perm)
+
+
+# --------------------------------------------------------------------------
+# linear attention (C restatement, the reference's own kernel, textbook form)
+# --------------------------------------------------------------------------
+def attn_forward(Q, K, V, eps=1e-6):
+    """attn_cpu.cpp attn_forward with DEN and the final state: (Y, DEN, S, z).
+
+    Q/K/V fp32 [B,T,H,D] (K raw, post-elu+1; normalised inside).  DEN [B,T,H],
+    S [B,H,D,D], z [B,H,D].
+    """
+    Qc, Kc, Vc = (t.detach().cpu().float().contiguous() for t in (Q, K, V))
+    B, T, H, D = Qc.shape
+    Y = torch.empty_like(Qc)
+    DEN = torch.empty(B, T, H)
+    S = torch.empty(B, H, D, D)
+    z = torch.empty(B, H, D)
+    rc = _load_lib().oracle_attn_forward(Qc.data_ptr(), Kc.data_ptr(), Vc.data_ptr(), Y.data_ptr(),
+                                         DEN.data_ptr(), S.data_ptr(), z.data_ptr(), B, T, H, D, eps)
+    if rc != 0:
+        raise RuntimeError(f"oracle_attn_forward failed ({rc})")
+    return Y, DEN, S, z
+
+
+def attn_step(S, z, q, k, v, eps=1e-6):
+    """attn_cpu.cpp attn_step on copies: returns (y [B,H,D], S', z')."""
+    S2 = S.detach().cpu().float().contiguous().clone()
+    z2 = z.detach().cpu().float().contiguous().clone()
+    qc, kc, vc = (t.detach().cpu().float().contiguous() for t in (q, k, v))
+    B, H, D = qc.shape
+    y = torch.empty_like(qc)
+    rc = _load_lib().oracle_attn_step(S2.data_ptr(), z2.data_ptr(), qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                      y.data_ptr(), B, H, D, eps)
+    if rc != 0:
+        raise RuntimeError(f"oracle_attn_step failed ({rc})")
+    return y, S2, z2
+
+
+_ref_attn_mod = None
+
+
+def ref_attn_module():
+    """The reference's own attn_cpu.cpp built by oracle/Makefile, or None."""
+    global _ref_attn_mod
+    if _ref_attn_mod is None:
+        hits = sorted(glob.glob(os.path.join(_HERE, "_ref", "smaul_attn_ref*.so")))
+        if not hits:
+            return None
+        spec = importlib.util.spec_from_file_location("smaul_attn_ref", hits[0])
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _ref_attn_mod = mod
+    return _ref_attn_mod
+
+
+def attn_textbook(Q, K, V, eps=1e-6):
+    """model.py:199-218 (_attn_reference): the recurrence in torch ops, fp32."""
+    B, T, H, D = Q.shape
+    S = torch.zeros(B, H, D, D)
+    z = torch.zeros(B, H, D)
+    ys = []
+    for t in range(T):
+        kt, vt, qt = K[:, t].float(), V[:, t].float(), Q[:, t].float()
+        kt = kt / kt.norm(dim=-1, keepdim=True).clamp_min(1e-6)
+        S = S + kt.unsqueeze(-1) @ vt.unsqueeze(-2)
+        z = z + kt
+        num = (qt.unsqueeze(-2) @ S).squeeze(-2)
+        den = (qt * z).sum(-1, keepdim=True).clamp_min(eps)
+        ys.append(num / den)
+    return torch.stack(ys, 1) if ys else torch.empty(B, 0, H, D)
 
 
 # --------------------------------------------------------------------------

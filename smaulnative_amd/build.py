@@ -1,4 +1,4 @@
-"""Builds libsmaul_rocm.so in-tree with hipcc for gfx950.
+"""Builds libsmaul_rocm.so in-tree with hipcc for gfx950 (one object per source, then one link).
 
     python -m smaulnative_amd.build
 
@@ -22,15 +22,17 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
-SRC = os.path.join(HERE, "csrc", "smaul_rocm.hip")
+CSRC = os.path.join(HERE, "csrc")
+SOURCES = [os.path.join(CSRC, n) for n in ("smaul_rocm.hip", "attn.hip")]
 OUT = os.path.join(HERE, "libsmaul_rocm.so")
+OBJDIR = os.path.join(HERE, "_build")
 
 HIPCC_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form",
-    "-I" + os.path.join(REPO, "include"), "-I" + os.path.join(HERE, "csrc"),
+    "-I" + os.path.join(REPO, "include"), "-I" + CSRC,
 ]
 
 
@@ -41,14 +43,29 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose: bool = False) -> str:
-    tmp = OUT + ".tmp"
-    cmd = [hipcc()] + HIPCC_FLAGS + [SRC, "-o", tmp]
-    res = subprocess.run(cmd, capture_output=True, text=True)
+def _compile(src: str) -> str:
+    obj = os.path.join(OBJDIR, os.path.basename(src) + ".o")
+    res = subprocess.run([hipcc()] + HIPCC_FLAGS + ["-c", src, "-o", obj], capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
-    if verbose and res.stderr:
-        sys.stderr.write("\n".join(l for l in res.stderr.splitlines() if "packed-fp32" not in l))
+        raise RuntimeError(f"hipcc failed on {src} ({res.returncode}):\n{res.stderr[-4000:]}")
+    return obj, res.stderr
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every source (in parallel) and link libsmaul_rocm.so; always rebuilds."""
+    from concurrent.futures import ThreadPoolExecutor
+    os.makedirs(OBJDIR, exist_ok=True)
+    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+        results = list(ex.map(_compile, SOURCES))
+    if verbose:
+        for _, err in results:
+            if err:
+                sys.stderr.write("\n".join(l for l in err.splitlines() if "packed-fp32" not in l))
+    tmp = OUT + ".tmp"
+    res = subprocess.run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC"] + [o for o, _ in results]
+                         + ["-o", tmp], capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed ({res.returncode}):\n{res.stderr[-4000:]}")
     os.replace(tmp, OUT)
     return OUT
 

@@ -38,6 +38,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include "smaul_common.h"
 #include "smaul_rocm.h"
 #include "topk_select.h"
 
@@ -49,21 +50,8 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-thread_local char g_err[512] = "";
-
-int fail(int code, const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_err, sizeof(g_err), fmt, ap);
-  va_end(ap);
-  return code;
-}
-
-int check_launch(const char* what) {
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(SMAUL_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
-  return SMAUL_OK;
-}
+using smaul::check_launch;
+using smaul::fail;
 
 // ---------------------------------------------------------------------------
 // scalar helpers
@@ -3151,7 +3139,7 @@ extern "C" {
 
 int smaul_version(void) { return SMAUL_VERSION; }
 
-const char* smaul_last_error(void) { return g_err; }
+const char* smaul_last_error(void) { return smaul::g_err; }
 
 int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* s, void* y,
                      int y_dtype, int64_t rows, int64_t in_f, int64_t out_f, int64_t tile, int flags,

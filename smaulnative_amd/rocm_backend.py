@@ -15,7 +15,9 @@ Behaviour differences from the reference CPU backend, all deliberate:
   and nothing synchronises;
 - ``fp8_forward`` also accepts bf16 ``x`` (fed to bf16 MFMA unchanged);
   fp32 ``x`` is split into two bf16 terms inside the kernel;
-- training entry points (backward, quantizer, attention, sparse) are not part
+- ``attn_forward`` / ``attn_step`` run the linear-attention recurrence on the
+  device, bit-identical to the reference's native kernels (attn_cpu.cpp);
+- training entry points (backward, attention backward, sparse) are not part
   of this path and raise ``NotImplementedError`` -- except
   ``fp8_quantize_tiles``, whose contract lets it return ``None`` so the caller
   runs the torch quantizer (compute.py:246-263, fp8_tile.py:96-113).
@@ -100,7 +102,7 @@ class RocmBackend:
 
     @property
     def has_attn_native(self):
-        return False
+        return self.has_native
 
     @property
     def has_sparse_native(self):
@@ -149,14 +151,77 @@ class RocmBackend:
         """No device quantizer: returning None makes the caller run the torch path."""
         return None
 
+    # ---- linear attention (compute.py:265-322, attn_cpu.cpp) ---------------
+    @staticmethod
+    def _attn_check(name, eps, tensors):
+        _need_device(name, *tensors)
+        for t in tensors:
+            if t.dtype != torch.float32:
+                raise RuntimeError(f"{name}: tensors must be float32, got {t.dtype}")
+        if not math.isfinite(eps) or eps <= 0:
+            raise RuntimeError(f"{name}: eps must be positive finite, got {eps!r}")
+
     def attn_forward(self, Q, K, V, eps, need_den, need_state=False):
-        raise NotImplementedError("rocm backend: linear attention is not implemented")
+        """(Y, DEN, S, z) as the reference backend returns them (compute.py:265-289).
+
+        Q/K/V fp32 [B,T,H,D] on the device (K raw, normalised inside).  DEN
+        [B,T,H] when ``need_den`` else None.  S [B,H,D,D] / z [B,H,D], the
+        final recurrent state, only when ``need_state``; otherwise
+        zero-element placeholders, as the native CPU backend returns them.
+        Bit-identical to the reference's attn_cpu.cpp on the same inputs.
+        """
+        lib = _lib.load()
+        self._attn_check("attn_forward", eps, (Q, K, V))
+        if Q.dim() != 4 or K.shape != Q.shape or V.shape != Q.shape:
+            raise RuntimeError("attn_forward: Q/K/V must be [B,T,H,D] with matching shapes")
+        B, T, H, D = Q.shape
+        if D <= 0 or D > 2048:
+            raise RuntimeError(f"attn_forward: D={D} out of the supported range (0, 2048]")
+        Qc, Kc, Vc = (t if t.is_contiguous() else t.contiguous() for t in (Q, K, V))
+        dev = Q.device
+        Y = torch.empty_like(Qc)
+        DEN = torch.empty(B, T, H, dtype=torch.float32, device=dev) if need_den else None
+        if need_state:
+            S = torch.empty(B, H, D, D, dtype=torch.float32, device=dev)
+            z = torch.empty(B, H, D, dtype=torch.float32, device=dev)
+        else:
+            S = torch.empty(0, dtype=torch.float32, device=dev)
+            z = torch.empty(0, dtype=torch.float32, device=dev)
+        ws_bytes = lib.smaul_attn_workspace_size(B, H, D, int(bool(need_state)))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+        with torch.cuda.device(dev):
+            rc = lib.smaul_attn_forward(Qc.data_ptr(), Kc.data_ptr(), Vc.data_ptr(), Y.data_ptr(),
+                                        None if DEN is None else DEN.data_ptr(),
+                                        S.data_ptr() if need_state else None, z.data_ptr() if need_state else None,
+                                        B, T, H, D, float(eps), None if ws is None else ws.data_ptr(), ws_bytes,
+                                        _stream_handle(dev))
+        _lib.check(rc, "attn_forward")
+        return Y, DEN, S, z
 
     def attn_step(self, S, z, q, k, v, eps):
-        raise NotImplementedError("rocm backend: linear attention is not implemented")
+        """One decode step advancing (S, z) in place; returns (y [B,H,D], S, z)
+        (compute.py:291-309, attn_cpu.cpp:421-492, bit-identical)."""
+        lib = _lib.load()
+        self._attn_check("attn_step", eps, (S, z, q, k, v))
+        if q.dim() != 3 or k.shape != q.shape or v.shape != q.shape:
+            raise RuntimeError("attn_step: q/k/v must be [B,H,D] with matching shapes")
+        B, H, D = q.shape
+        if tuple(S.shape) != (B, H, D, D) or tuple(z.shape) != (B, H, D):
+            raise RuntimeError("attn_step: S must be [B,H,D,D] and z [B,H,D]")
+        if not (S.is_contiguous() and z.is_contiguous()):
+            raise RuntimeError("attn_step: the state S and z must be contiguous (they are updated in place)")
+        if D <= 0 or D > 2048:
+            raise RuntimeError(f"attn_step: D={D} out of the supported range (0, 2048]")
+        qc, kc, vc = (t if t.is_contiguous() else t.contiguous() for t in (q, k, v))
+        y = torch.empty_like(qc)
+        with torch.cuda.device(q.device):
+            rc = lib.smaul_attn_step(S.data_ptr(), z.data_ptr(), qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                     y.data_ptr(), B, H, D, float(eps), _stream_handle(q.device))
+        _lib.check(rc, "attn_step")
+        return y, S, z
 
     def attn_backward(self, dY, Q, K, V, Y, DEN, eps):
-        raise NotImplementedError("rocm backend: linear attention is not implemented")
+        raise NotImplementedError("rocm backend: attn_backward (training) is not implemented")
 
     def sparse_grad_v(self, dout, x, cols, values, budget=1 << 22):
         raise NotImplementedError("rocm backend: sparse_grad_v is not implemented")

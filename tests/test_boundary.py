@@ -119,7 +119,7 @@ def test_backend_surface_and_no_fallback():
                  "attn_forward", "attn_step", "attn_backward", "sparse_grad_v", "moe_forward"):
         assert callable(getattr(be, attr)), attr
     assert be.has_native is True
-    assert be.has_attn_native is False and be.has_sparse_native is False
+    assert be.has_attn_native is True and be.has_sparse_native is False
     assert be.configure(2) == 2
     w = torch.zeros(8, 64, dtype=torch.uint8)
     s = torch.ones(8, 1)

@@ -193,3 +193,87 @@ def test_zero_weight_slot_is_not_dispatched(g):
     c = load_moe_case(g, "moe_zero_weight")
     assert c["topi"].reshape(-1, 3)[0].tolist() == [0, 4, 6]
     assert c["counts"] == [4, 0, 0, 0, 4, 0, 0, 0]
+
+
+# --------------------------------------------------------------------------
+# linear attention (oracle/attn.c), pinned to the reference kernel
+# --------------------------------------------------------------------------
+GOLD_ATTN = os.path.join(os.path.dirname(__file__), "golden", "golden_attn.npz")
+
+
+def _attn_inputs(B, T, H, D, seed):
+    gen = torch.Generator().manual_seed(seed)
+    Q = torch.nn.functional.elu(torch.randn(B, T, H, D, generator=gen)) + 1
+    K = torch.nn.functional.elu(torch.randn(B, T, H, D, generator=gen)) + 1
+    V = torch.randn(B, T, H, D, generator=gen)
+    return Q, K, V
+
+
+def _attn_golden_case(ga, i):
+    def get(n):
+        k = f"a{i}_{n}"
+        return torch.from_numpy(ga[k]) if k in ga else None
+    return {n: get(n) for n in ("Q", "K", "V", "Y", "DEN", "S", "z", "q", "k", "v", "y1", "S1", "z1")}
+
+
+def test_attn_oracle_matches_golden():
+    """Bit-exact against vectors written from the reference's attn_cpu.cpp."""
+    ga = np.load(GOLD_ATTN)
+    for i, eps in enumerate(ga["eps"].tolist()):
+        c = _attn_golden_case(ga, i)
+        Y, DEN, S, z = oracle.attn_forward(c["Q"], c["K"], c["V"], eps)
+        assert torch.equal(Y, c["Y"]) and torch.equal(DEN, c["DEN"]) and torch.equal(z, c["z"]), i
+        if c["S"] is not None:
+            assert torch.equal(S, c["S"]), i
+        y1, S1, z1 = oracle.attn_step(S, z, c["q"], c["k"], c["v"], eps)
+        assert torch.equal(y1, c["y1"]) and torch.equal(z1, c["z1"]), i
+        if c["S1"] is not None:
+            assert torch.equal(S1, c["S1"]), i
+
+
+@pytest.mark.skipif(oracle.ref_attn_module() is None, reason="oracle/_ref (reference attn_cpu.cpp) not built")
+@pytest.mark.parametrize("B,T,H,D", [(2, 37, 3, 64), (1, 5, 2, 13), (2, 64, 4, 128), (1, 3, 1, 200),
+                                     (1, 0, 2, 8), (1, 40, 1, 7)])
+def test_attn_oracle_matches_reference_kernel(B, T, H, D):
+    """Bit-exact against the reference's own attn_cpu.cpp (oracle/_ref), forward and step."""
+    Q, K, V = _attn_inputs(B, T, H, D, B * 1000 + T * 10 + D)
+    ref = oracle.ref_attn_module()
+    Y, DEN, S, z = oracle.attn_forward(Q, K, V)
+    Yr, Dr, Sr, zr = ref.attn_forward(Q, K, V, 1e-6, True, True)
+    assert torch.equal(Y, Yr) and torch.equal(S, Sr) and torch.equal(z, zr)
+    if T:
+        assert torch.equal(DEN, Dr)
+        q, k, v = Q[:, 0].contiguous(), K[:, 0].contiguous(), V[:, 0].contiguous()
+        y1, S1, z1 = oracle.attn_step(S, z, q, k, v)
+        S2, z2 = S.clone(), z.clone()
+        y2, _, _ = ref.attn_step(S2, z2, q, k, v, 1e-6)
+        assert torch.equal(y1, y2) and torch.equal(S1, S2) and torch.equal(z1, z2)
+
+
+def test_attn_oracle_textbook_and_closed_forms():
+    """Within fp32 rounding of the textbook recurrence (model.py:199-218), and a
+    planted mistake -- z updated after den instead of before -- is not."""
+    Q, K, V = _attn_inputs(2, 50, 3, 32, 5)
+    Y = oracle.attn_forward(Q, K, V)[0]
+    R = oracle.attn_textbook(Q, K, V)
+    assert float(((Y - R).abs() / R.abs().clamp_min(1e-3)).max()) < 1e-4
+    # planted: den from the state before this step's key
+    B, T, H, D = Q.shape
+    S = torch.zeros(B, H, D, D)
+    z = torch.zeros(B, H, D)
+    bad = []
+    for t in range(T):
+        kt = K[:, t] / K[:, t].norm(dim=-1, keepdim=True).clamp_min(1e-6)
+        den = (Q[:, t] * z).sum(-1, keepdim=True).clamp_min(1e-6)
+        S = S + kt.unsqueeze(-1) @ V[:, t].unsqueeze(-2)
+        z = z + kt
+        bad.append((Q[:, t].unsqueeze(-2) @ S).squeeze(-2) / den)
+    assert float((torch.stack(bad, 1) - Y).abs().max()) > 1e-2
+    # T=1 from zero state: y = v * (q.kn) / max(q.kn, eps) = v when q.kn >= eps
+    Q1, K1, V1 = _attn_inputs(1, 1, 2, 16, 6)
+    Y1 = oracle.attn_forward(Q1, K1, V1)[0]
+    assert float((Y1 - V1).abs().max()) < 1e-5
+    # all-zero keys: kn = 0 (the 1e-6 clamp), den clamps to eps, y = 0
+    Yz, DENz, Sz, zz = oracle.attn_forward(Q1, torch.zeros_like(K1), V1)
+    assert torch.equal(Yz, torch.zeros_like(Yz)) and float(DENz.max()) == np.float32(1e-6)
+    assert torch.equal(Sz, torch.zeros_like(Sz))
