@@ -304,6 +304,22 @@ int smaul_attn_step(float* S, float* z, const float* q, const float* k, const fl
                     int64_t H, int64_t D, float eps, hipStream_t stream);
 
 /*
+ * Tiled E4M3 quantizer: per (row, tile) scale = max(max(finite |w|, 1e-12) /
+ * 448, 1e-12) and code = order[first i with bounds[i] >= n] for n =
+ * clamp(nan_to_num(w / scale), -448, 448), code 0 where n == 0.  Replaces the
+ * reference's native quantizer kernel/quant_cpu.cpp:64-137 (the backend entry
+ * fp8_quantize_tiles, kernel/compute.py:246-263) with bit-identical codes and
+ * scales.  w fp32 [out_f, in_f]; order uint8 [256] / bounds fp32 [255]: the
+ * sorted-codebook permutation and its midpoints (torch.argsort's tie order,
+ * as the reference passes them); codes uint8 [out_f, ldc], ldc >= nt*tile,
+ * the last tile's padding written as 0; scales fp32 [out_f, nt]; *nonfinite
+ * (device) = the number of non-finite entries of w.  Any tile > 0.
+ */
+int smaul_fp8_quantize_tiles(const float* w, int64_t out_f, int64_t in_f, int64_t tile, const uint8_t* order,
+                             const float* bounds, uint8_t* codes, int64_t ldc, float* scales,
+                             unsigned long long* nonfinite, hipStream_t stream);
+
+/*
  * Host-side self-test of the top-k selection order used by the router (no GPU
  * involved): writes the k indices the router would select for `vals` [n].
  * Exposed only so the CPU test suite can check the order against torch.topk.

@@ -17,10 +17,11 @@ Behaviour differences from the reference CPU backend, all deliberate:
   fp32 ``x`` is split into two bf16 terms inside the kernel;
 - ``attn_forward`` / ``attn_step`` run the linear-attention recurrence on the
   device, bit-identical to the reference's native kernels (attn_cpu.cpp);
+- ``fp8_quantize_tiles`` quantizes HIP tensors on the device (bit-identical
+  codes and scales); for host tensors it returns ``None``, which the contract
+  defines as "run the torch quantizer" (compute.py:246-263, fp8_tile.py:96-113);
 - training entry points (backward, attention backward, sparse) are not part
-  of this path and raise ``NotImplementedError`` -- except
-  ``fp8_quantize_tiles``, whose contract lets it return ``None`` so the caller
-  runs the torch quantizer (compute.py:246-263, fp8_tile.py:96-113).
+  of this path and raise ``NotImplementedError``.
 """
 from __future__ import annotations
 
@@ -148,8 +149,34 @@ class RocmBackend:
         raise NotImplementedError("rocm backend: fp8_backward_input (training) is not implemented")
 
     def fp8_quantize_tiles(self, w32, tile):
-        """No device quantizer: returning None makes the caller run the torch path."""
-        return None
+        """(codes uint8 [out_f, nt*tile], scales fp32 [out_f, nt], non-finite count) on the device.
+
+        compute.py:246-263 / quant_cpu.cpp:64-137, bit-identical codes and
+        scales.  Host tensors return None, which the contract defines as
+        "the caller runs the torch quantizer" (fp8_tile.py:96-113).
+        """
+        if not (isinstance(w32, torch.Tensor) and w32.is_cuda):
+            return None
+        if tile <= 0:
+            raise ValueError(f"tile must be > 0, got {tile}")
+        if w32.dim() != 2 or w32.dtype != torch.float32:
+            raise RuntimeError(f"fp8_quantize_tiles: w32 must be 2-D float32, got {w32.dtype} dim {w32.dim()}")
+        from smaulnative_amd import codebook
+        lib = _lib.load()
+        w = w32 if w32.is_contiguous() else w32.contiguous()
+        out_f, in_f = w.shape
+        nt = (in_f + tile - 1) // tile
+        dev = w.device
+        _, mids, order8 = codebook.encode_tables(dev)
+        codes = torch.empty(out_f, nt * tile, dtype=torch.uint8, device=dev)
+        sc = torch.empty(out_f, nt, dtype=torch.float32, device=dev)
+        bad = torch.empty(1, dtype=torch.int64, device=dev)
+        with torch.cuda.device(dev):
+            rc = lib.smaul_fp8_quantize_tiles(w.data_ptr(), out_f, in_f, tile, order8.data_ptr(), mids.data_ptr(),
+                                              codes.data_ptr(), nt * tile, sc.data_ptr(), bad.data_ptr(),
+                                              _stream_handle(dev))
+        _lib.check(rc, "fp8_quantize_tiles")
+        return codes, sc, int(bad.item())
 
     # ---- linear attention (compute.py:265-322, attn_cpu.cpp) ---------------
     @staticmethod
