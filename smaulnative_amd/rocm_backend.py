@@ -319,6 +319,13 @@ class RocmBackend:
             weakref.finalize(t, _call_weak, evict, key, ent)
         return ent
 
+    def prepare_experts(self, experts, d, h, tile):
+        """Build the repack cache entry of a set of expert buffers ahead of the
+        first forward (the loader calls this after reading a checkpoint)."""
+        if not experts or not experts[0][0].is_cuda:
+            raise RuntimeError("prepare_experts: rocm backend needs HIP device tensors")
+        self._expert_entry(experts, experts[0][0].device, d, h, tile)
+
     def _evict(self, key, ent):
         with self._lock:
             if self._ptr_cache.get(key) is ent:
