@@ -772,19 +772,24 @@ fp8_gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) zacc[r] = 0.0f;
 
+  // One stage: both column tiles' codes decoded first (B fragments for all
+  // FN tiles), then the FM x FN 32x32 tiles in order t = i * FN + j.  The
+  // MFMA chain of tile t is issued before the scale FMAs of tile t - 1, which
+  // by then have their partial: the matrix core works on tile t while the
+  // VALU applies the previous tile's scales (a wave issues in order, so the
+  // reverse order would leave one unit idle while the other works).  A
+  // fragments are held for two row tiles at a time, the next one read from
+  // LDS while the current one is used.
   auto compute_stage = [&](int buf) {
     const char* base = smem + buf * STAGE;
-    bf16x8_t af[FM][4];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) af[i][ks] = *(const bf16x8_t*)(base + a_addr[ks] + i * 32 * 128);
+    bf16x8_t bfr[FN][4];
+    float sc[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int dj = b_row(j) - b_row(0);
       const uint4 c0 = *(const uint4*)(base + b_addr[0] + dj * 64);
       const uint4 c1 = *(const uint4*)(base + b_addr[1] + dj * 64);
-      const float sc = *(const float*)(base + s_addr + dj * 4);
+      sc[j] = *(const float*)(base + s_addr + dj * 4);
       uint32_t d[16];
       decode4<CANON>(c0.x, d[0], d[1]);
       decode4<CANON>(c0.y, d[2], d[3]);
@@ -794,20 +799,39 @@ fp8_gemm_dma_kernel(GemmArgs p) {
       decode4<CANON>(c1.y, d[10], d[11]);
       decode4<CANON>(c1.z, d[12], d[13]);
       decode4<CANON>(c1.w, d[14], d[15]);
-      bf16x8_t bfr[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
-        bfr[ks] = __builtin_bit_cast(bf16x8_t, make_uint4(d[4 * ks], d[4 * ks + 1], d[4 * ks + 2], d[4 * ks + 3]));
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        f32x16_t q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][0], bfr[0], zacc, 0, 0, 0);
-        q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][1], bfr[1], q, 0, 0, 0);
-        q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][2], bfr[2], q, 0, 0, 0);
-        q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][3], bfr[3], q, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(sc, q[r], acc[i][j][r]);
-      }
+        bfr[j][ks] = __builtin_bit_cast(bf16x8_t, make_uint4(d[4 * ks], d[4 * ks + 1], d[4 * ks + 2], d[4 * ks + 3]));
     }
+    bf16x8_t af[2][4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) af[0][ks] = *(const bf16x8_t*)(base + a_addr[ks]);
+    f32x16_t qp;
+#pragma unroll
+    for (int t = 0; t < FM * FN; ++t) {
+      const int i = t / FN, j = t % FN;
+      if (j == 0 && i + 1 < FM) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          af[(i + 1) & 1][ks] = *(const bf16x8_t*)(base + a_addr[ks] + (i + 1) * 32 * 128);
+      }
+      // one MFMA of tile t, then four of tile t - 1's FMAs, four times over;
+      // the scheduling fences keep that order
+      f32x16_t q = zacc;
+      const int pi = (t - 1) / FN, pj = (t - 1) % FN;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i & 1][ks], bfr[j][ks], q, 0, 0, 0);
+        if (t > 0) {
+#pragma unroll
+          for (int r = ks * 4; r < ks * 4 + 4; ++r) acc[pi][pj][r] = __builtin_fmaf(sc[pj], qp[r], acc[pi][pj][r]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      qp = q;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[FM - 1][FN - 1][r] = __builtin_fmaf(sc[FN - 1], qp[r], acc[FM - 1][FN - 1][r]);
   };
 
   // ---- the pipeline ----------------------------------------------------------
