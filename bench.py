@@ -162,19 +162,19 @@ def c2_bench(be, steps, warmup):
         be.swiffn_forward(x, bufs, 64)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     n = max(steps, 50)
-    ev0.record(stream)
-    for _ in range(n):
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for e0, e1 in evs:
+        e0.record(stream)
         be.swiffn_forward(x, bufs, 64)
-    ev1.record(stream)
+        e1.record(stream)
     torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / n
+    ms = statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
     flops = 6.0 * rows * d * h
     return {"workload": "C2 dense SwiGLU FFN: 4096 x 512 -> 2 x 1280 (fused gate+up) -> 512, bf16, tile 64",
             "tokens_per_s": rows / (ms * 1e-3), "ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
             "mfma_frac": flops / (ms * 1e-3) / PEAK_BF16_FLOPS, "flops_per_step": flops,
-            "timing": f"HIP events around {n} back-to-back calls on the launch stream"}
+            "timing": f"median of {n} back-to-back calls, each between two HIP events on the launch stream"}
 
 
 def cpu_model():

@@ -141,6 +141,64 @@ struct GemmArgs {
   int E;
 };
 
+// The expert segment of m-tile mt of a grouped GEMM, with all of its loads
+// in one round trip: lane j reads tile_off[j], tile_off[j + 1], seg_off[j],
+// seg_off[j + 1] and expert j's pointers, and the expert is the number of
+// lanes whose tiles end at or before mt (tile_off is non-decreasing).
+// Dense calls (no segment table) have one expert covering rows [0, R).
+// Returns false when mt is past the last tile (uniform).
+struct TileSeg {
+  int e, row0, rows;
+  const uint8_t* w1;
+  const float* s1;
+  const uint8_t* w2;
+  const float* s2;
+};
+
+template <int BM>
+__device__ __forceinline__ bool tile_lookup(const GemmArgs& p, int mt, int lane, TileSeg& t) {
+  if (!p.seg_off) {
+    t.e = 0;
+    t.row0 = mt * BM;
+    t.rows = (int)min<int64_t>(BM, p.R - t.row0);
+    t.w1 = p.wp ? p.wp[0] : p.w;
+    t.s1 = p.sp ? p.sp[0] : p.s;
+    t.w2 = p.wp2 ? p.wp2[0] : p.w2;
+    t.s2 = p.sp2 ? p.sp2[0] : p.s2;
+    return t.rows > 0;
+  }
+  const bool live = lane < p.E;
+  const int to0 = live ? p.tile_off[lane] : 0;
+  const int to1 = live ? p.tile_off[lane + 1] : 0x7fffffff;
+  const int so0 = live ? p.seg_off[lane] : 0;
+  const int so1 = live ? p.seg_off[lane + 1] : 0;
+  uint64_t w1 = 0, s1 = 0, w2 = 0, s2 = 0;
+  if (live) {
+    w1 = (uint64_t)(uintptr_t)(p.wp ? p.wp[lane] : p.w + lane * p.w_estride);
+    s1 = (uint64_t)(uintptr_t)(p.sp ? p.sp[lane] : p.s + lane * p.s_estride);
+    if (p.wp2 || p.w2) {
+      w2 = (uint64_t)(uintptr_t)(p.wp2 ? p.wp2[lane] : p.w2 + lane * p.w_estride);
+      s2 = (uint64_t)(uintptr_t)(p.sp2 ? p.sp2[lane] : p.s2 + lane * p.s_estride);
+    }
+  }
+  const int total = __builtin_amdgcn_readlane(to1, p.E - 1);
+  if (mt >= total) return false;
+  const int e = (int)__popcll(__ballot(to1 <= mt));
+  t.e = e;
+  t.row0 = __builtin_amdgcn_readlane(so0, e) + (mt - __builtin_amdgcn_readlane(to0, e)) * BM;
+  t.rows = min(BM, __builtin_amdgcn_readlane(so1, e) - t.row0);
+  auto lane_ptr = [&](uint64_t v) -> uint64_t {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, e);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), e);
+    return ((uint64_t)hi << 32) | lo;
+  };
+  t.w1 = (const uint8_t*)(uintptr_t)lane_ptr(w1);
+  t.s1 = (const float*)(uintptr_t)lane_ptr(s1);
+  t.w2 = (const uint8_t*)(uintptr_t)lane_ptr(w2);
+  t.s2 = (const float*)(uintptr_t)lane_ptr(s2);
+  return t.rows > 0;
+}
+
 // KMODE: how scale tiles line up with the 64-wide K stages.
 //   0: tile == 32   (two scale tiles per stage, one MFMA each)
 //   1: tile == 64   (one scale tile per stage)
@@ -214,28 +272,19 @@ fp8_gemm_kernel(GemmArgs p) {
       nt_idx = lin % n_tiles;
     }
   }
-  int e = 0, row0, rows_here;
-  if (p.seg_off) {
-    const int total = p.tile_off[p.E];
-    if (mt >= total) return;
-    while (p.tile_off[e + 1] <= mt) ++e;
-    row0 = p.seg_off[e] + (mt - p.tile_off[e]) * BM;
-    rows_here = min(BM, p.seg_off[e + 1] - row0);
-  } else {
-    row0 = mt * BM;
-    rows_here = (int)min<int64_t>(BM, p.R - row0);
-  }
-  if (rows_here <= 0) return;
+  TileSeg ts;
+  if (!tile_lookup<BM>(p, mt, lane, ts)) return;  // uniform per workgroup
+  const int row0 = ts.row0, rows_here = ts.rows;
   const int n0 = nt_idx * BNO;
   const int64_t K = p.K, N = p.N, nt = p.nt;
 
-  const uint8_t* W1 = p.wp ? p.wp[e] : p.w + e * p.w_estride;
-  const float* S1 = p.sp ? p.sp[e] : p.s + e * p.s_estride;
+  const uint8_t* W1 = ts.w1;
+  const float* S1 = ts.s1;
   const uint8_t* W2 = W1;
   const float* S2 = S1;
   if constexpr (SWIGLU) {
-    W2 = p.wp2 ? p.wp2[e] : p.w2 + e * p.w_estride;
-    S2 = p.sp2 ? p.sp2[e] : p.s2 + e * p.s_estride;
+    W2 = ts.w2;
+    S2 = ts.s2;
   }
 
   // ---- per-thread staging assignments --------------------------------------
@@ -662,28 +711,19 @@ fp8_gemm_dma_kernel(GemmArgs p) {
       nt_idx = lin % n_tiles;
     }
   }
-  int e = 0, row0, rows_here;
-  if (p.seg_off) {
-    const int total = p.tile_off[p.E];
-    if (mt >= total) return;
-    while (p.tile_off[e + 1] <= mt) ++e;
-    row0 = p.seg_off[e] + (mt - p.tile_off[e]) * BM;
-    rows_here = min(BM, p.seg_off[e + 1] - row0);
-  } else {
-    row0 = mt * BM;
-    rows_here = (int)min<int64_t>(BM, p.R - row0);
-  }
-  if (rows_here <= 0) return;
+  TileSeg ts;
+  if (!tile_lookup<BM>(p, mt, lane, ts)) return;  // uniform per workgroup
+  const int row0 = ts.row0, rows_here = ts.rows;
   const int n0 = nt_idx * BNO;
   const int64_t K = p.K, nt = p.nt;
 
-  const uint8_t* W1 = p.wp ? p.wp[e] : p.w + e * p.w_estride;
-  const float* S1 = p.sp ? p.sp[e] : p.s + e * p.s_estride;
+  const uint8_t* W1 = ts.w1;
+  const float* S1 = ts.s1;
   const uint8_t* W2 = W1;
   const float* S2 = S1;
   if constexpr (SWIGLU) {
-    W2 = p.wp2 ? p.wp2[e] : p.w2 + e * p.w_estride;
-    S2 = p.sp2 ? p.sp2[e] : p.s2 + e * p.s_estride;
+    W2 = ts.w2;
+    S2 = ts.s2;
   }
 
   // ---- DMA source offsets of this lane (32-bit; the host checks the range) --
