@@ -320,6 +320,17 @@ int smaul_fp8_quantize_tiles(const float* w, int64_t out_f, int64_t in_f, int64_
                              unsigned long long* nonfinite, hipStream_t stream);
 
 /*
+ * Input gradient of the tiled-FP8 linear: dx[rows, in_f] = g[rows, out_f] .
+ * decode(w, s), fp32.  Replaces the reference's native fp8_backward_input
+ * (kernel/fp8_cpu.cpp:167-259; backend entry kernel/compute.py:145-153).
+ * g fp32 [rows, out_f] row-major; w uint8 [out_f, in_f]; s fp32
+ * [out_f, ceil(in_f/tile)]; any tile > 0.  The sum runs in another fp32 order
+ * than the reference's, so results agree to fp32 rounding, not bitwise.
+ */
+int smaul_fp8_backward_input(const float* g, const uint8_t* w, const float* s, float* dx, int64_t rows,
+                             int64_t in_f, int64_t out_f, int64_t tile, hipStream_t stream);
+
+/*
  * Host-side self-test of the top-k selection order used by the router (no GPU
  * involved): writes the k indices the router would select for `vals` [n].
  * Exposed only so the CPU test suite can check the order against torch.topk.

@@ -14,6 +14,7 @@ checkout):
 - ``quantize_tiles``    kernel/fp8_tile.py:82-119 (the torch path)
 - ``decode_tile``       kernel/fp8_tile.py:121-131
 - ``fp8_forward``       kernel/fp8_cpu.cpp:49-141 via ``fp8_gemm.c`` (C, bit-exact)
+- ``fp8_backward_input`` kernel/fp8_cpu.cpp:167-259 via ``fp8_gemm.c`` (C, bit-exact)
 - ``fp8_linear``        kernel/fp8_tile.py:163-170 (_Fn.forward dtype handling)
 - ``swiffn_forward``    model.py:289-290
 - ``moe_forward``       model.py:557-585 (router, top-k, mask dispatch, combine)
@@ -32,6 +33,8 @@ How each piece is pinned (tests/test_oracle.py):
 - fp8_forward: bit-exact against the reference's own fp8_cpu.cpp built under
   oracle/_ref (when present), against golden vectors written from it, and
   against brute force x @ decode(W).T on tiny shapes.
+- fp8_backward_input: bit-exact against the same reference build on shapes
+  that take both of its arithmetic orders, and against g @ decode(W).
 - quantize_tiles: golden codes/scales from the reference quantizer on the
   special-value cases of tests/test_linear_fp8.py:484-510.
 - moe_forward: golden outputs, probabilities, top-k indices and counts of the
@@ -153,6 +156,8 @@ def _load_lib():
         lib.oracle_fp8_forward.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4 + [ctypes.c_int]
         lib.oracle_fp8_forward.restype = ctypes.c_int
         lib.oracle_e4m3_lut.argtypes = [ctypes.c_void_p]
+        lib.oracle_fp8_backward_input.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4 + [ctypes.c_int]
+        lib.oracle_fp8_backward_input.restype = ctypes.c_int
         lib.oracle_attn_forward.argtypes = [ctypes.c_void_p] * 7 + [ctypes.c_int64] * 4 + [ctypes.c_float]
         lib.oracle_attn_forward.restype = ctypes.c_int
         lib.oracle_attn_step.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int64] * 3 + [ctypes.c_float]
@@ -194,6 +199,24 @@ def fp8_forward(x, w, s, in_f, out_f, tile=TILE, threads: Optional[int] = None):
     if rc != 0:
         raise RuntimeError(f"oracle_fp8_forward failed ({rc})")
     return y
+
+
+def fp8_backward_input(g, w, s, in_f, out_f, tile=TILE, threads: Optional[int] = None):
+    """Reference fp8_backward_input semantics (fp8_cpu.cpp:167-259), C restatement.
+
+    g fp32 [rows, out_f]; w uint8 [out_f, in_f]; s fp32 [out_f, nt].  Returns
+    dx fp32 [rows, in_f] = g . decode(w, s).
+    """
+    gc = g.detach().cpu().float().contiguous()
+    wc = w.detach().cpu().reshape(-1).contiguous()
+    sc = s.detach().cpu().float().reshape(-1).contiguous()
+    rows = gc.shape[0]
+    dx = torch.empty(rows, in_f, dtype=torch.float32)
+    rc = _load_lib().oracle_fp8_backward_input(gc.data_ptr(), wc.data_ptr(), sc.data_ptr(), dx.data_ptr(),
+                                               rows, in_f, out_f, tile, threads or default_threads())
+    if rc != 0:
+        raise RuntimeError(f"oracle_fp8_backward_input failed ({rc})")
+    return dx
 
 
 def ref_module():

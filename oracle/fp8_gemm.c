@@ -115,3 +115,72 @@ int oracle_fp8_forward(const float* x, const uint8_t* w, const float* s, float* 
   }
   return 0;
 }
+
+/*
+ * Backward-input, fp8_cpu.cpp:167-259: dx[r, i] = sum_o g[r, o] * W[o, i].
+ * Tasks of RB=16 rows x IB=8 input columns; the output dimension runs in
+ * blocks of 64.  A block takes the "fast" order (fp8_cpu.cpp:182-206) when the
+ * task is exactly 16 x 8 and the block a whole 64: w = lut*s rounded first,
+ * eight accumulators a0..a7 (a0 continuing the running total, the others from
+ * zero), a_j += g[o]*w[o] for o = j (mod 8), then ((a0+a1)+(a2+a3)) +
+ * ((a4+a5)+(a6+a7)).  Every other block (fp8_cpu.cpp:208-214) adds
+ * (g*lut)*s to the running total in o order.
+ */
+static void backward_task(const float* gp, const uint8_t* wp, const float* sp, float* dxp, int64_t in_f,
+                          int64_t out_f, int64_t nt, int64_t tile, int64_t r0, int64_t RB, int64_t ib0,
+                          int64_t IBR) {
+  float acc[16][8];
+  float wsub[64][8];
+  for (int64_t r = 0; r < RB; ++r)
+    for (int64_t k = 0; k < IBR; ++k) acc[r][k] = 0.0f;
+  for (int64_t ob = 0; ob < out_f; ob += 64) {
+    const int64_t OBR = (out_f - ob) < 64 ? (out_f - ob) : 64;
+    if (RB == 16 && IBR == 8 && OBR == 64) {
+      for (int64_t o2 = 0; o2 < 64; ++o2)
+        for (int64_t k2 = 0; k2 < 8; ++k2) {
+          const int64_t o = ob + o2, i = ib0 + k2;
+          wsub[o2][k2] = g_lut[wp[o * in_f + i]] * sp[o * nt + i / tile];
+        }
+      for (int64_t r = 0; r < 16; ++r) {
+        const float* gr = gp + (r0 + r) * out_f + ob;
+        for (int64_t k2 = 0; k2 < 8; ++k2) {
+          float a[8];
+          a[0] = acc[r][k2];
+          for (int j = 1; j < 8; ++j) a[j] = 0.0f;
+          for (int64_t o2 = 0; o2 < 64; o2 += 8)
+            for (int j = 0; j < 8; ++j) a[j] = a[j] + gr[o2 + j] * wsub[o2 + j][k2];
+          acc[r][k2] = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+        }
+      }
+    } else {
+      for (int64_t o2 = 0; o2 < OBR; ++o2) {
+        const int64_t o = ob + o2;
+        for (int64_t r = 0; r < RB; ++r) {
+          const float gv = gp[(r0 + r) * out_f + o];
+          for (int64_t k2 = 0; k2 < IBR; ++k2) {
+            const int64_t i = ib0 + k2;
+            acc[r][k2] = acc[r][k2] + gv * g_lut[wp[o * in_f + i]] * sp[o * nt + i / tile];
+          }
+        }
+      }
+    }
+  }
+  for (int64_t r = 0; r < RB; ++r)
+    for (int64_t k = 0; k < IBR; ++k) dxp[(r0 + r) * in_f + ib0 + k] = acc[r][k];
+}
+
+int oracle_fp8_backward_input(const float* g, const uint8_t* w, const float* s, float* dx, int64_t rows,
+                              int64_t in_f, int64_t out_f, int64_t tile, int threads) {
+  if (tile <= 0 || in_f < 0 || out_f < 0 || rows < 0) return 1;
+  if (!g_lut_ready) build_lut();
+  const int64_t nt = (in_f + tile - 1) / tile;
+  const int64_t nrb = (rows + 15) / 16, nib = (in_f + 7) / 8;
+#pragma omp parallel for schedule(dynamic, 4) num_threads(threads > 0 ? threads : 1)
+  for (int64_t task = 0; task < nrb * nib; ++task) {
+    const int64_t rb = task / nib, ib = task % nib;
+    const int64_t RB = (rows - rb * 16) < 16 ? (rows - rb * 16) : 16;
+    const int64_t IBR = (in_f - ib * 8) < 8 ? (in_f - ib * 8) : 8;
+    backward_task(g, w, s, dx, in_f, out_f, nt, tile, rb * 16, RB, ib * 8, IBR);
+  }
+  return 0;
+}

@@ -57,6 +57,7 @@ SIGNATURES = {
     "smaul_attn_forward": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P]),
     "smaul_attn_step": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_float, _P]),
     "smaul_fp8_quantize_tiles": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P]),
+    "smaul_fp8_backward_input": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "smaul_selftest_topk": (_I, [_P, _I64, _I64, _P]),
 }
 

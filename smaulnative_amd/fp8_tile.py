@@ -11,9 +11,10 @@ fp32 master weight (kernel/fp8_tile.py:199-215).
 backend's ``fp8_forward`` and returns it in x's dtype (kernel/fp8_tile.py:
 163-170, 237-239).  On the rocm backend bf16 activations go to the kernel as
 they are (a bf16 value widened to fp32 is the same number).  The backward
-asks the backend for ``fp8_backward_input``, which the rocm backend does not
-provide, so training stops with NotImplementedError rather than producing
-wrong gradients.
+takes the input gradient from the backend's ``fp8_backward_input`` and, in
+training mode, adds the weight gradient to the module's bf16 ``_gw`` in
+64-row blocks -- the storage the reference's optimizers read
+(kernel/fp8_tile.py:172-197); there is no fp32 master weight.
 
 ``quantize_tiles`` gives the reference's codes and scales bit for bit: the
 backend's device quantizer for HIP tensors (``fp8_quantize_tiles``), and the
@@ -78,11 +79,17 @@ def decode_tile(w, s, o0, o1, t, tile=TILE, dtype=torch.float32):
     return lut[w[o0:o1, t * tile:(t + 1) * tile].long()] * s[o0:o1, t].to(dtype).unsqueeze(1)
 
 
+GRAD_DTYPE = torch.bfloat16   # storage of the accumulated weight gradient (kernel/fp8_tile.py:26)
+_GRAD_ROWS = 64               # weight-gradient rows added (and rounded) per step
+
+
 class _FP8Matmul(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, w8, sc, in_f, out_f, tile):
-        ctx.save_for_backward(w8, sc)
+    def forward(ctx, x, w8, sc, in_f, out_f, tile, module):
+        training = module is not None and module.training
+        ctx.save_for_backward(x if training else None, w8, sc)
         ctx.dims = (in_f, out_f, tile, x.shape)
+        ctx.module = module if training else None
         rows = x.reshape(-1, in_f)
         if not (rows.is_cuda and rows.dtype == torch.bfloat16):
             rows = rows.float()
@@ -91,11 +98,24 @@ class _FP8Matmul(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad):
-        w8, sc = ctx.saved_tensors
+        x, w8, sc = ctx.saved_tensors
         in_f, out_f, tile, xshape = ctx.dims
-        gx = get_backend().fp8_backward_input(grad.reshape(-1, out_f).float().contiguous(), w8, sc,
-                                              in_f, out_f, tile)
-        return gx.reshape(xshape), None, None, None, None, None
+        g = grad.reshape(-1, out_f).float().contiguous()
+        gx = None
+        if ctx.needs_input_grad[0]:
+            gx = get_backend().fp8_backward_input(g, w8, sc, in_f, out_f, tile).reshape(xshape)
+        m = ctx.module
+        if m is not None:
+            # the weight gradient accumulates in the module's bf16 _gw, which the
+            # reference's optimizers read and clear (kernel/fp8_tile.py:172-197):
+            # each 64-row block of g^T x is formed in fp32 and rounded once
+            xr = x.reshape(-1, in_f).float()
+            if m._gw is None or m._gw.device != g.device:
+                m._gw = torch.zeros(out_f, in_f, dtype=GRAD_DTYPE, device=g.device)
+            for o0 in range(0, out_f, _GRAD_ROWS):
+                o1 = min(o0 + _GRAD_ROWS, out_f)
+                m._gw[o0:o1].add_(g[:, o0:o1].t() @ xr)
+        return gx, None, None, None, None, None, None
 
 
 class FP8Linear(nn.Module):
@@ -114,6 +134,7 @@ class FP8Linear(nn.Module):
         self.register_buffer("w8", w8)
         self.register_buffer("sc", sc)
         self.bias = nn.Parameter(torch.zeros(out_f)) if bias else None
+        self._gw = None  # accumulated weight gradient (training), GRAD_DTYPE [out_f, in_f]
 
     @classmethod
     def from_float(cls, lin, tile=TILE):
@@ -128,7 +149,7 @@ class FP8Linear(nn.Module):
         return m
 
     def forward(self, x):
-        y = _FP8Matmul.apply(x, self.w8, self.sc, self.in_f, self.out_f, self.tile)
+        y = _FP8Matmul.apply(x, self.w8, self.sc, self.in_f, self.out_f, self.tile, self)
         return y if self.bias is None else y + self.bias
 
     def extra_repr(self):

@@ -20,8 +20,9 @@ Behaviour differences from the reference CPU backend, all deliberate:
 - ``fp8_quantize_tiles`` quantizes HIP tensors on the device (bit-identical
   codes and scales); for host tensors it returns ``None``, which the contract
   defines as "run the torch quantizer" (compute.py:246-263, fp8_tile.py:96-113);
-- training entry points (backward, attention backward, sparse) are not part
-  of this path and raise ``NotImplementedError``.
+- ``fp8_backward_input`` (the FP8Linear input gradient) runs on the device;
+  the attention backward and ``sparse_grad_v`` (Rawr) are not built and
+  raise ``NotImplementedError``.
 """
 from __future__ import annotations
 
@@ -146,7 +147,30 @@ class RocmBackend:
         return y
 
     def fp8_backward_input(self, g, w, s, in_f, out_f, tile):
-        raise NotImplementedError("rocm backend: fp8_backward_input (training) is not implemented")
+        """dx[rows, in_f] fp32 = g[rows, out_f] . decode(w, s) on the device
+        (compute.py:145-153, fp8_cpu.cpp:167-259; fp32, another summation order)."""
+        if tile <= 0 or in_f <= 0 or out_f <= 0:
+            raise ValueError(f"tile/in_f/out_f must be positive, got {tile}/{in_f}/{out_f}")
+        lib = _lib.load()
+        _need_device("fp8_backward_input", g, w, s)
+        if g.dtype != torch.float32 or w.dtype != torch.uint8:
+            raise RuntimeError(f"fp8_backward_input: expected dtypes f32/u8, got {g.dtype}/{w.dtype}")
+        if g.dim() != 2 or g.shape[1] != out_f:
+            raise RuntimeError(f"fp8_backward_input: g must be [rows, out_f={out_f}], got {tuple(g.shape)}")
+        nt = (in_f + tile - 1) // tile
+        if w.numel() != out_f * in_f or s.numel() != out_f * nt:
+            raise RuntimeError(f"fp8_backward_input: size mismatch w={w.numel()} s={s.numel()} expected "
+                               f"{out_f * in_f} and {out_f * nt}")
+        gc = g if g.is_contiguous() else g.contiguous()
+        wc = w.reshape(-1).contiguous()
+        sc = s.reshape(-1)
+        sc = (sc if sc.dtype == torch.float32 else sc.float()).contiguous()
+        dx = torch.empty(g.shape[0], in_f, dtype=torch.float32, device=g.device)
+        with torch.cuda.device(g.device):
+            rc = lib.smaul_fp8_backward_input(gc.data_ptr(), wc.data_ptr(), sc.data_ptr(), dx.data_ptr(), g.shape[0],
+                                              in_f, out_f, tile, _stream_handle(g.device))
+        _lib.check(rc, "fp8_backward_input")
+        return dx
 
     def fp8_quantize_tiles(self, w32, tile):
         """(codes uint8 [out_f, nt*tile], scales fp32 [out_f, nt], non-finite count) on the device.

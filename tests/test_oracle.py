@@ -277,3 +277,21 @@ def test_attn_oracle_textbook_and_closed_forms():
     Yz, DENz, Sz, zz = oracle.attn_forward(Q1, torch.zeros_like(K1), V1)
     assert torch.equal(Yz, torch.zeros_like(Yz)) and float(DENz.max()) == np.float32(1e-6)
     assert torch.equal(Sz, torch.zeros_like(Sz))
+
+
+@pytest.mark.skipif(oracle.ref_module() is None, reason="oracle/_ref (reference fp8_cpu.cpp) not built")
+@pytest.mark.parametrize("rows,in_f,out_f,tile", [(64, 128, 128, 64), (33, 70, 100, 64), (16, 8, 64, 64),
+                                                  (50, 300, 130, 32), (17, 96, 200, 128)])
+def test_backward_input_bit_exact_with_reference_kernel(rows, in_f, out_f, tile):
+    """The C restatement of fp8_backward_input (eight-way split fast path and
+    the (g*lut)*s remainder) against the reference's own kernel, bit for bit,
+    and against the decoded-weight product."""
+    gen = torch.Generator().manual_seed(rows + in_f + out_f)
+    g = torch.randn(rows, out_f, generator=gen)
+    w, s = oracle.quantize_tiles(torch.randn(out_f, in_f, generator=gen) * 0.05, tile)
+    dx = oracle.fp8_backward_input(g, w, s, in_f, out_f, tile)
+    ref = oracle.ref_module().fp8_backward_input(g, w.reshape(-1).contiguous(), s.reshape(-1).contiguous(),
+                                                 in_f, out_f, tile)
+    assert torch.equal(dx, ref)
+    bf = g.double() @ oracle.decode_full(w, s, tile).double()
+    assert float((dx.double() - bf).abs().max() / bf.abs().max()) < 1e-5
