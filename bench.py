@@ -14,7 +14,9 @@ Extra objects on the same JSON line:
   FLOPs per launch / its mean duration, from HIP events recorded on the
   stream it is launched on, around each launch inside a full layer;
   ``traffic`` is the calibrated HBM bytes per launch read from the committed
-  rocprofv3 summary profiles/gate_up_c3_traffic.txt (not measured in this run);
+  rocprofv3 summary profiles/moe_kernels_hbm_traffic.txt (not measured in this
+  run); profiles/moe_kernels_trace.txt recomputes ``frac`` from the kernel
+  trace of the same launches;
 - ``cpu_baseline``: the reference CPU path on this host's cores -- the
   reference's own fp8_cpu.cpp (built under oracle/_ref) inside the torch MoE
   loop of model.py:557-585 -- on bounded samples of the config-3 and config-5
@@ -107,17 +109,22 @@ def time_layer(be, xd, gwd, gbd, exd, k, steps, warmup):
 
 
 def time_stages(be, xd, gwd, gbd, exd, k, steps, warmup=2):
-    """Mean per-stage device time from HIP events on the launch stream."""
+    """Mean per-stage device time from HIP events on the launch stream.
+
+    The layers run back to back with one synchronisation at the end, so the
+    stages are timed under the same sustained load as the headline loop (a
+    synchronisation per layer leaves idle gaps in which the clock recovers).
+    """
     import torch
     names = ["router", "dispatch", "gate_up", "down", "combine"]
-    acc = [0.0] * 5
+    evs = []
     for it in range(steps + warmup):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
         be.moe_stages(xd, gwd, gbd, exd, k, 64, events=ev)
-        torch.cuda.synchronize()
         if it >= warmup:
-            for i in range(5):
-                acc[i] += ev[i].elapsed_time(ev[i + 1])
+            evs.append(ev)
+    torch.cuda.synchronize()
+    acc = [sum(ev[i].elapsed_time(ev[i + 1]) for ev in evs) for i in range(5)]
     return {n: a / steps for n, a in zip(names, acc)}
 
 
@@ -331,7 +338,7 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
 
 def read_traffic():
     """HBM bytes per gate_up launch from the committed rocprofv3 --pmc summary, if any."""
-    p = os.path.join(HERE, "profiles", "gate_up_c3_traffic.txt")
+    p = os.path.join(HERE, "profiles", "moe_kernels_hbm_traffic.txt")
     if not os.path.exists(p):
         return None
     for line in open(p):
@@ -399,8 +406,10 @@ def main():
             "frac": fl["gate_up"] / gu_s / PEAK_BF16_FLOPS, "traffic": read_traffic(),
             "flops_per_launch": fl["gate_up"], "mean_launch_ms": stages["gate_up"],
             "timing": f"HIP events on the launch stream around the gate_up launch of {n_stage} full layers "
-                      "(after 2 untimed layers), mean",
-            "traffic_source": "profiles/gate_up_c3_traffic.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)"}
+                      "run back to back after 2 untimed ones, mean; profiles/moe_kernels_trace.txt recomputes "
+                      "frac from the rocprofv3 kernel trace of the same launches",
+            "traffic_source": "committed summary profiles/moe_kernels_hbm_traffic.txt (rocprofv3 FETCH_SIZE + "
+                              "WRITE_SIZE, calibrated against a copy kernel), not measured in this run"}
     res = {
         "metric": METRIC,
         "value": T / sec,
