@@ -259,7 +259,13 @@ int smaul_moe_forward_norm(const void* x, int act_dtype, const float* gate_w, co
  *     into next_prob [T, next_E], next_topi / next_topw [T, next_k], equal
  *     bit for bit to smaul_moe_router(norm_out, ...).  For bf16, next_E <= 16
  *     and d <= 2048 (d % 16 == 0) the router runs inside the combine + norm
- *     kernel; otherwise it is launched after it.
+ *     kernel; otherwise it is launched after it.  In the decode regime
+ *     (T <= 64, bf16, d <= 1024, 4 < next_E <= 16, canonical codes, an 8-wave
+ *     down instance) that combine + norm + router runs in the tail of the
+ *     down-projection kernel instead, with the same results: the first
+ *     workgroups to finish their units wait for the rest through a counter
+ *     in the workspace (cleared by the gate/up kernel of the same call), so
+ *     two calls must not share one workspace concurrently.
  * out, norm_out, counts and (when not routed) prob/topi/topw are written as
  * by smaul_moe_forward_norm.  No counterpart entry in the reference: its
  * layers run the norm and the next router as separate calls.

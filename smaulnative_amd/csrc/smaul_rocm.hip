@@ -106,6 +106,19 @@ __device__ __forceinline__ uint4 ldg16(const void* p) {
 }
 __device__ __forceinline__ float ldgf(const float* p) { return *(g_fp)p; }
 
+// Device-coherent reads of data that other workgroups of the same launch wrote
+// (with device-scope stores, see coh_store16): a raw buffer load with the
+// device-scope cache policy (sc1) is served past this XCD's L2, which may hold
+// a stale copy of the line.  The descriptor covers `bytes` bytes from p
+// (word 3 is the gfx9 raw-buffer format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const void* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 coh_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16 /* sc1 */);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // silu(v) = v / (1 + e^-v) with the hardware exp2 and reciprocal (about two
 // ulp in fp32).  Every caller rounds the result to the activation dtype or
 // compares it at a tolerance far above that.
@@ -1912,7 +1925,9 @@ struct DsRing {
 
 // ridx: logical row -> activation row (SwiGLU only; down reads its rows in
 // place).
-template <bool SWIGLU, bool CANON, int KBW, int NRT>
+// COH: the outputs are stored with device scope, for workgroups of the same
+// launch that read them (the fused combine of decode_stream_kernel).
+template <bool SWIGLU, bool CANON, int KBW, int NRT, bool COH = false>
 __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, const int32_t* ridx, int u0,
                                         int u1, int ctn, float* red, int nw) {
   constexpr int NH = SWIGLU ? 2 : 1;
@@ -2051,7 +2066,11 @@ __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, con
           if (k2 < nw) uu += pu[k2];
         v = silu_f(bf2f(f2bf(g))) * bf2f(f2bf(uu));
       }
-      if (lr < nr) ((uint16_t*)p.y)[(int64_t)(r0 + lr) * p.ldy + (int64_t)ct * 16 + (ln & 15)] = (uint16_t)f2bf(v);
+      if (lr < nr) {
+        uint16_t* dst = (uint16_t*)p.y + (int64_t)(r0 + lr) * p.ldy + (int64_t)ct * 16 + (ln & 15);
+        if constexpr (COH) __hip_atomic_store(dst, (uint16_t)f2bf(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else *dst = (uint16_t)f2bf(v);
+      }
     }
     buf ^= 1;
   };
@@ -2078,7 +2097,33 @@ struct DsDispatch {
   const float* topw;
   RouteOut o;
   int T, k;
+  int32_t* sync;  // non-null: workgroup 0 clears the fused combine's sync words for the down kernel
 };
+
+// The combine + norm + next router fused into the tail of the decode down
+// kernel (CNR): the inputs of combine_norm_route_kernel, and the sync words
+// [arrivals, spin timeouts], cleared by the gate/up kernel of the same layer.
+struct CnrArgs {
+  const int64_t* topi;
+  const float* topw;
+  const int32_t* inv;
+  void* out;
+  const float* weight;
+  float eps;
+  void* norm_out;
+  int64_t T;
+  int d, k;
+  const float* ngw;
+  const float* ngb;
+  RouteOut no;
+  int nE, nk;
+  int32_t* sync;
+  int64_t ybytes;
+};
+constexpr int CNR_TAIL_TOK = 8;         // tokens per combining workgroup (one per wave)
+template <int NCH, int EMAX, bool EXACT, int KSW, int TOK, bool COH>
+struct CnrBlock;
+constexpr int CNR_SPIN_LIMIT = 1 << 20;  // polls of the arrival count before giving up
 
 // FUSED (gate/up only): every workgroup ranks the T <= 64 tokens per expert
 // itself into LDS (one wave, ballot ranks in token order, the same rule as
@@ -2086,9 +2131,18 @@ struct DsDispatch {
 // kernel; workgroup 0 also writes that dispatch (counts, seg_off, tile_off,
 // perm_row, perm_w, inv) for the down projection and the combine.  The
 // top-k is read from dd.topi/dd.topw (the router kernel's output).
-template <bool SWIGLU, bool CANON, int KBW, bool FUSED>
+//
+// CNR (down only, 8 waves): after its units every workgroup waits for its own
+// device-scope output stores, then counts itself in sync[0]; the first
+// ceil(T / 8) workgroups to arrive load what the combine needs besides the
+// outputs (slots, router weights), wait (a bounded poll: the others are
+// already running) until all have arrived, and each then runs the combine,
+// norm and next layer's router for 8 tokens, reading the outputs
+// device-coherently.  This replaces the separate
+// combine_norm_route_kernel launch, with the same arithmetic (CnrBlock).
+template <bool SWIGLU, bool CANON, int KBW, bool FUSED, bool CNR = false, int CEMAX = 8, bool CEXACT = false>
 __global__ void __launch_bounds__(DS_WMAX * 64)
-decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
+decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd, CnrArgs cr) {
   constexpr int NH = SWIGLU ? 2 : 1;
   static_assert(!FUSED || SWIGLU, "the fused dispatch feeds the gate/up projection");
   // the partial sums of the GEMM
@@ -2123,6 +2177,7 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
       }
       if (lane == 0) s_off[p.E] = off;
       if (blockIdx.x == 0) dispatch_one_wave(ti, tw, valid, lane, dd.o, p.E, dd.k);
+      if (blockIdx.x == 0 && lane < 2 && dd.sync) dd.sync[lane] = 0;
     }
     __syncthreads();
     ds_finish(lane < p.E ? s_off[lane] : 0, lane < p.E ? s_off[lane + 1] : 0, lane, sg);
@@ -2133,10 +2188,44 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd) {
   const int64_t U = (int64_t)sg.total * ctn;
   const int u0 = (int)((int64_t)blockIdx.x * U / gridDim.x);
   const int u1 = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
-  if (u0 >= u1) return;  // uniform per workgroup
-  // two row tiles when any segment has more than 16 rows
-  if (__ballot(sg.rows > 16) != 0) ds_body<SWIGLU, CANON, KBW, 2>(p, sg, ridx, u0, u1, ctn, red, nw);
-  else ds_body<SWIGLU, CANON, KBW, 1>(p, sg, ridx, u0, u1, ctn, red, nw);
+  if constexpr (!CNR) {
+    if (u0 >= u1) return;  // uniform per workgroup
+  }
+  if (u0 < u1) {
+    // two row tiles when any segment has more than 16 rows
+    if (__ballot(sg.rows > 16) != 0) ds_body<SWIGLU, CANON, KBW, 2, CNR>(p, sg, ridx, u0, u1, ctn, red, nw);
+    else ds_body<SWIGLU, CANON, KBW, 1, CNR>(p, sg, ridx, u0, u1, ctn, red, nw);
+  }
+  if constexpr (CNR) {
+    static_assert(!SWIGLU, "the combine follows the down projection");
+    __shared__ int s_arrival;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's output stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_arrival = (int)__hip_atomic_fetch_add(cr.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int G = (int)gridDim.x;
+    const int ncw = (int)((cr.T + CNR_TAIL_TOK - 1) / CNR_TAIL_TOK);
+    const int a = s_arrival;
+    if (a >= ncw) return;  // uniform: the first ncw to arrive combine (they wait longest)
+    const int64_t t0 = (int64_t)a * CNR_TAIL_TOK;
+    CnrBlock<1, CEMAX, CEXACT, 4, CNR_TAIL_TOK, true> b;
+    b.prefetch_slots(cr.topi, cr.topw, cr.inv, cr.T, cr.k, t0);
+    b.prefetch_router(cr.ngw, cr.ngb, cr.nE, cr.d);
+    if (threadIdx.x == 0) {
+      int spins = 0;
+      while (__hip_atomic_load(cr.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < G) {
+        if (++spins > CNR_SPIN_LIMIT) {
+          __hip_atomic_fetch_add(cr.sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    __syncthreads();
+    b.finish(p.y, cr.ybytes, cr.out, cr.weight, cr.eps, cr.norm_out, cr.T, cr.d, cr.ngw, cr.ngb, cr.no, cr.nE, cr.nk,
+             t0);
+  }
 }
 
 // K blocks per wave of the streaming decode kernel for K/64 = nkb blocks
@@ -2184,16 +2273,48 @@ int launch_decode_stream(const GemmArgs& a, const DsDispatch* dd, hipStream_t st
   const dim3 grid((unsigned)g), block(nw * 64);
   if constexpr (SWIGLU) {
     if (dd) {
-      hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true>), grid, block, 0, stream, a, nw, *dd);
+      hipLaunchKernelGGL((decode_stream_kernel<true, CANON, 2, true>), grid, block, 0, stream, a, nw, *dd, CnrArgs{});
       return check_launch("decode_stream_kernel");
     }
   }
   if (kbw == 2) {
-    hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 2, false>), grid, block, 0, stream, a, nw, none);
+    hipLaunchKernelGGL((decode_stream_kernel<SWIGLU, CANON, 2, false>), grid, block, 0, stream, a, nw, none, CnrArgs{});
   } else {
-    if constexpr (!SWIGLU) hipLaunchKernelGGL((decode_stream_kernel<false, CANON, 5, false>), grid, block, 0, stream, a, nw, none);
+    if constexpr (!SWIGLU)
+      hipLaunchKernelGGL((decode_stream_kernel<false, CANON, 5, false>), grid, block, 0, stream, a, nw, none, CnrArgs{});
   }
   return check_launch("decode_stream_kernel");
+}
+
+// The decode down projection with the combine + norm + next router in its
+// tail (CNR).  Returns 1 when the shape has no such instance: canonical codes,
+// 8 K-split waves (one per combined token of a workgroup), a router of 4 < E
+// <= 16 experts on d <= 1024, and at least ceil(T / 8) workgroups.
+template <int EMAX, bool EXACT>
+int launch_down_cnr_e(const GemmArgs& a, int kbw, int64_t g, const CnrArgs& cr, hipStream_t stream) {
+  const DsDispatch none{};
+  const dim3 grid((unsigned)g), block(8 * 64);
+  if (kbw == 2)
+    hipLaunchKernelGGL((decode_stream_kernel<false, true, 2, false, true, EMAX, EXACT>), grid, block, 0, stream, a, 8,
+                       none, cr);
+  else
+    hipLaunchKernelGGL((decode_stream_kernel<false, true, 5, false, true, EMAX, EXACT>), grid, block, 0, stream, a, 8,
+                       none, cr);
+  return check_launch("decode_stream_kernel");
+}
+
+int launch_down_cnr(const GemmArgs& a, bool canon, const CnrArgs& cr, hipStream_t stream) {
+  if (!canon || a.N % 16 != 0 || a.E > 64 || cr.d > 1024 || cr.nE <= 4 || cr.nE > 16) return 1;
+  const int64_t nkb = a.K / 64;
+  const int kbw = ds_kbw(nkb, false);
+  if (kbw == 0 || nkb / kbw != 8) return 1;
+  const int64_t ctn = a.N / 16;
+  const int64_t g = std::min<int64_t>(cu_count(), std::max<int64_t>(1, a.E * ctn * (64 / DS_ROWS)));
+  if (g < (cr.T + CNR_TAIL_TOK - 1) / CNR_TAIL_TOK) return 1;
+  if (cr.nE == 16) return launch_down_cnr_e<16, true>(a, kbw, g, cr, stream);
+  if (cr.nE > 8) return launch_down_cnr_e<16, false>(a, kbw, g, cr, stream);
+  if (cr.nE == 8) return launch_down_cnr_e<8, true>(a, kbw, g, cr, stream);
+  return launch_down_cnr_e<8, false>(a, kbw, g, cr, stream);
 }
 
 template <bool SWIGLU, bool CANON>
@@ -2876,14 +2997,29 @@ struct CombineNormRow {
   static constexpr int VPC = BF16 ? 2 : 4;
   float v[NCH][16];  // the combined row as stored in out (rounded to the dtype)
   float r;           // 1 / rms
+  int rw[8];         // the token's yperm rows (combine_slots order) and weights
+  float wt[8];
+  int n;
 
-  // the combine of the chunks and the row's 1/rms; no store
+  // the combine of the chunks and the row's 1/rms; no store.  COH: yperm
+  // (ybytes long) was written by other workgroups of the running launch and
+  // is read device-coherently.
+  template <bool COH = false>
   __device__ __forceinline__ void compute(const void* yperm, const int64_t* topi, const float* topw,
-                                          const int32_t* inv, float eps, int64_t t, int d, int k, int lane) {
+                                          const int32_t* inv, float eps, int64_t t, int d, int k, int lane,
+                                          int64_t ybytes = 0) {
+    slots(topi, topw, inv, t, k);
+    combine<COH>(yperm, eps, d, lane, ybytes);
+  }
+  // the slot loads alone (they do not depend on yperm)
+  __device__ __forceinline__ void slots(const int64_t* topi, const float* topw, const int32_t* inv, int64_t t,
+                                        int k) {
+    n = combine_slots(topi, topw, inv, t, k, rw, wt);
+  }
+  // the combine of the slots loaded by slots(), and the row's 1/rms
+  template <bool COH = false>
+  __device__ __forceinline__ void combine(const void* yperm, float eps, int d, int lane, int64_t ybytes = 0) {
     const int nch = d / 16;
-    int rw[8];
-    float wt[8];
-    const int n = combine_slots(topi, topw, inv, t, k, rw, wt);
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
@@ -2895,9 +3031,16 @@ struct CombineNormRow {
 #pragma unroll
         for (int s = 0; s < 8; ++s)
           if (s < n) {
-            const char* src = (const char*)yperm + ((int64_t)rw[s] * d + c * 16) * ES;
+            const int64_t off = ((int64_t)rw[s] * d + c * 16) * ES;
+            if constexpr (COH) {
+              const __amdgpu_buffer_rsrc_t yr = coh_rsrc(yperm, ybytes);
 #pragma unroll
-            for (int j = 0; j < VPC; ++j) yv[s][j] = ldg16(src + j * 16);
+              for (int j = 0; j < VPC; ++j) yv[s][j] = coh_load16(yr, (uint32_t)(off + j * 16));
+            } else {
+              const char* src = (const char*)yperm + off;
+#pragma unroll
+              for (int j = 0; j < VPC; ++j) yv[s][j] = ldg16(src + j * 16);
+            }
           }
 #pragma unroll
         for (int s = 0; s < 8; ++s)
@@ -2988,6 +3131,104 @@ constexpr int CNR_DMAX = 2048;  // the MFMA router's widest d
 // Workgroup barrier for LDS data only: waits for this wave's LDS accesses,
 // not for its global stores (__syncthreads waits for those too).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// The combine + norm + next router of the TOK tokens from t0, by the calling
+// workgroup's TOK waves (wave w: token t0 + w; waves < RK_SLICES also run the
+// router's K slices), in three phases: prefetch_slots (the top-k, weights and
+// yperm rows of each token), prefetch_router (the router weights and bias of
+// the K-slice waves) and finish (the rest).  The loads of the first two do not
+// depend on yperm, so a caller that waits for yperm can issue them before it
+// waits.  COH: yperm (ybytes long) was written by other workgroups of the
+// running launch and is read device-coherently.
+template <int NCH, int EMAX, bool EXACT, int KSW, int TOK, bool COH>
+struct CnrBlock {
+  static_assert(EMAX <= 16, "the MFMA router covers up to 16 experts");
+  static constexpr int NWAVES = TOK;
+  // RouteSlice's partial logits: one 16-token MFMA tile per K slice, whatever
+  // TOK (<= 16) is
+  static constexpr int RT = RouteSlice<KSW, 1>::TOK;
+  static_assert(TOK <= RT, "one MFMA token tile");
+  static_assert(NWAVES >= RK_SLICES, "one K slice per router wave");
+  static_assert(TOK * EMAX <= RK_SLICES * 64, "the bias-adding threads are router-wave threads");
+  // (At KSW = 8 the row held through the routing would spill: stored first.)
+  static constexpr bool LATE_STORE = KSW == 4;
+
+  CombineNormRow<true, NCH> cn;
+  RouteSlice<KSW, 1> rs;
+  float bias = 0.0f;
+  bool routed = false;  // router weights and bias loaded
+
+  __device__ __forceinline__ static int nvalid_of(int64_t T, int64_t t0) { return (int)min<int64_t>(TOK, T - t0); }
+
+  __device__ __forceinline__ void prefetch_slots(const int64_t* topi, const float* topw, const int32_t* inv,
+                                                 int64_t T, int k, int64_t t0) {
+    const int wave = threadIdx.x >> 6;
+    if (wave < nvalid_of(T, t0)) cn.slots(topi, topw, inv, t0 + wave, k);  // uniform per wave
+  }
+  __device__ __forceinline__ void prefetch_router(const float* ngw, const float* ngb, int nE, int d) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int E = EXACT ? EMAX : nE;
+    const int re = (int)(threadIdx.x % EMAX);
+    if (wave < RK_SLICES) {  // uniform per wave
+      rs.load_w(ngw, E, d, wave, lane);
+      if (threadIdx.x < (unsigned)(TOK * EMAX) && re < E && ngb) bias = ngb[re];
+    }
+    routed = true;
+  }
+
+  __device__ __forceinline__ void finish(const void* __restrict__ yperm, int64_t ybytes, void* __restrict__ out,
+                                         const float* __restrict__ weight, float eps, void* norm_out, int64_t T,
+                                         int d, const float* __restrict__ ngw, const float* __restrict__ ngb,
+                                         RouteOut no, int nE, int nk, int64_t t0) {
+    __shared__ __attribute__((aligned(16))) float part[RK_SLICES * RT * 16];
+    __shared__ float slog[TOK][EMAX];
+    __shared__ smaul_topk::Pair spair[TOK][EMAX];
+    __shared__ int s_ti[TOK][8];
+    __shared__ float s_tw[TOK][8];
+    __shared__ __attribute__((aligned(16))) uint16_t sx[TOK * CNR_DMAX];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int E = EXACT ? EMAX : nE;
+    const int nvalid = nvalid_of(T, t0);
+    // The combine and norm first, the normed row to LDS only.  Unless
+    // prefetched, the router weights and bias are loaded after the barrier: a
+    // CU returns reads in issue order, so cold weights issued before the
+    // combine's slot reads would hold those up.  The global stores of out /
+    // norm_out go out after the routing MFMAs, so that the wait for the
+    // weights does not also wait for them.
+    const bool mine = wave < nvalid;  // uniform per wave
+    if (mine) {
+      cn.template combine<COH>(yperm, eps, d, lane, ybytes);
+      cn.to_lds(weight, d, lane, (char*)(sx + wave * d));
+      if (!LATE_STORE) cn.store(out, weight, norm_out, t0 + wave, d, lane);
+    }
+    lds_barrier();
+    // route_reduce's thread q = tok * EMAX + e adds bias[e]
+    const int re = (int)(threadIdx.x % EMAX);
+    if (!routed) prefetch_router(ngw, ngb, nE, d);
+    if (wave < RK_SLICES) {  // uniform per wave
+      rs.load_x_lds(sx, d, nvalid, lane);
+      rs.compute(E, d, lane, part);
+    }
+    if (LATE_STORE && mine) cn.store(out, weight, norm_out, t0 + wave, d, lane);
+    lds_barrier();
+    // route_reduce with the bias from a register (the same sums, in slice order)
+    if (threadIdx.x < (unsigned)(TOK * EMAX)) {
+      const int tok = (int)threadIdx.x / EMAX;
+      if (re < E && t0 + tok < T) {
+        float v = part[tok * 16 + re];
+#pragma unroll
+        for (int sl = 1; sl < RK_SLICES; ++sl) v += part[(sl * RT + tok) * 16 + re];
+        slog[tok][re] = ngb ? v + bias : v;
+      }
+    }
+    lds_barrier();
+    constexpr int TPW = 64 / EMAX;
+    for (int tl = wave * TPW + (lane / EMAX); tl < TOK; tl += NWAVES * TPW) {
+      const int64_t t = t0 + tl;
+      route_select_group<EMAX>(slog[tl], spair[tl], E, nk, t, t < T, no, true, s_ti[tl], s_tw[tl], nullptr);
+    }
+  }
+};
+
 template <int NCH, int EMAX, bool EXACT, int KSW>
 __global__ void __launch_bounds__(CNR_TOK * 64)
 combine_norm_route_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
@@ -2995,64 +3236,10 @@ combine_norm_route_kernel(const void* __restrict__ yperm, const int64_t* __restr
                           const float* __restrict__ weight, float eps, void* norm_out, int64_t T, int d, int k,
                           const float* __restrict__ ngw, const float* __restrict__ ngb, RouteOut no, int nE,
                           int nk) {
-  static_assert(EMAX <= 16, "the MFMA router covers up to 16 experts");
-  constexpr int NWAVES = CNR_TOK;
-  __shared__ __attribute__((aligned(16))) float part[RK_SLICES * CNR_TOK * 16];
-  __shared__ float slog[CNR_TOK][EMAX];
-  __shared__ smaul_topk::Pair spair[CNR_TOK][EMAX];
-  __shared__ int s_ti[CNR_TOK][8];
-  __shared__ float s_tw[CNR_TOK][8];
-  __shared__ __attribute__((aligned(16))) uint16_t sx[CNR_TOK * CNR_DMAX];
-  static_assert(NWAVES >= RK_SLICES, "one K slice per router wave");
-  static_assert(CNR_TOK * EMAX <= RK_SLICES * 64, "the bias-adding threads are router-wave threads");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int E = EXACT ? EMAX : nE;
   const int64_t t0 = (int64_t)blockIdx.x * CNR_TOK;
-  const int nvalid = (int)min<int64_t>(CNR_TOK, T - t0);
-  // The combine and norm first, the normed row to LDS only.  The router
-  // weights and bias are loaded after the barrier: a CU returns reads in
-  // issue order, so cold weights issued before the combine's slot reads
-  // would hold those up.  The global stores of out / norm_out go out after
-  // the routing MFMAs, so that the wait for the weights does not also wait
-  // for them.
-  // (At KSW = 8 the row held through the routing would spill: stored first.)
-  constexpr bool LATE_STORE = KSW == 4;
-  CombineNormRow<true, NCH> cn;
-  const bool mine = wave < nvalid;  // uniform per wave
-  if (mine) {
-    cn.compute(yperm, topi, topw, inv, eps, t0 + wave, d, k, lane);
-    cn.to_lds(weight, d, lane, (char*)(sx + wave * d));
-    if (!LATE_STORE) cn.store(out, weight, norm_out, t0 + wave, d, lane);
-  }
-  lds_barrier();
-  // route_reduce's thread q = tok * EMAX + e adds bias[e]
-  const int re = (int)(threadIdx.x % EMAX);
-  float bias = 0.0f;
-  if (wave < RK_SLICES) {  // uniform per wave
-    RouteSlice<KSW, 1> rs;
-    rs.load_w(ngw, E, d, wave, lane);
-    if (threadIdx.x < (unsigned)(CNR_TOK * EMAX) && re < E && ngb) bias = ngb[re];
-    rs.load_x_lds(sx, d, nvalid, lane);
-    rs.compute(E, d, lane, part);
-  }
-  if (LATE_STORE && mine) cn.store(out, weight, norm_out, t0 + wave, d, lane);
-  lds_barrier();
-  // route_reduce with the bias from a register (the same sums, in slice order)
-  if (threadIdx.x < (unsigned)(CNR_TOK * EMAX)) {
-    const int tok = (int)threadIdx.x / EMAX;
-    if (re < E && t0 + tok < T) {
-      float v = part[tok * 16 + re];
-#pragma unroll
-      for (int sl = 1; sl < RK_SLICES; ++sl) v += part[(sl * CNR_TOK + tok) * 16 + re];
-      slog[tok][re] = ngb ? v + bias : v;
-    }
-  }
-  lds_barrier();
-  constexpr int TPW = 64 / EMAX;
-  for (int tl = wave * TPW + (lane / EMAX); tl < CNR_TOK; tl += NWAVES * TPW) {
-    const int64_t t = t0 + tl;
-    route_select_group<EMAX>(slog[tl], spair[tl], E, nk, t, t < T, no, true, s_ti[tl], s_tw[tl], nullptr);
-  }
+  CnrBlock<NCH, EMAX, EXACT, KSW, CNR_TOK, false> b;
+  b.prefetch_slots(topi, topw, inv, T, k, t0);
+  b.finish(yperm, 0, out, weight, eps, norm_out, T, d, ngw, ngb, no, nE, nk, t0);
 }
 
 // ---------------------------------------------------------------------------
@@ -3672,6 +3859,7 @@ int64_t smaul_moe_workspace_size(int64_t T, int64_t d, int64_t h, int64_t E, int
   n += align256(route_blocks(T, E, d, act_dtype) * E * 4) * 2;
   n += align256(R * h * el);
   n += align256(R * d * el);
+  n += 256;  // sync words of the decode path's fused combine
   return n;
 }
 
@@ -3799,6 +3987,8 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
   void* hdn = ws;
   ws += align256(R * h * el);
   void* yperm = ws;
+  ws += align256(R * d * el);
+  int32_t* sync = (int32_t*)ws;
 
   const int64_t bm = pick_block_m(T, d, h, E, k, tile, act_dtype);
   // decode regime: the gate/up kernel dispatches for itself
@@ -3847,10 +4037,40 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
     a.seg_off = seg_off;
     a.tile_off = tile_off;
     a.E = (int)E;
-    const DsDispatch dd{topi, topw, od, (int)T, (int)k};
-    rc = (flags & SMAUL_FLAG_CANONICAL_CODES) ? launch_decode_stream<true, true>(a, &dd, stream)
-                                              : launch_decode_stream<true, false>(a, &dd, stream);
+    // the combine + norm + next router in the down kernel's tail, when the
+    // shapes allow it (the same conditions as combine_norm_route_kernel, and
+    // launch_down_cnr's)
+    const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
+    const bool cnr = nrm && nr && act_dtype == SMAUL_DTYPE_BF16 && d % 16 == 0 && aligned16(yperm) &&
+                     aligned16(out) && aligned16(nrm->out) && route_mfma_ok(nr->E, d, act_dtype) &&
+                     aligned16(nr->gate_w) && route_ksw(d) == 4 && T <= 64;
+    DsDispatch dd{topi, topw, od, (int)T, (int)k, cnr ? sync : nullptr};
+    rc = canon ? launch_decode_stream<true, true>(a, &dd, stream) : launch_decode_stream<true, false>(a, &dd, stream);
     if (rc) return rc;
+    if (cnr) {
+      GemmArgs b{};
+      b.x = hdn;
+      b.ldx = h;
+      b.wp = down_w8;
+      b.sp = down_s;
+      b.y = yperm;
+      b.ldy = d;
+      b.K = h;
+      b.N = d;
+      b.nt = h / 64;
+      b.tile = 64;
+      b.seg_off = seg_off;
+      b.tile_off = tile_off;
+      b.E = (int)E;
+      RouteOut no{};
+      no.prob = nr->prob;
+      no.topi = nr->topi;
+      no.topw = nr->topw;
+      const CnrArgs cr{topi, topw, inv, out, nrm->weight, nrm->eps, nrm->out, T, (int)d, (int)k, nr->gate_w,
+                       nr->gate_b, no, (int)nr->E, (int)nr->k, sync, R * d * el};
+      rc = launch_down_cnr(b, canon, cr, stream);
+      if (rc != 1) return rc;  // else: no fused instance for this shape
+    }
     rc = smaul_moe_down(hdn, act_dtype, down_w8, down_s, yperm, seg_off, tile_off, max_tiles, E, d, h, tile,
                         bm, flags, stream);
     if (rc) return rc;

@@ -638,6 +638,8 @@ def test_moe_forward_norm(T, d, h, E, k, dtype, weighted):
     (33, 192, 320, 4, 3, 4, 3, torch.float32),      # fp32: the next router runs as its own kernel
     (5, 4160, 128, 4, 2, 4, 2, torch.bfloat16),     # d > 4096: combine, norm, router kernels
     (7, 512, 384, 4, 2, 8, 3, torch.bfloat16),      # one partial 16-token block, fused router
+    (20, 1024, 1024, 8, 2, 16, 4, torch.bfloat16),  # combine in the down kernel's tail: 3 workgroups, 16 experts
+    (64, 512, 2560, 16, 2, 6, 2, torch.bfloat16),   # the same with 6 of 8 router lanes (not exact)
 ])
 def test_moe_forward_chain(T, d, h, E, k, nE, nk, dtype):
     """Two chained layers: layer A routes its normalised output with layer B's
