@@ -79,8 +79,25 @@ def decode_tile(w, s, o0, o1, t, tile=TILE, dtype=torch.float32):
     return lut[w[o0:o1, t * tile:(t + 1) * tile].long()] * s[o0:o1, t].to(dtype).unsqueeze(1)
 
 
+def decode_block(w, s, o0, o1, in_f, tile=TILE, dtype=torch.float32):
+    """Rows [o0, o1) of every K tile decoded: ``[o1-o0, in_f]`` in ``dtype``.
+
+    Each value is the one product lut[code] * scale that decode_tile forms
+    (kernel/fp8_tile.py:134-160), the ragged last tile included: the codes are
+    padded to whole tiles so the scales broadcast over a [rows, nt, tile] view.
+    """
+    rows, nt = o1 - o0, -(-in_f // tile)
+    lut = codebook.values(w.device, dtype)
+    codes = w[o0:o1, :in_f].long()
+    if nt * tile != in_f:
+        codes = torch.nn.functional.pad(codes, (0, nt * tile - in_f))
+    vals = lut[codes].view(rows, nt, tile) * s[o0:o1, :nt].to(dtype).unsqueeze(-1)
+    return vals.view(rows, nt * tile)[:, :in_f]
+
+
 GRAD_DTYPE = torch.bfloat16   # storage of the accumulated weight gradient (kernel/fp8_tile.py:26)
 _GRAD_ROWS = 64               # weight-gradient rows added (and rounded) per step
+_REQUANT_ELEMS = 1 << 24      # fp32 values decoded at once by requant (64 MB)
 
 
 class _FP8Matmul(torch.autograd.Function):
@@ -154,6 +171,62 @@ class FP8Linear(nn.Module):
 
     def extra_repr(self):
         return f"in_f={self.in_f}, out_f={self.out_f}, tile={self.tile}, bias={self.bias is not None}"
+
+    # -- weight updates: decode, apply, quantize again (kernel/fp8_tile.py:240-285) --
+    # Quantization is per (row, tile), so rows may be processed in any grouping
+    # with the same codes; the groups here only bound the fp32 temporary.
+    def _row_groups(self):
+        step = max(1, _REQUANT_ELEMS // max(1, self.in_f))
+        for o0 in range(0, self.out_f, step):
+            yield o0, min(o0 + step, self.out_f)
+
+    @torch.no_grad()
+    def _requant_rows(self, o0, o1, update, decay):
+        w = decode_block(self.w8, self.sc, o0, o1, self.in_f, self.tile)
+        if decay:
+            w.mul_(1 - decay)
+        if update is not None:
+            w.sub_(update.to(w.dtype))
+        codes, scales = quantize_tiles(w, self.tile)
+        self.w8[o0:o1].copy_(codes)
+        self.sc[o0:o1].copy_(scales)
+
+    @torch.no_grad()
+    def requant(self, update=None, decay=0.0):
+        """W <- quantize(decode(W) * (1 - decay) - update) in place; clears ``_gw``.
+
+        ``update`` is ``[out_f, in_f]`` (any float dtype) or None.  HIP buffers
+        are decoded and quantized on the device.
+        """
+        if update is not None and (update.dim() != 2 or tuple(update.shape) != (self.out_f, self.in_f)):
+            raise ValueError(f"requant update must be [{self.out_f}, {self.in_f}], got {tuple(update.shape)} "
+                             "(a transposed [in_f, out_f] update is the usual mistake)")
+        for o0, o1 in self._row_groups():
+            self._requant_rows(o0, o1, None if update is None else update[o0:o1], decay)
+        self._gw = None
+
+    @torch.no_grad()
+    def fused_lion_requant(self, gw, st, lr, wd, b1, b2):
+        """One Lion step folded into requant: the update sign(b1*m + (1-b1)*g) * lr
+        with decay lr * wd, the fp32 momentum ``st`` advanced in place to
+        b2*m + (1-b2)*g; the same elementwise formulas as the reference
+        (kernel/fp8_tile.py:266-282), so codes and momentum match it bit for bit.
+        Clears ``_gw``."""
+        for o0, o1 in self._row_groups():
+            g = gw[o0:o1].float()
+            m = st[o0:o1]
+            step = (m * b1 + g * (1.0 - b1)).sign() * lr
+            m.mul_(b2).add_(g, alpha=1.0 - b2)
+            self._requant_rows(o0, o1, step, lr * wd)
+        self._gw = None
+
+    def err_stats(self):
+        """{"amax_fp8": largest |decoded weight|, "mean_scale": mean of the scales}."""
+        with torch.no_grad():
+            amax = 0.0
+            for o0, o1 in self._row_groups():
+                amax = max(amax, float(decode_block(self.w8, self.sc, o0, o1, self.in_f, self.tile).abs().amax()))
+            return {"amax_fp8": amax, "mean_scale": float(self.sc.double().mean())}
 
 
 def fp8_modules(model):

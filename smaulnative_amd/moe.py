@@ -7,7 +7,10 @@ diagnostic attributes read by training logs and retention reports:
 
 The whole layer (router, dispatch, the expert SwiGLU GEMMs, combine) is one
 call to the backend's ``moe_forward``; the per-expert Python loop with a host
-sync per expert (model.py:574-582) is gone.  ``expert_token_counts`` and
+sync per expert (model.py:574-582) is gone.  In training (grad enabled and
+the module in train mode) the layer runs as device torch ops around the
+experts' FP8Linear kernels instead, so autograd reaches the router and the
+experts' weight gradients (``_forward_train``).  ``expert_token_counts`` and
 ``last_executed`` are materialised from the device counts only when read, so
 a decode step does not force a device->host sync per layer.
 
@@ -130,7 +133,7 @@ class SwiFFN_MoE(nn.Module):
             raise RuntimeError(f"compute backend {be.name!r} has no moe_forward entry")
         if torch.is_grad_enabled() and (x.requires_grad or self.gate.weight.requires_grad) \
                 and self.training:
-            raise NotImplementedError("rocm MoE path is forward-only (training is not implemented)")
+            return self._forward_train(x)
         experts = [ex.buffers6() for ex in self.experts]
         out, prob, topi, counts = be.moe_forward(x, self.gate.weight, self.gate.bias, experts,
                                                  self.top_k, self.tile)
@@ -138,6 +141,38 @@ class SwiFFN_MoE(nn.Module):
         self.last_topi = topi
         self._counts_dev = counts
         return out
+
+    def _forward_train(self, x):
+        """The layer with autograd, for training.
+
+        The router softmax, top-k and renormalisation of model.py:557-570 as
+        torch ops on the device (gradient reaches the router through the
+        selected probabilities only, as in the reference); each expert's rows
+        gathered and run through its SwiFFN, whose FP8Linear modules compute
+        the forward and the input gradient with the backend's kernels and
+        accumulate their weight gradients in ``_gw``; the weighted outputs added
+        back token by token in ascending expert order (model.py:571-585).  The
+        fused moe_forward path has no backward, so training runs this one.
+        """
+        d = x.shape[-1]
+        xs = x.reshape(-1, d)
+        prob = torch.softmax(self.gate(xs.float()), -1)
+        self.last_prob = prob
+        topv, topi = torch.topk(prob, self.top_k, -1)
+        self.last_topi = topi.detach()
+        total = topv.sum(-1, keepdim=True)
+        topv = torch.where(total < 1e-6, torch.full_like(topv, 1.0 / self.top_k), topv / total.clamp_min(1e-9))
+        out = torch.zeros(xs.shape, dtype=torch.float32, device=xs.device)
+        counts = []
+        for e, expert in enumerate(self.experts):
+            weight = torch.where(topi == e, topv, torch.zeros_like(topv)).sum(-1)
+            rows = torch.nonzero(weight > 0).squeeze(-1)
+            counts.append(int(rows.numel()))
+            if counts[-1]:
+                y = expert(xs.index_select(0, rows)).float() * weight.index_select(0, rows).unsqueeze(-1)
+                out = out.index_add(0, rows, y)
+        self.expert_token_counts = counts
+        return out.view(x.shape).to(x.dtype if x.is_floating_point() else torch.float32)
 
     def routing_stats(self) -> dict:
         counts = list(self.expert_token_counts)

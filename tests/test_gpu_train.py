@@ -1,0 +1,90 @@
+"""GPU: the training side of the layer (not on the forward path).
+
+- requant / fused_lion_requant on device buffers replay the reference's own
+  outputs bit for bit (tests/golden/golden_requant.npz, kernel/fp8_tile.py:240-285;
+  the CPU replay is tests/test_requant.py).
+- A SwiFFN_MoE training step (model.py:557-585 under autograd): the input
+  gradient, the router-weight gradient (through the selected probabilities,
+  model.py:559-563) and every executed expert's bf16 weight gradients
+  (kernel/fp8_tile.py:172-197) against a float64 autograd restatement of the
+  same layer on the decoded weights with the same routing.  Bar: relative
+  1e-1 of the largest magnitude -- the layer computes in bf16 activations
+  (x, the SwiGLU product, expert outputs), so the gradients carry bf16
+  rounding; unselected experts get no gradient.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from smaulnative_amd import MoEConfig, SwiFFN_MoE
+from smaulnative_amd.fp8_tile import decode_block
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def test_requant_and_lion_match_reference_on_device():
+    from test_requant import replay
+    print("case requant/lion replay on the device", flush=True)
+    replay(DEV)
+
+
+def _dense(lin):
+    return decode_block(lin.w8, lin.sc, 0, lin.out_f, lin.in_f, lin.tile).double().cpu()
+
+
+def rel(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-300))
+
+
+@pytest.mark.parametrize("E,k", [(4, 2), (8, 1)])
+def test_moe_training_step_gradients(E, k):
+    print(f"case moe training step E={E} k={k}", flush=True)
+    torch.manual_seed(11 + E)
+    cfg = MoEConfig(d_model=128, ffn_mult=2.5, tile=64, num_experts=E, num_experts_per_tok=k)
+    moe = SwiFFN_MoE(cfg).to(DEV).train()
+    x = torch.randn(2, 40, 128, device=DEV).to(torch.bfloat16).requires_grad_(True)
+    c = torch.randn(2, 40, 128, device=DEV)
+    out = moe(x)
+    assert out.dtype == torch.bfloat16 and out.shape == x.shape
+    (out.float() * c).sum().backward()
+    topi = moe.last_topi.cpu()
+
+    # float64 restatement with the module's routing
+    xs = x.detach().double().cpu().reshape(-1, 128).requires_grad_(True)
+    gw = moe.gate.weight.detach().double().cpu().requires_grad_(True)
+    ws = [{n: _dense(getattr(ex, n)).requires_grad_(True) for n in ("gate", "up", "down")} for ex in moe.experts]
+    prob = torch.softmax(xs @ gw.t(), -1)
+    topv = prob.gather(-1, topi)
+    topv = topv / topv.sum(-1, keepdim=True)
+    ref = torch.zeros_like(xs)
+    for e in range(E):
+        wsel = torch.where(topi == e, topv, torch.zeros_like(topv)).sum(-1)
+        rows = torch.nonzero(wsel > 0).squeeze(-1)
+        if rows.numel():
+            xm = xs.index_select(0, rows)
+            h = F.silu(xm @ ws[e]["gate"].t()) * (xm @ ws[e]["up"].t())
+            ref = ref.index_add(0, rows, (h @ ws[e]["down"].t()) * wsel.index_select(0, rows).unsqueeze(-1))
+    (ref * c.double().cpu().reshape(-1, 128)).sum().backward()
+
+    assert rel(out.float().reshape(-1, 128), ref.detach()) < 3e-2
+    assert rel(x.grad.float().reshape(-1, 128), xs.grad) < 1e-1
+    assert torch.isfinite(moe.gate.weight.grad).all()
+    if k == 1:
+        # one expert per token: the renormalised weight is p / p = 1, so the
+        # router's gradient is zero up to rounding (model.py:565-567)
+        assert float(gw.grad.abs().max()) < 1e-9
+        assert float(moe.gate.weight.grad.abs().max()) < 1e-4
+    else:
+        assert rel(moe.gate.weight.grad, gw.grad) < 1e-1
+    counts = moe.expert_token_counts
+    assert sum(counts) == 80 * k
+    for e, ex in enumerate(moe.experts):
+        for n in ("gate", "up", "down"):
+            lin = getattr(ex, n)
+            if counts[e] == 0:
+                assert lin._gw is None
+            else:
+                assert lin._gw is not None and lin._gw.dtype == torch.bfloat16
+                assert rel(lin._gw.float(), ws[e][n].grad) < 1e-1, (e, n)
