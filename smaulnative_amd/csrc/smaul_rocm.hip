@@ -2210,7 +2210,7 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd, CnrArgs cr) {
     if (a >= ncw) return;  // uniform: the first ncw to arrive combine (they wait longest)
     const int64_t t0 = (int64_t)a * CNR_TAIL_TOK;
     CnrBlock<1, CEMAX, CEXACT, 4, CNR_TAIL_TOK, true> b;
-    b.prefetch_slots(cr.topi, cr.topw, cr.inv, cr.T, cr.k, t0);
+    b.prefetch_slots(cr.topi, cr.topw, cr.inv, cr.weight, cr.T, cr.d, cr.k, t0);
     b.prefetch_router(cr.ngw, cr.ngb, cr.nE, cr.d);
     if (threadIdx.x == 0) {
       int spins = 0;
@@ -2878,15 +2878,12 @@ __device__ __forceinline__ void rms_unpack(const uint4* v, float (&f)[16]) {
 // (f * r) * weight for 16 columns from c0, cast and stored at dst and/or
 // lds_dst (either may be null)
 template <bool BF16>
-__device__ __forceinline__ void rms_scale_store(const float (&f)[16], float r, const float* weight, int c0,
-                                                char* dst, char* lds_dst = nullptr) {
+__device__ __forceinline__ void rms_scale_store_w(const float (&f)[16], float r, const float (&wv)[16], bool hasw,
+                                                  char* dst, char* lds_dst = nullptr) {
   float o[16];
 #pragma unroll
   for (int q = 0; q < 16; ++q) o[q] = f[q] * r;
-  if (weight) {  // all 16 loads in flight before the first product
-    float wv[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) wv[q] = ldgf(weight + c0 + q);
+  if (hasw) {
 #pragma unroll
     for (int q = 0; q < 16; ++q) o[q] = o[q] * wv[q];
   }
@@ -2909,6 +2906,18 @@ __device__ __forceinline__ void rms_scale_store(const float (&f)[16], float r, c
       if (lds_dst) ((float4*)lds_dst)[j] = w;
     }
   }
+}
+
+// the same with the norm weight read here (all 16 loads in flight before the first product)
+template <bool BF16>
+__device__ __forceinline__ void rms_scale_store(const float (&f)[16], float r, const float* weight, int c0,
+                                                char* dst, char* lds_dst = nullptr) {
+  float wv[16];
+  if (weight) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) wv[q] = ldgf(weight + c0 + q);
+  }
+  rms_scale_store_w<BF16>(f, r, wv, weight != nullptr, dst, lds_dst);
 }
 
 template <bool BF16, bool VEC>
@@ -3000,6 +3009,23 @@ struct CombineNormRow {
   int rw[8];         // the token's yperm rows (combine_slots order) and weights
   float wt[8];
   int n;
+  float wv[NCH][16];  // the norm weight of the lane's columns (load_weight)
+  bool hasw;
+
+  // the norm weight of the lane's columns into registers (read once, before
+  // to_lds / store; weight may be null)
+  __device__ __forceinline__ void load_weight(const float* weight, int d, int lane) {
+    hasw = weight != nullptr;
+    if (!hasw) return;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = lane + i * 64;
+      if (c < d / 16) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) wv[i][q] = ldgf(weight + c * 16 + q);
+      }
+    }
+  }
 
   // the combine of the chunks and the row's 1/rms; no store.  COH: yperm
   // (ybytes long) was written by other workgroups of the running launch and
@@ -3065,23 +3091,23 @@ struct CombineNormRow {
     r = 1.0f / __fsqrt_rn(ss / (float)d + eps);
   }
 
-  // the normalised row to LDS only (lds_row: d values of the dtype)
-  __device__ __forceinline__ void to_lds(const float* weight, int d, int lane, char* lds_row) const {
+  // the normalised row to LDS only (lds_row: d values of the dtype); after
+  // load_weight
+  __device__ __forceinline__ void to_lds(int d, int lane, char* lds_row) const {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int c = lane + i * 64;
-      if (c < d / 16) rms_scale_store<BF16>(v[i], r, weight, c * 16, nullptr, lds_row + c * 16 * ES);
+      if (c < d / 16) rms_scale_store_w<BF16>(v[i], r, wv[i], hasw, nullptr, lds_row + c * 16 * ES);
     }
   }
 
-  // out and norm_out of token t
-  __device__ __forceinline__ void store(void* out, const float* weight, void* norm_out, int64_t t, int d,
-                                        int lane) const {
+  // out and norm_out of token t; after load_weight
+  __device__ __forceinline__ void store(void* out, void* norm_out, int64_t t, int d, int lane) const {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int c = lane + i * 64;
       if (c < d / 16) {
-        rms_scale_store<BF16>(v[i], r, weight, c * 16, (char*)norm_out + (t * d + c * 16) * ES);
+        rms_scale_store_w<BF16>(v[i], r, wv[i], hasw, (char*)norm_out + (t * d + c * 16) * ES);
         char* dst = (char*)out + (t * d + c * 16) * ES;
         if constexpr (BF16) {
 #pragma unroll
@@ -3113,7 +3139,8 @@ combine_norm_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ 
   if (t >= T) return;
   CombineNormRow<BF16, NCH> cn;
   cn.compute(yperm, topi, topw, inv, eps, t, d, k, threadIdx.x & 63);
-  cn.store(out, weight, norm_out, t, d, threadIdx.x & 63);
+  cn.load_weight(weight, d, threadIdx.x & 63);
+  cn.store(out, norm_out, t, d, threadIdx.x & 63);
 }
 
 // The combine and output norm of 16 tokens (one wave each, combine_norm_row)
@@ -3134,7 +3161,7 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // The combine + norm + next router of the TOK tokens from t0, by the calling
 // workgroup's TOK waves (wave w: token t0 + w; waves < RK_SLICES also run the
 // router's K slices), in three phases: prefetch_slots (the top-k, weights and
-// yperm rows of each token), prefetch_router (the router weights and bias of
+// yperm rows of each token, and the norm weight), prefetch_router (the router weights and bias of
 // the K-slice waves) and finish (the rest).  The loads of the first two do not
 // depend on yperm, so a caller that waits for yperm can issue them before it
 // waits.  COH: yperm (ybytes long) was written by other workgroups of the
@@ -3160,9 +3187,14 @@ struct CnrBlock {
   __device__ __forceinline__ static int nvalid_of(int64_t T, int64_t t0) { return (int)min<int64_t>(TOK, T - t0); }
 
   __device__ __forceinline__ void prefetch_slots(const int64_t* topi, const float* topw, const int32_t* inv,
-                                                 int64_t T, int k, int64_t t0) {
+                                                 const float* weight, int64_t T, int d, int k, int64_t t0) {
     const int wave = threadIdx.x >> 6;
-    if (wave < nvalid_of(T, t0)) cn.slots(topi, topw, inv, t0 + wave, k);  // uniform per wave
+    if (wave < nvalid_of(T, t0)) {  // uniform per wave
+      cn.slots(topi, topw, inv, t0 + wave, k);
+      // the norm weight too where the row is held through the routing (with
+      // it live from here, the wider rows of KSW = 8 would spill)
+      if (LATE_STORE) cn.load_weight(weight, d, threadIdx.x & 63);
+    }
   }
   __device__ __forceinline__ void prefetch_router(const float* ngw, const float* ngb, int nE, int d) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -3197,8 +3229,9 @@ struct CnrBlock {
     const bool mine = wave < nvalid;  // uniform per wave
     if (mine) {
       cn.template combine<COH>(yperm, eps, d, lane, ybytes);
-      cn.to_lds(weight, d, lane, (char*)(sx + wave * d));
-      if (!LATE_STORE) cn.store(out, weight, norm_out, t0 + wave, d, lane);
+      if (!LATE_STORE) cn.load_weight(weight, d, lane);
+      cn.to_lds(d, lane, (char*)(sx + wave * d));
+      if (!LATE_STORE) cn.store(out, norm_out, t0 + wave, d, lane);
     }
     lds_barrier();
     // route_reduce's thread q = tok * EMAX + e adds bias[e]
@@ -3208,7 +3241,7 @@ struct CnrBlock {
       rs.load_x_lds(sx, d, nvalid, lane);
       rs.compute(E, d, lane, part);
     }
-    if (LATE_STORE && mine) cn.store(out, weight, norm_out, t0 + wave, d, lane);
+    if (LATE_STORE && mine) cn.store(out, norm_out, t0 + wave, d, lane);
     lds_barrier();
     // route_reduce with the bias from a register (the same sums, in slice order)
     if (threadIdx.x < (unsigned)(TOK * EMAX)) {
@@ -3238,7 +3271,7 @@ combine_norm_route_kernel(const void* __restrict__ yperm, const int64_t* __restr
                           int nk) {
   const int64_t t0 = (int64_t)blockIdx.x * CNR_TOK;
   CnrBlock<NCH, EMAX, EXACT, KSW, CNR_TOK, false> b;
-  b.prefetch_slots(topi, topw, inv, T, k, t0);
+  b.prefetch_slots(topi, topw, inv, weight, T, d, k, t0);
   b.finish(yperm, 0, out, weight, eps, norm_out, T, d, ngw, ngb, no, nE, nk, t0);
 }
 
