@@ -1276,48 +1276,89 @@ __device__ __forceinline__ uint64_t selection_of(const int* ti, const float* tw,
   return sel;
 }
 
+// Token t's top-k ids (outside [0, E) as -1) and weights, as the dispatch
+// reads them (t invalid: -1 / 0); every load is issued before the first is
+// used, so the k reads take one round trip.
+__device__ __forceinline__ void load_topk(const int64_t* topi, const float* topw, int64_t t, int k, bool valid,
+                                          int E, int (&ti)[8], float (&tw)[8]) {
+  int64_t v[8];
+  float w[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    v[j] = -1;
+    w[j] = 0.0f;
+  }
+  if (valid) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < k) {
+        v[j] = topi[t * k + j];
+        w[j] = topw[t * k + j];
+      }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    ti[j] = (j < k && v[j] >= 0 && v[j] < E) ? (int)v[j] : -1;
+    tw[j] = j < k ? w[j] : 0.0f;
+  }
+}
+
 // Deterministic dispatch of up to 64 tokens by one wave: lane t holds token
-// t's top-k ids and weights; each expert's rows are the tokens that selected
-// it, ranked by ballot in ascending token order (model.py:574-581).
+// t's top-k ids and weights (load_topk); each expert's rows are the tokens
+// that selected it, ranked by ballot in ascending token order
+// (model.py:574-581).  A token's live slots are the first slot of each
+// expert with a positive weight (selection_of); the others get inv -1.  The
+// expert loop only ranks; every store follows it (E <= 64).
 __device__ __forceinline__ void dispatch_one_wave(const int* ti, const float* tw, bool valid, int lane,
                                                   const RouteOut& o, int E, int k) {
   const int64_t t = lane;
-  const uint64_t sel = valid ? selection_of(ti, tw, E, k) : 0ull;
+  bool live[8];
+  uint64_t sel = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int ee = ti[j];
+    live[j] = valid && j < k && tw[j] > 0.0f && ee >= 0 && ee < E && !((sel >> ee) & 1ull);
+    if (live[j]) sel |= 1ull << ee;
+  }
   const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  int off = 0, toff = 0;
+  int pos[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) pos[j] = -1;
+  int off = 0, toff = 0, my_n = 0, my_off = 0, my_toff = 0;
   for (int e = 0; e < E; ++e) {
     const uint64_t b = __ballot((sel >> e) & 1ull);
     const int n = __popcll(b);
-    if (lane == 0) {
-      o.counts[e] = n;
-      o.seg_off[e] = off;
-      o.tile_off[e] = toff;
+    if (lane == e) {
+      my_n = n;
+      my_off = off;
+      my_toff = toff;
     }
-    if ((sel >> e) & 1ull) {
-      const int pos = off + __popcll(b & lt);
-      o.perm_row[pos] = (int32_t)t;
-      for (int j = 0; j < k; ++j)
-        if (ti[j] == e && tw[j] > 0.0f) {
-          o.perm_w[pos] = tw[j];
-          o.inv[t * k + j] = pos;
-          break;
-        }
-    }
+    const int p = off + __popcll(b & lt);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (live[j] && ti[j] == e) pos[j] = p;
     off += n;
     toff += (n + o.block_m - 1) / o.block_m;
+  }
+  if (lane < E) {
+    o.counts[lane] = my_n;
+    o.seg_off[lane] = my_off;
+    o.tile_off[lane] = my_toff;
   }
   if (lane == 0) {
     o.seg_off[E] = off;
     o.tile_off[E] = toff;
   }
   if (valid) {
-    uint64_t seen = 0;
-    for (int j = 0; j < k; ++j) {
-      const int ee = ti[j];
-      const bool ok = tw[j] > 0.0f && ee >= 0 && ee < E && !((seen >> ee) & 1ull);
-      if (ok) seen |= 1ull << ee;
-      else o.inv[t * k + j] = -1;
-    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < k) {
+        if (live[j]) {
+          o.perm_row[pos[j]] = (int32_t)t;
+          o.perm_w[pos[j]] = tw[j];
+        }
+        o.inv[t * k + j] = live[j] ? pos[j] : -1;
+      }
   }
 }
 
@@ -1562,6 +1603,7 @@ struct RouteSlice {
   static constexpr int TOK = NTT * 16;  // tokens of the block
   uint4 xr[NTT][KSW];
   float4 wr[KSW][2];
+  bf16x8_t wa[KSW][3];  // the weights as three bf16 terms (split())
   int slice;
 
   // Every load is issued unconditionally from an in-bounds address (column
@@ -1615,6 +1657,41 @@ struct RouteSlice {
     }
   }
 
+  // block i of the weights as three bf16 terms: w = hi + mid + lo, each term
+  // the bf16 rounding of what the terms before it leave
+  __device__ __forceinline__ void terms(int i, bf16x8_t (&a)[3]) const {
+    const float w8[8] = {wr[i][0].x, wr[i][0].y, wr[i][0].z, wr[i][0].w,
+                         wr[i][1].x, wr[i][1].y, wr[i][1].z, wr[i][1].w};
+    uint32_t q0[8], q1[8], q2[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      q0[j] = bf16_rne(w8[j]);
+      const float r1 = w8[j] - bf2f(q0[j]);
+      q1[j] = bf16_rne(r1);
+      q2[j] = bf16_rne(r1 - bf2f(q1[j]));
+    }
+    a[0] = __builtin_bit_cast(bf16x8_t, make_uint4(q0[0] | (q0[1] << 16), q0[2] | (q0[3] << 16),
+                                                   q0[4] | (q0[5] << 16), q0[6] | (q0[7] << 16)));
+    a[1] = __builtin_bit_cast(bf16x8_t, make_uint4(q1[0] | (q1[1] << 16), q1[2] | (q1[3] << 16),
+                                                   q1[4] | (q1[5] << 16), q1[6] | (q1[7] << 16)));
+    a[2] = __builtin_bit_cast(bf16x8_t, make_uint4(q2[0] | (q2[1] << 16), q2[2] | (q2[3] << 16),
+                                                   q2[4] | (q2[5] << 16), q2[6] | (q2[7] << 16)));
+  }
+  // the weights out of range (column >= d, expert >= E) to zero
+  __device__ __forceinline__ void mask_w(int E, int d, int lane) {
+    const int n = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < KSW; ++i) {
+      const int c = (slice * KSW + i) * 32 + 8 * g;
+      if (c >= d || n >= E) wr[i][0] = wr[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+
+  // Waits for the loads, runs the MFMAs and writes the partials; PRE: the
+  // weights' terms were made by split() (which holds them all at once: for a
+  // caller with time and registers to spare before the activations arrive),
+  // else each block's terms are made as it is used.
+  template <bool PRE = false>
   __device__ __forceinline__ void compute(int E, int d, int lane, float* part) {
     const int n = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -1624,8 +1701,8 @@ struct RouteSlice {
 #pragma unroll
         for (int tt = 0; tt < NTT; ++tt) xr[tt][i] = make_uint4(0u, 0u, 0u, 0u);
       }
-      if (c >= d || n >= E) wr[i][0] = wr[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    if constexpr (!PRE) mask_w(E, d, lane);
     f32x4_t acc[NTT][3];
 #pragma unroll
     for (int tt = 0; tt < NTT; ++tt)
@@ -1633,23 +1710,14 @@ struct RouteSlice {
       for (int term = 0; term < 3; ++term) acc[tt][term] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < KSW; ++i) {
-      const float w8[8] = {wr[i][0].x, wr[i][0].y, wr[i][0].z, wr[i][0].w,
-                           wr[i][1].x, wr[i][1].y, wr[i][1].z, wr[i][1].w};
-      uint32_t q0[8], q1[8], q2[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        q0[j] = bf16_rne(w8[j]);
-        const float r1 = w8[j] - bf2f(q0[j]);
-        q1[j] = bf16_rne(r1);
-        q2[j] = bf16_rne(r1 - bf2f(q1[j]));
-      }
       bf16x8_t a[3];
-      a[0] = __builtin_bit_cast(bf16x8_t, make_uint4(q0[0] | (q0[1] << 16), q0[2] | (q0[3] << 16),
-                                                     q0[4] | (q0[5] << 16), q0[6] | (q0[7] << 16)));
-      a[1] = __builtin_bit_cast(bf16x8_t, make_uint4(q1[0] | (q1[1] << 16), q1[2] | (q1[3] << 16),
-                                                     q1[4] | (q1[5] << 16), q1[6] | (q1[7] << 16)));
-      a[2] = __builtin_bit_cast(bf16x8_t, make_uint4(q2[0] | (q2[1] << 16), q2[2] | (q2[3] << 16),
-                                                     q2[4] | (q2[5] << 16), q2[6] | (q2[7] << 16)));
+      if constexpr (PRE) {
+        a[0] = wa[i][0];
+        a[1] = wa[i][1];
+        a[2] = wa[i][2];
+      } else {
+        terms(i, a);
+      }
 #pragma unroll
       for (int tt = 0; tt < NTT; ++tt)
 #pragma unroll
@@ -1663,6 +1731,12 @@ struct RouteSlice {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         part[(slice * TOK + tt * 16 + n) * 16 + 4 * g + r] = (acc[tt][0][r] + acc[tt][1][r]) + acc[tt][2][r];
+  }
+  // every block's terms ahead of compute<true>() (waits for the weight loads)
+  __device__ __forceinline__ void split(int E, int d, int lane) {
+    mask_w(E, d, lane);
+#pragma unroll
+    for (int i = 0; i < KSW; ++i) terms(i, wa[i]);
   }
 };
 
@@ -2125,6 +2199,75 @@ template <int NCH, int EMAX, bool EXACT, int KSW, int TOK, bool COH>
 struct CnrBlock;
 constexpr int CNR_SPIN_LIMIT = 1 << 20;  // polls of the arrival count before giving up
 
+// The dispatch of the fused gate/up kernel (FUSED below): wave 0 ranks the
+// T <= 64 tokens per expert into s_perm / s_off (LDS), workgroup 0 also
+// writes the dispatch for the later stages and clears dd.sync; returns the
+// segments, with p's pointers.  All threads call it (it ends with a barrier).
+__device__ __forceinline__ void ds_fused_dispatch(const GemmArgs& p, const DsDispatch& dd, int lane, DsSegs& sg,
+                                                  int32_t* s_perm, int32_t* s_off) {
+  ds_pointers(p, lane, sg);
+  if (threadIdx.x < 64) {
+    const bool valid = lane < dd.T;
+    int ti[8];
+    float tw[8];
+    load_topk(dd.topi, dd.topw, lane, dd.k, valid, p.E, ti, tw);
+    const uint64_t sel = valid ? selection_of(ti, tw, p.E, dd.k) : 0ull;
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    int off = 0;
+    for (int e = 0; e < p.E; ++e) {
+      const uint64_t b = __ballot((sel >> e) & 1ull);
+      if (lane == 0) s_off[e] = off;
+      if ((sel >> e) & 1ull) s_perm[off + __popcll(b & lt)] = lane;
+      off += __popcll(b);
+    }
+    if (lane == 0) s_off[p.E] = off;
+    if (blockIdx.x == 0) dispatch_one_wave(ti, tw, valid, lane, dd.o, p.E, dd.k);
+    if (blockIdx.x == 0 && lane < 2 && dd.sync) dd.sync[lane] = 0;
+  }
+  __syncthreads();
+  ds_finish(lane < p.E ? s_off[lane] : 0, lane < p.E ? s_off[lane + 1] : 0, lane, sg);
+}
+
+// Bounded wait of thread 0 until *ctr reaches target (device scope); past
+// CNR_SPIN_LIMIT polls it counts a timeout in *err and gives up.
+__device__ __forceinline__ void ds_spin(const int32_t* ctr, int target, int32_t* err) {
+  if (threadIdx.x == 0) {
+    int spins = 0;
+    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      if (++spins > CNR_SPIN_LIMIT) {
+        __hip_atomic_fetch_add(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+}
+
+// The combine tail (CNR below) after this workgroup's down units: wait for
+// its own device-scope output stores, count itself in *arr; the first
+// ceil(T / 8) to arrive prefetch what the combine needs besides y, wait for
+// all gridDim.x arrivals and run the combine + norm + next router of 8
+// tokens each.  Every workgroup returns from it.
+template <int CEMAX, bool CEXACT>
+__device__ __forceinline__ void cnr_tail(const CnrArgs& cr, const void* y, int32_t* arr, int32_t* err) {
+  __shared__ int s_arrival;
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's output stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) s_arrival = (int)__hip_atomic_fetch_add(arr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const int ncw = (int)((cr.T + CNR_TAIL_TOK - 1) / CNR_TAIL_TOK);
+  const int a = s_arrival;
+  if (a >= ncw) return;  // uniform: the first ncw to arrive combine (they wait longest)
+  const int64_t t0 = (int64_t)a * CNR_TAIL_TOK;
+  CnrBlock<1, CEMAX, CEXACT, 4, CNR_TAIL_TOK, true> b;
+  b.prefetch_slots(cr.topi, cr.topw, cr.inv, cr.weight, cr.T, cr.d, cr.k, t0);
+  b.prefetch_router(cr.ngw, cr.ngb, cr.nE, cr.d);
+  b.prepare_router(cr.nE, cr.d);
+  ds_spin(arr, (int)gridDim.x, err);
+  __syncthreads();
+  b.finish(y, cr.ybytes, cr.out, cr.weight, cr.eps, cr.norm_out, cr.T, cr.d, cr.ngw, cr.ngb, cr.no, cr.nE, cr.nk, t0);
+}
+
 // FUSED (gate/up only): every workgroup ranks the T <= 64 tokens per expert
 // itself into LDS (one wave, ballot ranks in token order, the same rule as
 // dispatch_one_wave) instead of reading a dispatch written by an earlier
@@ -2154,33 +2297,7 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd, CnrArgs cr) {
   const int ctn = (int)(p.N >> 4);
   DsSegs sg;
   if constexpr (FUSED) {
-    ds_pointers(p, lane, sg);
-    if (threadIdx.x < 64) {
-      const bool valid = lane < dd.T;
-      int ti[8];
-      float tw[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (j < dd.k) {
-          const int64_t v = valid ? dd.topi[lane * dd.k + j] : -1;
-          ti[j] = (v >= 0 && v < p.E) ? (int)v : -1;
-          tw[j] = valid ? dd.topw[lane * dd.k + j] : 0.0f;
-        }
-      const uint64_t sel = valid ? selection_of(ti, tw, p.E, dd.k) : 0ull;
-      const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-      int off = 0;
-      for (int e = 0; e < p.E; ++e) {
-        const uint64_t b = __ballot((sel >> e) & 1ull);
-        if (lane == 0) s_off[e] = off;
-        if ((sel >> e) & 1ull) s_perm[off + __popcll(b & lt)] = lane;
-        off += __popcll(b);
-      }
-      if (lane == 0) s_off[p.E] = off;
-      if (blockIdx.x == 0) dispatch_one_wave(ti, tw, valid, lane, dd.o, p.E, dd.k);
-      if (blockIdx.x == 0 && lane < 2 && dd.sync) dd.sync[lane] = 0;
-    }
-    __syncthreads();
-    ds_finish(lane < p.E ? s_off[lane] : 0, lane < p.E ? s_off[lane + 1] : 0, lane, sg);
+    ds_fused_dispatch(p, dd, lane, sg, s_perm, s_off);
   } else {
     sg = ds_segments(p, lane);
   }
@@ -2198,33 +2315,7 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd, CnrArgs cr) {
   }
   if constexpr (CNR) {
     static_assert(!SWIGLU, "the combine follows the down projection");
-    __shared__ int s_arrival;
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's output stores have completed
-    __syncthreads();
-    if (threadIdx.x == 0)
-      s_arrival = (int)__hip_atomic_fetch_add(cr.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    const int G = (int)gridDim.x;
-    const int ncw = (int)((cr.T + CNR_TAIL_TOK - 1) / CNR_TAIL_TOK);
-    const int a = s_arrival;
-    if (a >= ncw) return;  // uniform: the first ncw to arrive combine (they wait longest)
-    const int64_t t0 = (int64_t)a * CNR_TAIL_TOK;
-    CnrBlock<1, CEMAX, CEXACT, 4, CNR_TAIL_TOK, true> b;
-    b.prefetch_slots(cr.topi, cr.topw, cr.inv, cr.weight, cr.T, cr.d, cr.k, t0);
-    b.prefetch_router(cr.ngw, cr.ngb, cr.nE, cr.d);
-    if (threadIdx.x == 0) {
-      int spins = 0;
-      while (__hip_atomic_load(cr.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < G) {
-        if (++spins > CNR_SPIN_LIMIT) {
-          __hip_atomic_fetch_add(cr.sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-      }
-    }
-    __syncthreads();
-    b.finish(p.y, cr.ybytes, cr.out, cr.weight, cr.eps, cr.norm_out, cr.T, cr.d, cr.ngw, cr.ngb, cr.no, cr.nE, cr.nk,
-             t0);
+    cnr_tail<CEMAX, CEXACT>(cr, p.y, cr.sync, cr.sync + 1);
   }
 }
 
@@ -2623,13 +2714,7 @@ dispatch_scan_scatter_kernel(const int64_t* __restrict__ topi, const float* __re
   const bool valid = lane < tpb && t < T;
   int ti[8];
   float tw[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    if (j < k) {
-      const int64_t v = valid ? topi[t * k + j] : -1;
-      ti[j] = (v >= 0 && v < E) ? (int)v : -1;
-      tw[j] = valid ? topw[t * k + j] : 0.0f;
-    }
+  load_topk(topi, topw, t, k, valid, E, ti, tw);
   int before[EMAX], total[EMAX];
 #pragma unroll
   for (int e = 0; e < EMAX; ++e) before[e] = total[e] = 0;
@@ -2711,11 +2796,7 @@ dispatch_small_kernel(const int64_t* __restrict__ topi, const float* __restrict_
   const bool valid = lane < T;
   int ti[8];
   float tw[8];
-  for (int j = 0; j < k; ++j) {
-    const int64_t v = valid ? topi[lane * k + j] : -1;
-    ti[j] = (v >= 0 && v < E) ? (int)v : -1;
-    tw[j] = valid ? topw[lane * k + j] : 0.0f;
-  }
+  load_topk(topi, topw, lane, k, valid, E, ti, tw);
   dispatch_one_wave(ti, tw, valid, lane, o, E, k);
 }
 
@@ -3011,6 +3092,12 @@ struct CombineNormRow {
   int n;
   float wv[NCH][16];  // the norm weight of the lane's columns (load_weight)
   bool hasw;
+  // PACK (bf16, one chunk per lane): the lane's out and norm_out values, two
+  // per word (combine() and norm()), so that to_lds() and store() only move
+  // them.  Wider rows convert in to_lds() / store() (held packed beside the
+  // row and the weight, they would not fit the registers of 16 waves).
+  static constexpr bool PACK = BF16 && NCH == 1;
+  uint32_t po[PACK ? NCH : 1][8], pn[PACK ? NCH : 1][8];
 
   // the norm weight of the lane's columns into registers (read once, before
   // to_lds / store; weight may be null)
@@ -3079,7 +3166,15 @@ struct CombineNormRow {
               v[i][q] = v[i][q] + pr;
             }
           }
-        if constexpr (BF16) {
+        if constexpr (PACK) {
+#pragma unroll
+          for (int q = 0; q < 16; q += 2) {
+            const uint32_t b0 = f2bf(v[i][q]), b1 = f2bf(v[i][q + 1]);
+            po[i][q / 2] = b0 | (b1 << 16);
+            v[i][q] = bf2f(b0);
+            v[i][q + 1] = bf2f(b1);
+          }
+        } else if constexpr (BF16) {
 #pragma unroll
           for (int q = 0; q < 16; ++q) v[i][q] = bf2f(f2bf(v[i][q]));
         }
@@ -3091,25 +3186,60 @@ struct CombineNormRow {
     r = 1.0f / __fsqrt_rn(ss / (float)d + eps);
   }
 
+  // PACK: the normalised row, (v * r) * weight rounded to bf16, into pn;
+  // after combine() and load_weight() (else a no-op)
+  __device__ __forceinline__ void norm(int d, int lane) {
+    if constexpr (!PACK) return;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = lane + i * 64;
+      if (c < d / 16) {
+        float o[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) o[q] = v[i][q] * r;
+        if (hasw) {
+#pragma unroll
+          for (int q = 0; q < 16; ++q) o[q] = o[q] * wv[i][q];
+        }
+#pragma unroll
+        for (int q = 0; q < 16; q += 2) pn[i][q / 2] = f2bf(o[q]) | (f2bf(o[q + 1]) << 16);
+      }
+    }
+  }
+
   // the normalised row to LDS only (lds_row: d values of the dtype); after
-  // load_weight
+  // norm()
   __device__ __forceinline__ void to_lds(int d, int lane, char* lds_row) const {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int c = lane + i * 64;
-      if (c < d / 16) rms_scale_store_w<BF16>(v[i], r, wv[i], hasw, nullptr, lds_row + c * 16 * ES);
+      if (c < d / 16) {
+        if constexpr (PACK) {
+          uint4* dst = (uint4*)(lds_row + c * 16 * ES);
+          dst[0] = make_uint4(pn[i][0], pn[i][1], pn[i][2], pn[i][3]);
+          dst[1] = make_uint4(pn[i][4], pn[i][5], pn[i][6], pn[i][7]);
+        } else {
+          rms_scale_store_w<BF16>(v[i], r, wv[i], hasw, nullptr, lds_row + c * 16 * ES);
+        }
+      }
     }
   }
 
-  // out and norm_out of token t; after load_weight
+  // out and norm_out of token t; after norm()
   __device__ __forceinline__ void store(void* out, void* norm_out, int64_t t, int d, int lane) const {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int c = lane + i * 64;
       if (c < d / 16) {
-        rms_scale_store_w<BF16>(v[i], r, wv[i], hasw, (char*)norm_out + (t * d + c * 16) * ES);
         char* dst = (char*)out + (t * d + c * 16) * ES;
-        if constexpr (BF16) {
+        if constexpr (PACK) {
+          uint4* no = (uint4*)((char*)norm_out + (t * d + c * 16) * ES);
+          no[0] = make_uint4(pn[i][0], pn[i][1], pn[i][2], pn[i][3]);
+          no[1] = make_uint4(pn[i][4], pn[i][5], pn[i][6], pn[i][7]);
+          ((uint4*)dst)[0] = make_uint4(po[i][0], po[i][1], po[i][2], po[i][3]);
+          ((uint4*)dst)[1] = make_uint4(po[i][4], po[i][5], po[i][6], po[i][7]);
+        } else if constexpr (BF16) {
+          rms_scale_store_w<BF16>(v[i], r, wv[i], hasw, (char*)norm_out + (t * d + c * 16) * ES);
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             uint4 w;
@@ -3120,6 +3250,7 @@ struct CombineNormRow {
             ((uint4*)dst)[j] = w;
           }
         } else {
+          rms_scale_store_w<BF16>(v[i], r, wv[i], hasw, (char*)norm_out + (t * d + c * 16) * ES);
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             ((float4*)dst)[j] = make_float4(v[i][j * 4], v[i][j * 4 + 1], v[i][j * 4 + 2], v[i][j * 4 + 3]);
@@ -3140,6 +3271,7 @@ combine_norm_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ 
   CombineNormRow<BF16, NCH> cn;
   cn.compute(yperm, topi, topw, inv, eps, t, d, k, threadIdx.x & 63);
   cn.load_weight(weight, d, threadIdx.x & 63);
+  cn.norm(d, threadIdx.x & 63);
   cn.store(out, norm_out, t, d, threadIdx.x & 63);
 }
 
@@ -3161,10 +3293,11 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // The combine + norm + next router of the TOK tokens from t0, by the calling
 // workgroup's TOK waves (wave w: token t0 + w; waves < RK_SLICES also run the
 // router's K slices), in three phases: prefetch_slots (the top-k, weights and
-// yperm rows of each token, and the norm weight), prefetch_router (the router weights and bias of
-// the K-slice waves) and finish (the rest).  The loads of the first two do not
-// depend on yperm, so a caller that waits for yperm can issue them before it
-// waits.  COH: yperm (ybytes long) was written by other workgroups of the
+// yperm rows of each token, and the norm weight), prefetch_router (the router
+// weights and bias of the K-slice waves) and finish (the rest).  The loads of
+// the first two do not depend on yperm, so a caller that waits for yperm can
+// issue them before it waits, and also split the router weights into their
+// bf16 terms meanwhile (prepare_router).  COH: yperm (ybytes long) was written by other workgroups of the
 // running launch and is read device-coherently.
 template <int NCH, int EMAX, bool EXACT, int KSW, int TOK, bool COH>
 struct CnrBlock {
@@ -3183,6 +3316,7 @@ struct CnrBlock {
   RouteSlice<KSW, 1> rs;
   float bias = 0.0f;
   bool routed = false;  // router weights and bias loaded
+  bool split = false;   // router weights split into bf16 terms
 
   __device__ __forceinline__ static int nvalid_of(int64_t T, int64_t t0) { return (int)min<int64_t>(TOK, T - t0); }
 
@@ -3205,6 +3339,13 @@ struct CnrBlock {
       if (threadIdx.x < (unsigned)(TOK * EMAX) && re < E && ngb) bias = ngb[re];
     }
     routed = true;
+  }
+  // the split of the router weights into bf16 terms (waits for their loads),
+  // for a caller that has time to spare before the combine
+  __device__ __forceinline__ void prepare_router(int nE, int d) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (wave < RK_SLICES) rs.split(EXACT ? EMAX : nE, d, lane);  // uniform per wave
+    split = true;
   }
 
   __device__ __forceinline__ void finish(const void* __restrict__ yperm, int64_t ybytes, void* __restrict__ out,
@@ -3230,6 +3371,7 @@ struct CnrBlock {
     if (mine) {
       cn.template combine<COH>(yperm, eps, d, lane, ybytes);
       if (!LATE_STORE) cn.load_weight(weight, d, lane);
+      cn.norm(d, lane);
       cn.to_lds(d, lane, (char*)(sx + wave * d));
       if (!LATE_STORE) cn.store(out, norm_out, t0 + wave, d, lane);
     }
@@ -3239,7 +3381,8 @@ struct CnrBlock {
     if (!routed) prefetch_router(ngw, ngb, nE, d);
     if (wave < RK_SLICES) {  // uniform per wave
       rs.load_x_lds(sx, d, nvalid, lane);
-      rs.compute(E, d, lane, part);
+      if (split) rs.template compute<true>(E, d, lane, part);
+      else rs.compute(E, d, lane, part);
     }
     if (LATE_STORE && mine) cn.store(out, norm_out, t0 + wave, d, lane);
     lds_barrier();
@@ -4077,30 +4220,33 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
     const bool cnr = nrm && nr && act_dtype == SMAUL_DTYPE_BF16 && d % 16 == 0 && aligned16(yperm) &&
                      aligned16(out) && aligned16(nrm->out) && route_mfma_ok(nr->E, d, act_dtype) &&
                      aligned16(nr->gate_w) && route_ksw(d) == 4 && T <= 64;
-    DsDispatch dd{topi, topw, od, (int)T, (int)k, cnr ? sync : nullptr};
-    rc = canon ? launch_decode_stream<true, true>(a, &dd, stream) : launch_decode_stream<true, false>(a, &dd, stream);
-    if (rc) return rc;
+    GemmArgs b{};
+    b.x = hdn;
+    b.ldx = h;
+    b.wp = down_w8;
+    b.sp = down_s;
+    b.y = yperm;
+    b.ldy = d;
+    b.K = h;
+    b.N = d;
+    b.nt = h / 64;
+    b.tile = 64;
+    b.seg_off = seg_off;
+    b.tile_off = tile_off;
+    b.E = (int)E;
+    CnrArgs cr{};
     if (cnr) {
-      GemmArgs b{};
-      b.x = hdn;
-      b.ldx = h;
-      b.wp = down_w8;
-      b.sp = down_s;
-      b.y = yperm;
-      b.ldy = d;
-      b.K = h;
-      b.N = d;
-      b.nt = h / 64;
-      b.tile = 64;
-      b.seg_off = seg_off;
-      b.tile_off = tile_off;
-      b.E = (int)E;
       RouteOut no{};
       no.prob = nr->prob;
       no.topi = nr->topi;
       no.topw = nr->topw;
-      const CnrArgs cr{topi, topw, inv, out, nrm->weight, nrm->eps, nrm->out, T, (int)d, (int)k, nr->gate_w,
-                       nr->gate_b, no, (int)nr->E, (int)nr->k, sync, R * d * el};
+      cr = CnrArgs{topi, topw, inv, out, nrm->weight, nrm->eps, nrm->out, T, (int)d, (int)k, nr->gate_w,
+                   nr->gate_b, no, (int)nr->E, (int)nr->k, sync, R * d * el};
+    }
+    DsDispatch dd{topi, topw, od, (int)T, (int)k, cnr ? sync : nullptr};
+    rc = canon ? launch_decode_stream<true, true>(a, &dd, stream) : launch_decode_stream<true, false>(a, &dd, stream);
+    if (rc) return rc;
+    if (cnr) {
       rc = launch_down_cnr(b, canon, cr, stream);
       if (rc != 1) return rc;  // else: no fused instance for this shape
     }

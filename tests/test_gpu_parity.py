@@ -670,3 +670,25 @@ def test_moe_forward_chain(T, d, h, E, k, nE, nk, dtype):
     assert len(got_b) == 5
     for a, b in zip(ref_b, got_b):
         assert torch.equal(a.cpu(), b.cpu())
+
+
+@pytest.mark.parametrize("T,h,nE", [(64, 2560, 8), (17, 1024, 16)])
+def test_moe_chain_repeated(T, h, nE):
+    """The decode layer whose combine tail waits on a workspace counter
+    (cleared by the gate/up kernel of each call): 12 chained calls in a row,
+    each equal bit for bit to the unchained layer and router."""
+    d, E, k, nk = 1024, 8, 2, 2
+    print(f"case chain repeated T={T} h={h} nE={nE}", flush=True)
+    x, gw, gb, ex = make_moe(T * 7 + h, T, d, h, E, k, dtype=torch.bfloat16)
+    _, gwb, gbb, _ = make_moe(T * 11 + nE, 1, d, h, nE, nk, dtype=torch.bfloat16)
+    dx, dgw, dgb, dex = x.to(DEV), gw.to(DEV), gb.to(DEV), to_dev_experts(ex)
+    dgwb, dgbb = gwb.to(DEV), gbb.to(DEV)
+    ref = be().moe_forward_norm(dx, dgw, dgb, dex, k, 64, None, 1e-6)
+    ref_r = be().moe_router(ref[4], dgwb, dgbb, nk)
+    for it in range(12):
+        got = be().moe_forward_norm(dx, dgw, dgb, dex, k, 64, None, 1e-6, next_router=(dgwb, dgbb, nk))
+        torch.cuda.synchronize()
+        for a, b in zip(ref, got[:5]):
+            assert torch.equal(a.cpu(), b.cpu()), it
+        for a, b in zip(ref_r, got[5]):
+            assert torch.equal(a.cpu(), b.cpu()), it
