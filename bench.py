@@ -33,6 +33,7 @@ Only one GPU is measured: ``--gpus`` above 1 exits with a message.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import statistics
@@ -399,6 +400,11 @@ def main():
     # idle, the first ~35 layers of a cold start run through a power-management
     # transient (gate_up 367 -> 474 -> 358 us per launch in a kernel trace),
     # which a 5-step warm-up does not cover.
+    # The garbage collector stays off through the GPU legs (as timeit does): a
+    # collection pass in the middle of a timed loop leaves the GPU idle for
+    # tens of ms, and the kernels after such a gap run in that transient.
+    gc.collect()
+    gc.disable()
     c5_res = c5_inputs = None
     if not args.no_c5:
         log("bench: config 5")
@@ -461,6 +467,7 @@ def main():
             res["decode"] = decode_bench(be, max(5, args.steps), args.warmup)
         except Exception as exc:
             res["decode"] = {"error": f"{type(exc).__name__}: {exc}"}
+    gc.enable()
     if not args.no_cpu:
         log("bench: CPU baseline")
         try:
