@@ -2848,14 +2848,17 @@ __device__ __forceinline__ int combine_slots(const int64_t* topi, const float* t
   return n;
 }
 
-template <bool BF16, int CW>
+template <bool BF16, int CW, int KM>
 __global__ void __launch_bounds__(256)
 combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
                const float* __restrict__ topw, const int32_t* __restrict__ inv,
                void* __restrict__ out, int64_t T, int d, int k) {
-  // a thread handles CW (16, or 8 when d % 16 != 0) consecutive columns of
-  // one token; every row load of its k slots is issued before the first product
-  static_assert(CW == 8 || CW == 16, "columns per thread");
+  // a thread handles CW consecutive columns of one token (the widest of 32,
+  // 16, 8 that divides d; 32 for bf16 only); every row load of its k <= KM
+  // slots is issued before the first product, and registers are held for KM
+  // slots only
+  static_assert(CW == 8 || CW == 16 || (CW == 32 && BF16), "columns per thread");
+  static_assert(KM == 2 || KM == 4 || KM == 8, "slots per token");
   constexpr int NV = BF16 ? CW / 8 : CW / 4;  // 16-byte loads per row chunk
   const int cpt = d / CW;                      // chunks per token (d % CW == 0)
   const int64_t gidx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -2865,9 +2868,9 @@ combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
   int rw[8];
   float wt[8];
   const int n = combine_slots(topi, topw, inv, t, k, rw, wt);
-  uint4 yv[8][NV];
+  uint4 yv[KM][NV];
 #pragma unroll
-  for (int s = 0; s < 8; ++s)
+  for (int s = 0; s < KM; ++s)
     if (s < n) {
       const char* src = (const char*)yperm + ((int64_t)rw[s] * d + c0) * (BF16 ? 2 : 4);
 #pragma unroll
@@ -2877,7 +2880,7 @@ combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
 #pragma unroll
   for (int q = 0; q < CW; ++q) acc[q] = 0.0f;
 #pragma unroll
-  for (int s = 0; s < 8; ++s)
+  for (int s = 0; s < KM; ++s)
     if (s < n) {
       float y[CW];
 #pragma unroll
@@ -3981,17 +3984,28 @@ int smaul_moe_combine(const void* yperm, int act_dtype, const int64_t* topi, con
   if (T == 0) return SMAUL_OK;
   if (!yperm || !topi || !topw || !inv || !out) return fail(SMAUL_ERR_INVALID, "combine: null pointer");
   if (!aligned16(yperm) || !aligned16(out)) return fail(SMAUL_ERR_INVALID, "combine: unaligned buffers");
-  const bool wide = d % 16 == 0;
-  const int64_t total = T * (d / (wide ? 16 : 8));
-  const int64_t blocks = (total + 255) / 256;
-  const dim3 grid((unsigned)blocks), block(256);
-  if (act_dtype == SMAUL_DTYPE_BF16) {
-    if (wide) hipLaunchKernelGGL((combine_kernel<true, 16>), grid, block, 0, stream, yperm, topi, topw, inv, out, T, (int)d, (int)k);
-    else hipLaunchKernelGGL((combine_kernel<true, 8>), grid, block, 0, stream, yperm, topi, topw, inv, out, T, (int)d, (int)k);
+  const bool bf16 = act_dtype == SMAUL_DTYPE_BF16;
+  const int cw = (bf16 && d % 32 == 0) ? 32 : d % 16 == 0 ? 16 : 8;
+  const int km = k <= 2 ? 2 : k <= 4 ? 4 : 8;
+  const int64_t total = T * (d / cw);
+  const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+#define SMAUL_COMB(B, CW, KM)                                                                                  \
+  hipLaunchKernelGGL((combine_kernel<B, CW, KM>), grid, block, 0, stream, yperm, topi, topw, inv, out, T, (int)d, \
+                     (int)k)
+#define SMAUL_COMB_K(B, CW)       \
+  if (km == 2) SMAUL_COMB(B, CW, 2); \
+  else if (km == 4) SMAUL_COMB(B, CW, 4); \
+  else SMAUL_COMB(B, CW, 8)
+  if (bf16) {
+    if (cw == 32) { SMAUL_COMB_K(true, 32); }
+    else if (cw == 16) { SMAUL_COMB_K(true, 16); }
+    else { SMAUL_COMB_K(true, 8); }
   } else {
-    if (wide) hipLaunchKernelGGL((combine_kernel<false, 16>), grid, block, 0, stream, yperm, topi, topw, inv, out, T, (int)d, (int)k);
-    else hipLaunchKernelGGL((combine_kernel<false, 8>), grid, block, 0, stream, yperm, topi, topw, inv, out, T, (int)d, (int)k);
+    if (cw == 16) { SMAUL_COMB_K(false, 16); }
+    else { SMAUL_COMB_K(false, 8); }
   }
+#undef SMAUL_COMB_K
+#undef SMAUL_COMB
   return check_launch("combine_kernel");
 }
 
