@@ -188,7 +188,13 @@ int smaul_rms_norm(const void* x, int act_dtype, const float* weight, void* out,
  * one call; SwiFFN_MoE.forward of model.py:557-585.  `workspace` must hold
  * smaul_moe_workspace_size(...) bytes (256-byte aligned).  prob/topi/topw are
  * the router outputs (kept by the module as last_prob / last_topi); counts is
- * int32 [E] (expert_token_counts; last_executed is counts > 0).
+ * int32 [E] (expert_token_counts; last_executed is counts > 0).  In the
+ * decode regime (T <= 64, bf16, d % 16 == 0, d <= 1024, canonical codes, an
+ * 8-wave down instance) the combine runs in the tail of the down-projection
+ * kernel, with the same results: the first workgroups to finish their units
+ * wait for the rest through a counter in the workspace (cleared by the
+ * gate/up kernel of the same call), so two calls must not share one
+ * workspace concurrently.
  */
 int64_t smaul_moe_workspace_size(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
                                  int act_dtype);
@@ -230,7 +236,9 @@ int smaul_moe_forward_noalloc(const void* x, int act_dtype, const float* gate_w,
  * RMSNorm.forward, model.py:124-139): out as smaul_moe_forward writes it, and
  * norm_out [T, d] (act_dtype) = smaul_rms_norm(out, norm_w, eps), bit for bit.
  * With d % 16 == 0 and d <= 4096 the norm is fused into the combine kernel
- * (one wave per token); otherwise the two kernels run one after the other.
+ * (one wave per token), which in the decode regime of smaul_moe_forward runs
+ * in the tail of the down-projection kernel; otherwise the two kernels run
+ * one after the other.
  * No counterpart in the reference: its Block norms the FFN output in fp32
  * (n4 on fx.float(), model.py:640-641), so norm_out is not that norm; it is
  * for stacks whose next MoE layer reads the normalised rows in act_dtype

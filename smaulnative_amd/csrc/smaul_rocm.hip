@@ -2268,6 +2268,10 @@ __device__ __forceinline__ void cnr_tail(const CnrArgs& cr, const void* y, int32
   b.finish(y, cr.ybytes, cr.out, cr.weight, cr.eps, cr.norm_out, cr.T, cr.d, cr.ngw, cr.ngb, cr.no, cr.nE, cr.nk, t0);
 }
 
+// The same tail without a next router (defined after CombineNormRow)
+template <bool NORM>
+__device__ void cn_tail(const CnrArgs& cr, const void* y, int32_t* arr, int32_t* err);
+
 // FUSED (gate/up only): every workgroup ranks the T <= 64 tokens per expert
 // itself into LDS (one wave, ballot ranks in token order, the same rule as
 // dispatch_one_wave) instead of reading a dispatch written by an earlier
@@ -2275,15 +2279,17 @@ __device__ __forceinline__ void cnr_tail(const CnrArgs& cr, const void* y, int32
 // perm_row, perm_w, inv) for the down projection and the combine.  The
 // top-k is read from dd.topi/dd.topw (the router kernel's output).
 //
-// CNR (down only, 8 waves): after its units every workgroup waits for its own
-// device-scope output stores, then counts itself in sync[0]; the first
+// TAIL (down only, 8 waves): after its units every workgroup waits for its
+// own device-scope output stores, then counts itself in sync[0]; the first
 // ceil(T / 8) workgroups to arrive load what the combine needs besides the
 // outputs (slots, router weights), wait (a bounded poll: the others are
-// already running) until all have arrived, and each then runs the combine,
-// norm and next layer's router for 8 tokens, reading the outputs
-// device-coherently.  This replaces the separate
-// combine_norm_route_kernel launch, with the same arithmetic (CnrBlock).
-template <bool SWIGLU, bool CANON, int KBW, bool FUSED, bool CNR = false, int CEMAX = 8, bool CEXACT = false>
+// already running) until all have arrived, and each then combines 8 tokens,
+// reading the outputs device-coherently: TAIL_CNR also normalises them and
+// runs the next layer's router (replacing the combine_norm_route_kernel
+// launch, with the same arithmetic: CnrBlock), TAIL_CN normalises
+// (combine_norm_kernel's arithmetic), TAIL_C only combines (combine_kernel's).
+constexpr int TAIL_NONE = 0, TAIL_C = 1, TAIL_CN = 2, TAIL_CNR = 3;
+template <bool SWIGLU, bool CANON, int KBW, bool FUSED, int TAIL = TAIL_NONE, int CEMAX = 8, bool CEXACT = false>
 __global__ void __launch_bounds__(DS_WMAX * 64)
 decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd, CnrArgs cr) {
   constexpr int NH = SWIGLU ? 2 : 1;
@@ -2305,18 +2311,18 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd, CnrArgs cr) {
   const int64_t U = (int64_t)sg.total * ctn;
   const int u0 = (int)((int64_t)blockIdx.x * U / gridDim.x);
   const int u1 = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
-  if constexpr (!CNR) {
+  constexpr bool COH = TAIL != TAIL_NONE;
+  static_assert(!COH || !SWIGLU, "the combine follows the down projection");
+  if constexpr (!COH) {
     if (u0 >= u1) return;  // uniform per workgroup
   }
   if (u0 < u1) {
     // two row tiles when any segment has more than 16 rows
-    if (__ballot(sg.rows > 16) != 0) ds_body<SWIGLU, CANON, KBW, 2, CNR>(p, sg, ridx, u0, u1, ctn, red, nw);
-    else ds_body<SWIGLU, CANON, KBW, 1, CNR>(p, sg, ridx, u0, u1, ctn, red, nw);
+    if (__ballot(sg.rows > 16) != 0) ds_body<SWIGLU, CANON, KBW, 2, COH>(p, sg, ridx, u0, u1, ctn, red, nw);
+    else ds_body<SWIGLU, CANON, KBW, 1, COH>(p, sg, ridx, u0, u1, ctn, red, nw);
   }
-  if constexpr (CNR) {
-    static_assert(!SWIGLU, "the combine follows the down projection");
-    cnr_tail<CEMAX, CEXACT>(cr, p.y, cr.sync, cr.sync + 1);
-  }
+  if constexpr (TAIL == TAIL_CNR) cnr_tail<CEMAX, CEXACT>(cr, p.y, cr.sync, cr.sync + 1);
+  if constexpr (TAIL == TAIL_CN || TAIL == TAIL_C) cn_tail<TAIL == TAIL_CN>(cr, p.y, cr.sync, cr.sync + 1);
 }
 
 // K blocks per wave of the streaming decode kernel for K/64 = nkb blocks
@@ -2386,11 +2392,11 @@ int launch_down_cnr_e(const GemmArgs& a, int kbw, int64_t g, const CnrArgs& cr, 
   const DsDispatch none{};
   const dim3 grid((unsigned)g), block(8 * 64);
   if (kbw == 2)
-    hipLaunchKernelGGL((decode_stream_kernel<false, true, 2, false, true, EMAX, EXACT>), grid, block, 0, stream, a, 8,
-                       none, cr);
+    hipLaunchKernelGGL((decode_stream_kernel<false, true, 2, false, TAIL_CNR, EMAX, EXACT>), grid, block, 0, stream,
+                       a, 8, none, cr);
   else
-    hipLaunchKernelGGL((decode_stream_kernel<false, true, 5, false, true, EMAX, EXACT>), grid, block, 0, stream, a, 8,
-                       none, cr);
+    hipLaunchKernelGGL((decode_stream_kernel<false, true, 5, false, TAIL_CNR, EMAX, EXACT>), grid, block, 0, stream,
+                       a, 8, none, cr);
   return check_launch("decode_stream_kernel");
 }
 
@@ -2406,6 +2412,33 @@ int launch_down_cnr(const GemmArgs& a, bool canon, const CnrArgs& cr, hipStream_
   if (cr.nE > 8) return launch_down_cnr_e<16, false>(a, kbw, g, cr, stream);
   if (cr.nE == 8) return launch_down_cnr_e<8, true>(a, kbw, g, cr, stream);
   return launch_down_cnr_e<8, false>(a, kbw, g, cr, stream);
+}
+
+// The decode down projection with the combine (norm: and the output RMSNorm)
+// in its tail, for layers without a next router.  Returns 1 when the shape
+// has no such instance: canonical codes, 8 K-split waves, d <= 1024 and at
+// least ceil(T / 8) workgroups.
+int launch_down_cn(const GemmArgs& a, bool canon, const CnrArgs& cr, bool norm, hipStream_t stream) {
+  if (!canon || a.N % 16 != 0 || a.E > 64 || cr.d > 1024) return 1;
+  const int64_t nkb = a.K / 64;
+  const int kbw = ds_kbw(nkb, false);
+  if (kbw == 0 || nkb / kbw != 8) return 1;
+  const int64_t ctn = a.N / 16;
+  const int64_t g = std::min<int64_t>(cu_count(), std::max<int64_t>(1, a.E * ctn * (64 / DS_ROWS)));
+  if (g < (cr.T + CNR_TAIL_TOK - 1) / CNR_TAIL_TOK) return 1;
+  const DsDispatch none{};
+  const dim3 grid((unsigned)g), block(8 * 64);
+#define SMAUL_CN(KB, TL) \
+  hipLaunchKernelGGL((decode_stream_kernel<false, true, KB, false, TL>), grid, block, 0, stream, a, 8, none, cr)
+  if (kbw == 2) {
+    if (norm) SMAUL_CN(2, TAIL_CN);
+    else SMAUL_CN(2, TAIL_C);
+  } else {
+    if (norm) SMAUL_CN(5, TAIL_CN);
+    else SMAUL_CN(5, TAIL_C);
+  }
+#undef SMAUL_CN
+  return check_launch("decode_stream_kernel");
 }
 
 template <bool SWIGLU, bool CANON>
@@ -3132,8 +3165,8 @@ struct CombineNormRow {
                                         int k) {
     n = combine_slots(topi, topw, inv, t, k, rw, wt);
   }
-  // the combine of the slots loaded by slots(), and the row's 1/rms
-  template <bool COH = false>
+  // the combine of the slots loaded by slots(), and (SS) the row's 1/rms
+  template <bool COH = false, bool SS = true>
   __device__ __forceinline__ void combine(const void* yperm, float eps, int d, int lane, int64_t ybytes = 0) {
     const int nch = d / 16;
     float ss = 0.0f;
@@ -3182,11 +3215,13 @@ struct CombineNormRow {
           for (int q = 0; q < 16; ++q) v[i][q] = bf2f(f2bf(v[i][q]));
         }
       }
-      ss = rms_chunk_sumsq(ss, v[i]);
+      if constexpr (SS) ss = rms_chunk_sumsq(ss, v[i]);
     }
-    // rms_norm_kernel also adds RMS_KEEP - NCH all-zero chunks here: +0 changes nothing
-    ss = wave_sum(ss);
-    r = 1.0f / __fsqrt_rn(ss / (float)d + eps);
+    if constexpr (SS) {
+      // rms_norm_kernel also adds RMS_KEEP - NCH all-zero chunks here: +0 changes nothing
+      ss = wave_sum(ss);
+      r = 1.0f / __fsqrt_rn(ss / (float)d + eps);
+    }
   }
 
   // PACK: the normalised row, (v * r) * weight rounded to bf16, into pn;
@@ -3228,6 +3263,20 @@ struct CombineNormRow {
     }
   }
 
+  // out of token t alone (PACK); after combine()
+  __device__ __forceinline__ void store_out(void* out, int64_t t, int d, int lane) const {
+    static_assert(PACK, "bf16 rows of one chunk per lane");
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = lane + i * 64;
+      if (c < d / 16) {
+        uint4* dst = (uint4*)((char*)out + (t * d + c * 16) * ES);
+        dst[0] = make_uint4(po[i][0], po[i][1], po[i][2], po[i][3]);
+        dst[1] = make_uint4(po[i][4], po[i][5], po[i][6], po[i][7]);
+      }
+    }
+  }
+
   // out and norm_out of token t; after norm()
   __device__ __forceinline__ void store(void* out, void* norm_out, int64_t t, int d, int lane) const {
 #pragma unroll
@@ -3262,6 +3311,41 @@ struct CombineNormRow {
     }
   }
 };
+
+// The same tail without a next router (a layer whose caller routes its output
+// itself): the first ceil(T / 8) workgroups to arrive combine 8 tokens each,
+// one wave per token, with CombineNormRow (the arithmetic of combine_kernel,
+// and with NORM of combine_norm_kernel), reading y device-coherently.
+template <bool NORM>
+__device__ void cn_tail(const CnrArgs& cr, const void* y, int32_t* arr, int32_t* err) {
+  __shared__ int s_arrival;
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's output stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) s_arrival = (int)__hip_atomic_fetch_add(arr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const int ncw = (int)((cr.T + CNR_TAIL_TOK - 1) / CNR_TAIL_TOK);
+  const int a = s_arrival;
+  if (a >= ncw) return;  // uniform: the first ncw to arrive combine
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)a * CNR_TAIL_TOK + (threadIdx.x >> 6);
+  const bool mine = t < cr.T;  // uniform per wave
+  CombineNormRow<true, 1> cn;
+  if (mine) {
+    cn.slots(cr.topi, cr.topw, cr.inv, t, cr.k);
+    if (NORM) cn.load_weight(cr.weight, cr.d, lane);
+  }
+  ds_spin(arr, (int)gridDim.x, err);
+  __syncthreads();
+  if (mine) {
+    cn.template combine<true, NORM>(y, cr.eps, cr.d, lane, cr.ybytes);
+    if constexpr (NORM) {
+      cn.norm(cr.d, lane);
+      cn.store(cr.out, cr.norm_out, t, cr.d, lane);
+    } else {
+      cn.store_out(cr.out, t, cr.d, lane);
+    }
+  }
+}
 
 template <bool BF16, int NCH>
 __global__ void __launch_bounds__(256)
@@ -4234,6 +4318,9 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
     const bool cnr = nrm && nr && act_dtype == SMAUL_DTYPE_BF16 && d % 16 == 0 && aligned16(yperm) &&
                      aligned16(out) && aligned16(nrm->out) && route_mfma_ok(nr->E, d, act_dtype) &&
                      aligned16(nr->gate_w) && route_ksw(d) == 4 && T <= 64;
+    // without a next router: the combine (and the norm) alone in that tail
+    const bool cn = !nr && act_dtype == SMAUL_DTYPE_BF16 && d % 16 == 0 && aligned16(yperm) && aligned16(out) &&
+                    (!nrm || aligned16(nrm->out)) && T <= 64;
     GemmArgs b{};
     b.x = hdn;
     b.ldx = h;
@@ -4257,11 +4344,16 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
       cr = CnrArgs{topi, topw, inv, out, nrm->weight, nrm->eps, nrm->out, T, (int)d, (int)k, nr->gate_w,
                    nr->gate_b, no, (int)nr->E, (int)nr->k, sync, R * d * el};
     }
-    DsDispatch dd{topi, topw, od, (int)T, (int)k, cnr ? sync : nullptr};
+    if (cn) {
+      cr = CnrArgs{topi, topw, inv, out, nrm ? nrm->weight : nullptr, nrm ? nrm->eps : 0.0f,
+                   nrm ? nrm->out : nullptr, T, (int)d, (int)k, nullptr, nullptr, RouteOut{}, 0, 0, sync,
+                   R * d * el};
+    }
+    DsDispatch dd{topi, topw, od, (int)T, (int)k, (cnr || cn) ? sync : nullptr};
     rc = canon ? launch_decode_stream<true, true>(a, &dd, stream) : launch_decode_stream<true, false>(a, &dd, stream);
     if (rc) return rc;
-    if (cnr) {
-      rc = launch_down_cnr(b, canon, cr, stream);
+    if (cnr || cn) {
+      rc = cnr ? launch_down_cnr(b, canon, cr, stream) : launch_down_cn(b, canon, cr, nrm != nullptr, stream);
       if (rc != 1) return rc;  // else: no fused instance for this shape
     }
     rc = smaul_moe_down(hdn, act_dtype, down_w8, down_s, yperm, seg_off, tile_off, max_tiles, E, d, h, tile,

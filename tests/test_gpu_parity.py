@@ -387,12 +387,15 @@ def test_moe_skewed_segments():
     assert rel_l2(out.float(), ref.out.float()) < 2e-3
 
 
-@pytest.mark.parametrize("T,d,h", [(900, 512, 1280), (64, 1024, 2560), (5, 256, 640)])
+@pytest.mark.parametrize("T,d,h", [(900, 512, 1280), (64, 1024, 2560), (5, 256, 640), (17, 1024, 2560),
+                                   (20, 1024, 1024)])
 def test_staged_call_equals_fused_call(T, d, h):
     """The five stage entries and the single-call layer give identical bits.
     At decode sizes the single call routes with one router block per 16 tokens
-    (the stage entry uses 64-token blocks) and its gate/up kernel dispatches
-    for itself, so this also checks that neither changes a bit."""
+    (the stage entry uses 64-token blocks), its gate/up kernel dispatches for
+    itself and (d = 1024: 8-wave down instances, 5 or 2 K blocks per wave) the
+    combine runs in the down kernel's tail, so this also checks that none of
+    them changes a bit; T = 17 leaves the last combining workgroup one token."""
     print(f"case staged T={T} d={d} h={h}", flush=True)
     x, gw, gb, experts = make_moe(91, T, d, h, 8, 2)
     b = be()
@@ -601,7 +604,9 @@ def test_rms_norm(T, d, dtype, weighted):
 
 
 @pytest.mark.parametrize("T,d,h,E,k,dtype,weighted", [
-    (64, 1024, 2560, 8, 2, torch.bfloat16, False),  # C4 layer: decode path, fused norm
+    (64, 1024, 2560, 8, 2, torch.bfloat16, False),  # C4 layer: combine + norm in the down kernel's tail
+    (64, 1024, 2560, 8, 2, torch.bfloat16, True),   # the same with a norm weight
+    (20, 1024, 1024, 8, 2, torch.bfloat16, True),   # the same tail on the 2-block down instance
     (40, 2048, 256, 4, 2, torch.bfloat16, True),    # two chunks per lane
     (300, 256, 640, 8, 2, torch.bfloat16, True),    # prefill path
     (33, 192, 320, 4, 3, torch.float32, False),     # fp32 activations
