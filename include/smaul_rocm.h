@@ -43,8 +43,13 @@ enum { SMAUL_DTYPE_F32 = 0, SMAUL_DTYPE_BF16 = 1 };
  * rewriting them on the fly.  SMAUL_FLAG_ALIGNED_CODES promises that every
  * expert code buffer starts on a 16-byte boundary, which lets the grouped
  * GEMMs stage code rows with 16-byte LDS-DMA loads.  Results are identical
- * with or without either flag. */
-enum { SMAUL_FLAG_CANONICAL_CODES = 1, SMAUL_FLAG_ALIGNED_CODES = 2 };
+ * with or without either flag.  SMAUL_FLAG_TILED_LAYOUT says that the expert
+ * code and scale buffers are in the tiled layout of smaul_fp8_tile_layout
+ * instead of FP8Linear's [out_f][in_f] / [out_f][in_f / tile]; it needs tile
+ * 64 and d, h multiples of 64, is accepted by smaul_moe_forward*,
+ * smaul_moe_gate_up, smaul_moe_down and smaul_swiffn_forward (rejected by
+ * smaul_fp8_linear), and gives the same results as the reference layout. */
+enum { SMAUL_FLAG_CANONICAL_CODES = 1, SMAUL_FLAG_ALIGNED_CODES = 2, SMAUL_FLAG_TILED_LAYOUT = 4 };
 
 /* Library version as an integer (major*10000 + minor*100 + patch). */
 int smaul_version(void);
@@ -74,6 +79,20 @@ int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* 
  * buffers 16-byte aligned.
  */
 int smaul_fp8_canonicalize(const uint8_t* codes, uint8_t* out, int64_t n, hipStream_t stream);
+
+/*
+ * One FP8Linear weight (codes uint8 [N][K], fp32 scales [N][K / 64], tile 64)
+ * rewritten for SMAUL_FLAG_TILED_LAYOUT: codes_out [K / 64][N][64] holds the
+ * canonical codes (as smaul_fp8_canonicalize writes them) of each 64-wide K
+ * block of every column, scales_out [K / 64][N] the scales.  A stage of the
+ * GEMMs (64 K of a run of columns) then reads whole cache lines of codes and
+ * of scales instead of one line per column.  No counterpart in the
+ * reference: it is the device repack step of a caller that keeps expert
+ * weights resident (RocmBackend's expert cache).  K % 64 == 0; code buffers
+ * 16-byte aligned; not in place.
+ */
+int smaul_fp8_tile_layout(const uint8_t* codes, const float* scales, uint8_t* codes_out, float* scales_out,
+                          int64_t N, int64_t K, hipStream_t stream);
 
 /*
  * MoE router: logits = x . gate_w^T (+ gate_b), prob = softmax(logits),

@@ -21,6 +21,7 @@ DTYPE_F32 = 0
 DTYPE_BF16 = 1
 FLAG_CANONICAL_CODES = 1
 FLAG_ALIGNED_CODES = 2
+FLAG_TILED_LAYOUT = 4
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -32,6 +33,7 @@ SIGNATURES = {
     "smaul_last_error": (ctypes.c_char_p, []),
     "smaul_fp8_linear": (_I, [_P, _I, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I, _P]),
     "smaul_fp8_canonicalize": (_I, [_P, _P, _I64, _P]),
+    "smaul_fp8_tile_layout": (_I, [_P, _P, _P, _P, _I64, _I64, _P]),
     "smaul_moe_router": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "smaul_moe_dispatch_workspace_size": (_I64, [_I64, _I64]),
     "smaul_moe_dispatch": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P]),

@@ -152,7 +152,21 @@ struct GemmArgs {
   const int32_t* tile_off;     // [E+1]
   int64_t R;
   int E;
+  int tiled;                   // codes/scales in the tiled layout (SMAUL_FLAG_TILED_LAYOUT)
 };
+
+// Where an expert's codes and scales for column n and 64-wide K block kb
+// live: codes at n * wc + kb * wk (+ k within the block), scales at
+// n * sc + kb * sk.  The reference layout ([N][K] codes, [N][nt] scales:
+// FP8Linear's w8 / sc) or the tiled one ([K/64][N][64] codes, [K/64][N]
+// scales), in which the 64-wide K block of consecutive columns is
+// contiguous: a K stage of a column tile is then whole cache lines.
+struct WLayout {
+  int64_t wc, wk, sc, sk;
+};
+__device__ __forceinline__ WLayout wlayout(const GemmArgs& p) {
+  return p.tiled ? WLayout{64, p.N * 64, 1, p.N} : WLayout{p.K, 64, p.nt, 1};
+}
 
 // The expert segment of m-tile mt of a grouped GEMM, with all of its loads
 // in one round trip: lane j reads tile_off[j], tile_off[j + 1], seg_off[j],
@@ -290,6 +304,7 @@ fp8_gemm_kernel(GemmArgs p) {
   const int row0 = ts.row0, rows_here = ts.rows;
   const int n0 = nt_idx * BNO;
   const int64_t K = p.K, N = p.N, nt = p.nt;
+  const WLayout L = wlayout(p);
 
   const uint8_t* W1 = ts.w1;
   const float* S1 = ts.s1;
@@ -327,7 +342,7 @@ fp8_gemm_kernel(GemmArgs p) {
     const bool up = SWIGLU && r >= BNO;
     int64_t col = n0 + (up ? r - BNO : r);
     if (col >= N) col = N - 1;  // columns past N are computed but never stored
-    brow[i] = (up ? W2 : W1) + col * K;
+    brow[i] = (up ? W2 : W1) + col * L.wc;
   }
   // scale staging: slot q = tid + i*NT < SPS * BNB owns (sub, column)
   constexpr int S_CH = (SPS * BNB + NT - 1) / NT;
@@ -343,7 +358,7 @@ fp8_gemm_kernel(GemmArgs p) {
     const bool up = SWIGLU && s_col[i] >= BNO;
     int64_t col = n0 + (up ? s_col[i] - BNO : s_col[i]);
     if (col >= N) col = N - 1;
-    srow[i] = (up ? S2 : S1) + col * nt;
+    srow[i] = (up ? S2 : S1) + col * L.sc;
   }
   // K % 64 == 0: every stage is full and the loads need no K guard
   const bool full_k = (K & 63) == 0;
@@ -381,7 +396,8 @@ fp8_gemm_kernel(GemmArgs p) {
     for (int i = 0; i < B_CH; ++i) {
       const int64_t kk = k0 + bkoff[i];
       if constexpr (VEC) {
-        rb[i] = (full_k || kk < K) ? ldg16(brow[i] + kk) : make_uint4(0, 0, 0, 0);
+        // (the tiled layout needs K % 64 == 0: kk < K always)
+        rb[i] = (full_k || kk < K) ? ldg16(brow[i] + kt * L.wk + bkoff[i]) : make_uint4(0, 0, 0, 0);
       } else {
         uint32_t v[4] = {0, 0, 0, 0};
         {
@@ -398,7 +414,7 @@ fp8_gemm_kernel(GemmArgs p) {
       if constexpr (KMODE == 0) kb = kt * 2 + s_sub[i];
       else if constexpr (KMODE == 1) kb = kt;
       else kb = k0 / p.tile;
-      rs[i] = ldgf(srow[i] + (kb < nt ? kb : nt - 1));  // kb == nt only past K (zero data)
+      rs[i] = ldgf(srow[i] + (kb < nt ? kb : nt - 1) * L.sk);  // kb == nt only past K (zero data)
     }
   };
 
@@ -732,7 +748,8 @@ fp8_gemm_dma_kernel(GemmArgs p) {
   if (!tile_lookup<BM>(p, mt, lane, ts)) return;  // uniform per workgroup
   const int row0 = ts.row0, rows_here = ts.rows;
   const int n0 = nt_idx * BNO;
-  const int64_t K = p.K, nt = p.nt;
+  const int64_t K = p.K;
+  const WLayout L = wlayout(p);
 
   const uint8_t* W1 = ts.w1;
   const float* S1 = ts.s1;
@@ -766,21 +783,21 @@ fp8_gemm_dma_kernel(GemmArgs p) {
   uint32_t b_off;
   {
     const int r = lane >> 2;
-    b_off = (uint32_t)(r * K + (((lane & 3) ^ swz_b(r)) << 4));
+    b_off = (uint32_t)(r * L.wc + (((lane & 3) ^ swz_b(r)) << 4));
   }
   auto b_src = [&](int b) -> const uint8_t* {
     const int q = wave * B_INS + b;
     const bool up = SWIGLU && q * 16 >= BNO;
     const int64_t col0 = n0 + (up ? q * 16 - BNO : q * 16);
-    return (up ? W2 : W1) + col0 * K;
+    return (up ? W2 : W1) + col0 * L.wc;
   };
   // scale instruction `wave` (waves < S_INS) stages columns 64*wave + lane
   const float* s_src = S1;
   if (wave < S_INS) {
     const bool up = SWIGLU && wave * 64 >= BNO;
-    s_src = (up ? S2 : S1) + (n0 + (up ? wave * 64 - BNO : wave * 64)) * nt;
+    s_src = (up ? S2 : S1) + (n0 + (up ? wave * 64 - BNO : wave * 64)) * L.sc;
   }
-  const uint32_t s_off = (uint32_t)(lane * nt * 4);
+  const uint32_t s_off = (uint32_t)(lane * L.sc * 4);
 
   // The K advance of a stage goes into the (scalar) base addresses; the
   // per-lane offsets stay fixed.  Every wave issues DMA_MIN = A_INS + B_INS
@@ -788,12 +805,12 @@ fp8_gemm_dma_kernel(GemmArgs p) {
   const uint32_t lds0 = lds_offset(&smem[0]);
   auto dma_stage = [&](int kt, int buf) {
     const uint32_t lbase = lds0 + (uint32_t)(buf * STAGE);
-    if (S_INS == NW || wave < S_INS) dma4(s_src + kt, s_off, lbase + A_BYTES + B_BYTES + wave * 256);
+    if (S_INS == NW || wave < S_INS) dma4(s_src + kt * L.sk, s_off, lbase + A_BYTES + B_BYTES + wave * 256);
     const char* xa = (const char*)p.x + kt * 128;
 #pragma unroll
     for (int a = 0; a < A_INS; ++a) dma16(xa, a_off[a], lbase + (wave * A_INS + a) * 1024);
 #pragma unroll
-    for (int b = 0; b < B_INS; ++b) dma16(b_src(b) + kt * 64, b_off, lbase + A_BYTES + (wave * B_INS + b) * 1024);
+    for (int b = 0; b < B_INS; ++b) dma16(b_src(b) + kt * L.wk, b_off, lbase + A_BYTES + (wave * B_INS + b) * 1024);
   };
 
   // ---- fragment addresses (fixed over K) -----------------------------------
@@ -1049,7 +1066,8 @@ __device__ __forceinline__ void decode_wave(const GemmArgs& p, const uint8_t* W1
                                             f32x4_t (*acc2)[4]) {
   constexpr int NH = SWIGLU ? 2 : 1;
   const int kq = (lane >> 4) * 16;
-  const int64_t tstride_w = 16 * p.K, tstride_s = 16 * p.nt;
+  const WLayout L = wlayout(p);
+  const int64_t tstride_w = 16 * L.wc, tstride_s = 16 * L.sc;
   // Row indices first; rows past the segment are computed, never stored.
   int64_t xr[NRT];
 #pragma unroll
@@ -1074,8 +1092,8 @@ __device__ __forceinline__ void decode_wave(const GemmArgs& p, const uint8_t* W1
     for (int h = 0; h < NH; ++h)
 #pragma unroll
       for (int t = 0; t < CT; ++t) {
-        bw[slot][h][t] = ldg16((h ? W2 : W1) + t * tstride_w + kb * 64 + kq);
-        sw[slot][h][t] = ldgf((h ? S2 : S1) + t * tstride_s + kb);
+        bw[slot][h][t] = ldg16((h ? W2 : W1) + t * tstride_w + kb * L.wk + kq);
+        sw[slot][h][t] = ldgf((h ? S2 : S1) + t * tstride_s + kb * L.sk);
       }
   };
   auto fetch_a = [&](int slot, int64_t kb) {
@@ -1171,10 +1189,11 @@ decode_gemm_kernel(GemmArgs p, int col_groups, int ks_count) {
   // the lane's column of tile 0 (the launcher guarantees N % (16 * CT) == 0,
   // so every tile of every group lies inside the matrix)
   const int64_t col = n0 + (lane & 15);
-  const uint8_t* W1 = table_entry(p.wp, e) + col * p.K;
-  const float* S1 = table_entry(p.sp, e) + col * p.nt;
-  const uint8_t* W2 = SWIGLU ? table_entry(p.wp2, e) + col * p.K : W1;
-  const float* S2 = SWIGLU ? table_entry(p.sp2, e) + col * p.nt : S1;
+  const WLayout L = wlayout(p);
+  const uint8_t* W1 = table_entry(p.wp, e) + col * L.wc;
+  const float* S1 = table_entry(p.sp, e) + col * L.sc;
+  const uint8_t* W2 = SWIGLU ? table_entry(p.wp2, e) + col * L.wc : W1;
+  const float* S2 = SWIGLU ? table_entry(p.sp2, e) + col * L.sc : S1;
   const int64_t nblk = (p.K >> 6) / ks_count;
   const int64_t kb0 = ks * nblk;
   const int nthr = ks_count * 64;
@@ -1979,11 +1998,12 @@ struct DsRing {
     int e, r0, nr;
     ds_locate(sg, j, e, r0, nr);
     const int64_t col = (int64_t)ct * 16 + (lane & 15);
-    wsrc[0] = ds_ptr<const uint8_t>(sg.w1, e) + col * p.K + kb0 * 64 + kq;
-    ssrc[0] = ds_ptr<const float>(sg.s1, e) + col * p.nt + kb0;
+    const WLayout L = wlayout(p);
+    wsrc[0] = ds_ptr<const uint8_t>(sg.w1, e) + col * L.wc + kb0 * L.wk + kq;
+    ssrc[0] = ds_ptr<const float>(sg.s1, e) + col * L.sc + kb0 * L.sk;
     if constexpr (SWIGLU) {
-      wsrc[NH - 1] = ds_ptr<const uint8_t>(sg.w2, e) + col * p.K + kb0 * 64 + kq;
-      ssrc[NH - 1] = ds_ptr<const float>(sg.s2, e) + col * p.nt + kb0;
+      wsrc[NH - 1] = ds_ptr<const uint8_t>(sg.w2, e) + col * L.wc + kb0 * L.wk + kq;
+      ssrc[NH - 1] = ds_ptr<const float>(sg.s2, e) + col * L.sc + kb0 * L.sk;
     }
   }
   __device__ __forceinline__ void fetch(const GemmArgs& p, const DsSegs& sg, int ctn, int64_t kb0, int kq, int lane,
@@ -1991,12 +2011,13 @@ struct DsRing {
     const uint8_t* ws[NH];
     const float* ss[NH];
     unit_src(p, sg, ctn, kb0, kq, lane, u, ws, ss);
+    const WLayout L = wlayout(p);
 #pragma unroll
     for (int b = 0; b < KBW; ++b)
 #pragma unroll
       for (int h = 0; h < NH; ++h) {
-        bw[slot][b][h] = ldg16(ws[h] + b * 64);
-        sw[slot][b][h] = ldgf(ss[h] + b);
+        bw[slot][b][h] = ldg16(ws[h] + b * L.wk);
+        sw[slot][b][h] = ldgf(ss[h] + b * L.sk);
       }
   }
 };
@@ -2016,6 +2037,7 @@ __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, con
   const f32x4_t z4 = {0.f, 0.f, 0.f, 0.f};
   const int last = u1 - 1;
   DsRing<SWIGLU, KBW> ring;
+  const WLayout L = wlayout(p);
 
   // the segment's activation rows, this wave's K slice
   uint4 a0[NRT][KBW], a1[NRT][KBW];
@@ -2092,8 +2114,8 @@ __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, con
         g1[h] = __builtin_bit_cast(bf16x8_t, make_uint4(d[4], d[5], d[6], d[7]));
         sc[h] = ring.sw[i][b][h];
         if (refill) {
-          ring.bw[i][b][h] = ldg16(nws[h] + b * 64);
-          ring.sw[i][b][h] = ldgf(nss[h] + b);
+          ring.bw[i][b][h] = ldg16(nws[h] + b * L.wk);
+          ring.sw[i][b][h] = ldgf(nss[h] + b * L.sk);
         }
       }
 #pragma unroll
@@ -3531,6 +3553,36 @@ canonicalize_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ out, i
   }
 }
 
+// The tiled layout (WLayout): canonical codes out[(kb * N + n) * 64 + j] =
+// in[n * K + kb * 64 + j], one thread per 16 bytes of out, and fp32 scales
+// sout[kb * N + n] = sin[n * nb + kb], nb = K / 64.
+__global__ void __launch_bounds__(256)
+tile_codes_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ out, int64_t N, int64_t K) {
+  const int64_t nv = N * K / 16;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += stride) {
+    const int64_t o = i * 16;
+    const int64_t kb = o / (N * 64);
+    const int64_t n = (o / 64) % N;
+    const int64_t j = o % 64;
+    uint4 v = *(const uint4*)(in + n * K + kb * 64 + j);
+    v.x = canon4(v.x);
+    v.y = canon4(v.y);
+    v.z = canon4(v.z);
+    v.w = canon4(v.w);
+    *(uint4*)(out + o) = v;
+  }
+}
+
+__global__ void __launch_bounds__(256)
+tile_scales_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t N, int64_t nb) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < N * nb; i += stride) {
+    const int64_t kb = i / N, n = i - kb * N;
+    out[i] = in[n * nb + kb];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // host helpers
 // ---------------------------------------------------------------------------
@@ -3667,6 +3719,8 @@ int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* 
                 (long long)tile, (long long)in_f, (long long)out_f);
   if (!dtype_ok(x_dtype) || y_dtype != SMAUL_DTYPE_F32)
     return fail(SMAUL_ERR_INVALID, "x dtype must be f32|bf16 and y dtype f32");
+  if (flags & SMAUL_FLAG_TILED_LAYOUT)
+    return fail(SMAUL_ERR_INVALID, "fp8_linear: codes and scales must be in the reference layout");
   if (kmode_of(tile) < 0)
     return fail(SMAUL_ERR_UNSUPPORTED, "tile %lld: need 32 or a multiple of 64", (long long)tile);
   if (rows == 0) return SMAUL_OK;
@@ -3923,6 +3977,8 @@ static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* 
     return fail(SMAUL_ERR_INVALID, "moe gemm: block_m must come from smaul_moe_block_m");
   if (!act || !w1 || !s1 || !out || !seg_off || !tile_off || (swiglu && (!w2 || !s2)))
     return fail(SMAUL_ERR_INVALID, "moe gemm: null pointer");
+  if ((flags & SMAUL_FLAG_TILED_LAYOUT) && (tile != 64 || K % 64 != 0))
+    return fail(SMAUL_ERR_INVALID, "moe gemm: the tiled layout needs tile 64 and K a multiple of 64");
   if (max_tiles == 0) return SMAUL_OK;
   GemmArgs a{};
   a.x = act;
@@ -3941,6 +3997,7 @@ static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* 
   a.seg_off = seg_off;
   a.tile_off = tile_off;
   a.E = (int)E;
+  a.tiled = (flags & SMAUL_FLAG_TILED_LAYOUT) != 0;
   const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
   if (block_m == DECODE_BM) {
     // decode kernels: K in whole 64-wide blocks, one scale per block, rows per
@@ -4017,6 +4074,7 @@ static int dense_gemm(bool swiglu, const void* act, int act_dtype, const uint8_t
   a.tile_off = nullptr;
   a.R = rows;
   a.E = 1;
+  a.tiled = (flags & SMAUL_FLAG_TILED_LAYOUT) != 0;
   const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
   const int64_t bno = swiglu ? CfgDmaGU::BN / 2 : CfgDmaDown::BN;
   if (dma_gemm_ok(a, act_dtype, flags | SMAUL_FLAG_ALIGNED_CODES, rows, bno)) {
@@ -4047,6 +4105,8 @@ int smaul_swiffn_forward(const void* x, int act_dtype, const uint8_t* gate_w8, c
     return fail(SMAUL_ERR_INVALID, "swiffn: need rows >= 0 and positive d, h, tile");
   if (kmode_of(tile) < 0) return fail(SMAUL_ERR_UNSUPPORTED, "swiffn: tile must be 32 or a multiple of 64");
   if (d % 16 != 0 || h % 16 != 0) return fail(SMAUL_ERR_UNSUPPORTED, "swiffn: d and h must be multiples of 16");
+  if ((flags & SMAUL_FLAG_TILED_LAYOUT) && (tile != 64 || d % 64 != 0 || h % 64 != 0))
+    return fail(SMAUL_ERR_INVALID, "swiffn: the tiled layout needs tile 64 and d, h multiples of 64");
   const int64_t need = smaul_swiffn_workspace_size(rows, h, act_dtype);
   if (workspace_bytes < need) return fail(SMAUL_ERR_INVALID, "swiffn: workspace %lld < %lld bytes",
                                           (long long)workspace_bytes, (long long)need);
@@ -4244,6 +4304,8 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
   if (T == 0) return SMAUL_OK;
   if (T * k > 2147483647LL) return fail(SMAUL_ERR_UNSUPPORTED, "moe_forward: T*k exceeds int32");
   if (((uintptr_t)workspace & 255u) != 0) return fail(SMAUL_ERR_INVALID, "moe_forward: workspace not 256-byte aligned");
+  if ((flags & SMAUL_FLAG_TILED_LAYOUT) && (tile != 64 || d % 64 != 0 || h % 64 != 0))
+    return fail(SMAUL_ERR_INVALID, "moe_forward: the tiled layout needs tile 64 and d, h multiples of 64");
   const int64_t el = act_dtype == SMAUL_DTYPE_BF16 ? 2 : 4;
   const int64_t R = T * k;
   const int64_t nb = route_blocks(T, E, d, act_dtype);
@@ -4315,6 +4377,7 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
     a.seg_off = seg_off;
     a.tile_off = tile_off;
     a.E = (int)E;
+    a.tiled = (flags & SMAUL_FLAG_TILED_LAYOUT) != 0;
     // the combine + norm + next router in the down kernel's tail, when the
     // shapes allow it (the same conditions as combine_norm_route_kernel, and
     // launch_down_cnr's)
@@ -4339,6 +4402,7 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
     b.seg_off = seg_off;
     b.tile_off = tile_off;
     b.E = (int)E;
+    b.tiled = a.tiled;
     CnrArgs cr{};
     if (cnr) {
       RouteOut no{};
@@ -4481,6 +4545,24 @@ int smaul_fp8_canonicalize(const uint8_t* codes, uint8_t* out, int64_t n, hipStr
   if (blocks > 8192) blocks = 8192;
   hipLaunchKernelGGL(canonicalize_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, codes, out, n);
   return check_launch("canonicalize_kernel");
+}
+
+int smaul_fp8_tile_layout(const uint8_t* codes, const float* scales, uint8_t* codes_out, float* scales_out,
+                          int64_t N, int64_t K, hipStream_t stream) {
+  if (N < 0 || K < 0 || K % 64 != 0) return fail(SMAUL_ERR_INVALID, "tile_layout: need N >= 0 and K a multiple of 64");
+  if (N == 0 || K == 0) return SMAUL_OK;
+  if (!codes || !scales || !codes_out || !scales_out) return fail(SMAUL_ERR_INVALID, "tile_layout: null pointer");
+  if (!aligned16(codes) || !aligned16(codes_out))
+    return fail(SMAUL_ERR_INVALID, "tile_layout: code buffers must be 16-byte aligned");
+  if (codes == codes_out || scales == scales_out) return fail(SMAUL_ERR_INVALID, "tile_layout: not in place");
+  const int64_t nv = N * K / 16, ns = N * (K / 64);
+  const unsigned bc = (unsigned)std::min<int64_t>(8192, std::max<int64_t>(1, (nv + 255) / 256));
+  const unsigned bs = (unsigned)std::min<int64_t>(8192, std::max<int64_t>(1, (ns + 255) / 256));
+  hipLaunchKernelGGL(tile_codes_kernel, dim3(bc), dim3(256), 0, stream, codes, codes_out, N, K);
+  int rc = check_launch("tile_codes_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(tile_scales_kernel, dim3(bs), dim3(256), 0, stream, scales, scales_out, N, K / 64);
+  return check_launch("tile_scales_kernel");
 }
 
 int smaul_selftest_topk(const float* vals, int64_t n, int64_t k, int64_t* out_idx) {

@@ -280,15 +280,20 @@ class RocmBackend:
     # ---- MoE (model.py:557-585) -------------------------------------------
     def _expert_entry(self, experts: Sequence[Sequence[torch.Tensor]], device, d, h, tile):
         """The repack cache entry of a set of experts: ``table``, a device int64
-        [6, E] table of the experts' buffer addresses, and ``ptrs``, the same
-        addresses as host ints.
+        [6, E] table of the experts' buffer addresses, ``ptrs``, the same
+        addresses as host ints, and ``flags``, the C-ABI flags that describe
+        the buffers they point at.
 
         Rows: gate codes, gate scales, up codes, up scales, down codes, down
         scales.  The code rows point at *canonical copies* of the ``w8``
         buffers (0x7F/0xFF rewritten to 0x7E/0xFE, the same +-448 values) so
         the GEMMs can use the hardware E4M3 converter directly; the stored
-        ``w8`` buffers are never modified.  fp32 contiguous scales are used in
-        place; other scales (a model cast to bf16) are widened into copies.
+        ``w8`` buffers are never modified.  With tile 64 and d, h multiples of
+        64 the copies are in the tiled layout (``smaul_fp8_tile_layout``:
+        each 64-wide K block of consecutive columns contiguous, scales K-major
+        in fp32), which the GEMMs stage in whole cache lines; otherwise the
+        codes keep FP8Linear's layout, fp32 contiguous scales are used in place
+        and other scales (a model cast to bf16) are widened into copies.
 
         The cache is keyed on the buffers' addresses and holds only weak
         references to them.  When a buffer's ``_version`` changes (requant,
@@ -324,9 +329,13 @@ class RocmBackend:
                                    f"expected {shapes[idx]}")
             if idx % 2 == 0 and t.dtype != torch.uint8:
                 raise RuntimeError(f"moe_forward: expert {e} codes must be uint8, got {t.dtype}")
-        copies = [torch.empty(t.numel(), dtype=torch.uint8, device=device) if i % 2 == 0 else None
+        tiled = tile == 64 and d % 64 == 0 and h % 64 == 0
+        copies = [torch.empty(t.numel(), dtype=torch.uint8, device=device) if i % 2 == 0 else
+                  (torch.empty(t.numel(), dtype=torch.float32, device=device) if tiled else None)
                   for i, t in enumerate(flat)]
-        ent = {"copies": copies, "refs": [weakref.ref(t) for t in flat], "versions": versions}
+        flags = _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES | (_lib.FLAG_TILED_LAYOUT if tiled else 0)
+        ent = {"copies": copies, "refs": [weakref.ref(t) for t in flat], "versions": versions, "tiled": tiled,
+               "flags": flags}
         self._refresh(ent, flat, lib, device)
         E = len(experts)
         rows = [[0] * E for _ in range(6)]
@@ -359,6 +368,17 @@ class RocmBackend:
     def _refresh(ent, flat, lib, device):
         """(Re)write the cached canonical codes and widened scales from the source buffers."""
         stream = _stream_handle(device)
+        if ent["tiled"]:
+            for n in range(0, len(flat), 2):
+                codes, sc = flat[n], flat[n + 1]
+                codes = codes if codes.is_contiguous() else codes.contiguous()
+                sc = sc if (sc.dtype == torch.float32 and sc.is_contiguous()) else sc.float().contiguous()
+                N, K = codes.shape
+                with torch.cuda.device(device):
+                    rc = lib.smaul_fp8_tile_layout(codes.data_ptr(), sc.data_ptr(), ent["copies"][n].data_ptr(),
+                                                   ent["copies"][n + 1].data_ptr(), N, K, stream)
+                _lib.check(rc, "fp8_tile_layout")
+            return
         for n, t in enumerate(flat):
             if n % 2 == 0:
                 src = t if t.is_contiguous() else t.contiguous()
@@ -394,14 +414,15 @@ class RocmBackend:
         x2 = x2 if x2.is_contiguous() else x2.contiguous()
         rows = x2.shape[0]
         dev = x.device
-        ptrs = self._expert_entry([buffers], dev, d, h, tile)["ptrs"]
+        ent = self._expert_entry([buffers], dev, d, h, tile)
+        ptrs = ent["ptrs"]
         out = torch.empty_like(x2)
         ws_bytes = lib.smaul_swiffn_workspace_size(rows, h, _ACT[x.dtype])
         ws = torch.empty(max(1, ws_bytes), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
             rc = lib.smaul_swiffn_forward(x2.data_ptr(), _ACT[x.dtype], *[ptrs[i][0] for i in range(6)],
                                           out.data_ptr(), ws.data_ptr(), ws_bytes, rows, d, h, tile,
-                                          _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES, _stream_handle(dev))
+                                          ent["flags"], _stream_handle(dev))
         _lib.check(rc, "swiffn_forward")
         return out.reshape(x.shape)
 
@@ -484,7 +505,8 @@ class RocmBackend:
         h = experts[0][0].shape[0]
         dev = x2.device
         act = _ACT[x2.dtype]
-        table = self._expert_entry(experts, dev, d, h, tile)["table"]
+        ent = self._expert_entry(experts, dev, d, h, tile)
+        table, eflags = ent["table"], ent["flags"]
         gw = gate_w.detach().float().contiguous()
         gb = None if gate_b is None else gate_b.detach().float().contiguous()
         R = T * top_k
@@ -506,13 +528,12 @@ class RocmBackend:
             sh = stream.cuda_stream
             rc = lib.smaul_moe_gate_up(x2.data_ptr(), act, disp["perm_row"].data_ptr(), tp, tp + row,
                                        tp + 2 * row, tp + 3 * row, hdn.data_ptr(), disp["seg_off"].data_ptr(),
-                                       disp["tile_off"].data_ptr(), max_tiles, E, d, h, tile, bm,
-                                       _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES, sh)
+                                       disp["tile_off"].data_ptr(), max_tiles, E, d, h, tile, bm, eflags, sh)
             _lib.check(rc, "moe_gate_up")
             rec(3)
             rc = lib.smaul_moe_down(hdn.data_ptr(), act, tp + 4 * row, tp + 5 * row, yperm.data_ptr(),
                                     disp["seg_off"].data_ptr(), disp["tile_off"].data_ptr(), max_tiles, E, d,
-                                    h, tile, bm, _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES, sh)
+                                    h, tile, bm, eflags, sh)
             _lib.check(rc, "moe_down")
             rec(4)
             rc = lib.smaul_moe_combine(yperm.data_ptr(), act, topi.data_ptr(), topw.data_ptr(),
@@ -602,7 +623,8 @@ class RocmBackend:
         x2 = x2 if x2.is_contiguous() else x2.contiguous()
         T = x2.shape[0]
         dev = x.device
-        table = self._expert_entry(experts, dev, d, h, tile)["table"]
+        ent = self._expert_entry(experts, dev, d, h, tile)
+        table, eflags = ent["table"], ent["flags"]
         gw = gate_w.detach()
         gw = gw if (gw.dtype == torch.float32 and gw.is_contiguous()) else gw.float().contiguous()
         gb = None
@@ -660,8 +682,7 @@ class RocmBackend:
             args = [x2.data_ptr(), act, gw.data_ptr(), None if gb is None else gb.data_ptr(),
                     tp, tp + row, tp + 2 * row, tp + 3 * row, tp + 4 * row, tp + 5 * row,
                     out.data_ptr(), prob.data_ptr(), topi.data_ptr(), topw.data_ptr(),
-                    counts.data_ptr(), ws.data_ptr(), ws_bytes, T, d, h, E, top_k, tile,
-                    _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES]
+                    counts.data_ptr(), ws.data_ptr(), ws_bytes, T, d, h, E, top_k, tile, eflags]
             with torch.cuda.device(dev):
                 if norm is None:
                     rc = lib.smaul_moe_forward(*args, _stream_handle(dev))

@@ -479,6 +479,107 @@ def test_moe_raw_codes_any_flags(T, flags, block_m):
     assert err < 2e-3
 
 
+def tiled_copies(ex_dev):
+    """The experts' buffers rewritten by smaul_fp8_tile_layout (canonical codes)."""
+    from smaulnative_amd import _lib
+    lib = _lib.load()
+    out = []
+    for bufs in ex_dev:
+        t = []
+        for j in range(0, 6, 2):
+            codes, sc = bufs[j], bufs[j + 1].float().contiguous()
+            N, K = codes.shape
+            c2 = torch.empty_like(codes)
+            s2 = torch.empty_like(sc)
+            rc = lib.smaul_fp8_tile_layout(codes.data_ptr(), sc.data_ptr(), c2.data_ptr(), s2.data_ptr(), N, K,
+                                           torch.cuda.current_stream().cuda_stream)
+            _lib.check(rc, "fp8_tile_layout")
+            t += [c2, s2]
+        out.append(tuple(t))
+    return out
+
+
+def test_tile_layout_entry():
+    """smaul_fp8_tile_layout: codes [K/64][N][64] canonical, scales [K/64][N]."""
+    gen = torch.Generator().manual_seed(31)
+    N, K = 96, 320
+    codes = torch.randint(0, 256, (N, K), generator=gen, dtype=torch.uint8)
+    codes[0, :4] = torch.tensor([0x7F, 0xFF, 0x7E, 0xFE], dtype=torch.uint8)
+    sc = torch.rand(N, K // 64, generator=gen)
+    (c2, s2, _, _, _, _), = tiled_copies([(codes.to(DEV), sc.to(DEV)) * 3])
+    canon = torch.where((codes & 0x7F) == 0x7F, codes - 1, codes)
+    assert torch.equal(c2.cpu().reshape(-1), canon.reshape(N, K // 64, 64).permute(1, 0, 2).reshape(-1))
+    assert torch.equal(s2.cpu().reshape(-1), sc.t().reshape(-1))
+
+
+@pytest.mark.parametrize("T,d,h,E,k,dtype", [
+    (900, 512, 1280, 8, 2, torch.bfloat16),    # prefill: the LDS-DMA grouped GEMMs
+    (300, 256, 640, 8, 2, torch.float32),      # fp32 activations: the register-staged GEMMs
+    (200, 256, 640, 16, 2, torch.bfloat16),    # short segments: 32-row register-staged tiles
+    (64, 1024, 2560, 8, 2, torch.bfloat16),    # decode: streaming kernels, combine in the down tail
+    (20, 1024, 1024, 8, 2, torch.bfloat16),    # decode, the 2-block down instance
+    (40, 256, 640, 8, 2, torch.bfloat16),      # decode, the split-K fallback kernel
+])
+def test_tiled_layout_equals_reference_layout(T, d, h, E, k, dtype):
+    """The same layer through the C-ABI on FP8Linear's layout (raw codes) and on
+    the tiled copies (SMAUL_FLAG_TILED_LAYOUT): identical bits."""
+    from smaulnative_amd import _lib
+    lib = _lib.load()
+    act = 1 if dtype == torch.bfloat16 else 0
+    bm = lib.smaul_moe_block_m(T, d, h, E, k, 64, act)
+    print(f"case tiled layout T={T} d={d} h={h} E={E} k={k} {dtype} block_m={bm}", flush=True)
+    x, gw, gb, experts = make_moe(5150 + T + d, T, d, h, E, k, dtype)
+    ex = to_dev_experts(experts)
+    ref = abi_moe(x, gw, gb, experts, k, 64, _lib.FLAG_ALIGNED_CODES, ex)
+    flags = _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES | _lib.FLAG_TILED_LAYOUT
+    got = abi_moe(x, gw, gb, experts, k, 64, flags, tiled_copies(ex))
+    for a, b in zip(ref, got):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("rows,d,h", [(300, 256, 640), (4096, 512, 1280), (37, 256, 640)])
+def test_swiffn_tiled_layout_equals_reference_layout(rows, d, h):
+    from smaulnative_amd import _lib
+    lib = _lib.load()
+    print(f"case swiffn tiled layout rows={rows} d={d} h={h}", flush=True)
+    gen = torch.Generator().manual_seed(rows + d)
+    x = torch.randn(rows, d, generator=gen).to(torch.bfloat16).to(DEV)
+    ex = oracle.make_expert(d, h, gen)
+    bufs = [t.to(DEV) for t in (ex.gate_w, ex.gate_s, ex.up_w, ex.up_s, ex.down_w, ex.down_s)]
+    tiled = tiled_copies([bufs])[0]
+    outs = []
+    for b, flags in ((bufs, _lib.FLAG_ALIGNED_CODES),
+                     (tiled, _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES | _lib.FLAG_TILED_LAYOUT)):
+        out = torch.empty_like(x)
+        ws_bytes = lib.smaul_swiffn_workspace_size(rows, h, 1)
+        ws = torch.empty(max(1, ws_bytes), dtype=torch.uint8, device=DEV)
+        rc = lib.smaul_swiffn_forward(x.data_ptr(), 1, *[t.data_ptr() for t in b], out.data_ptr(), ws.data_ptr(),
+                                      ws_bytes, rows, d, h, 64, flags, torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "swiffn_forward")
+        outs.append(out.cpu())
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_tiled_layout_rejected_where_unsupported():
+    """The tiled flag needs tile 64 and widths that are multiples of 64, and
+    smaul_fp8_linear never takes it."""
+    from smaulnative_amd import _lib
+    lib = _lib.load()
+    flags = _lib.FLAG_ALIGNED_CODES | _lib.FLAG_TILED_LAYOUT
+    x = torch.zeros(4, 64, dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros(64, 64, dtype=torch.uint8, device=DEV)
+    s = torch.ones(64, 2, device=DEV)
+    y = torch.empty(4, 64, device=DEV)
+    rc = lib.smaul_fp8_linear(x.data_ptr(), 1, w.data_ptr(), s.data_ptr(), y.data_ptr(), 0, 4, 64, 64, 32, flags,
+                              torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.SMAUL_ERR_INVALID
+    ws = torch.empty(1 << 16, dtype=torch.uint8, device=DEV)
+    rc = lib.smaul_swiffn_forward(x.data_ptr(), 1, w.data_ptr(), s.data_ptr(), w.data_ptr(), s.data_ptr(),
+                                  w.data_ptr(), s.data_ptr(), y.data_ptr(), ws.data_ptr(), 1 << 16, 4, 64, 64, 32,
+                                  flags, torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.SMAUL_ERR_INVALID
+
+
 @pytest.mark.parametrize("T,d,k", [(37, 24, 3), (100, 1040, 2), (5, 2048, 4),
                                    (29, 64, 8), (50, 128, 7)])  # every slot order of the sorting network
 def test_combine_entry_direct(T, d, k):
