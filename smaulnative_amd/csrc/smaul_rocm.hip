@@ -2912,18 +2912,21 @@ __global__ void __launch_bounds__(256)
 combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
                const float* __restrict__ topw, const int32_t* __restrict__ inv,
                void* __restrict__ out, int64_t T, int d, int k) {
-  // a thread handles CW consecutive columns of one token (the widest of 32,
-  // 16, 8 that divides d; 32 for bf16 only); every row load of its k <= KM
-  // slots is issued before the first product, and registers are held for KM
-  // slots only
+  // a thread handles CW columns of one token (the widest of 32, 16, 8 that
+  // divides d; 32 for bf16 only) as NV 16-byte chunks: chunk v of the
+  // token's thread j is chunk v * cpt + j of the row, so the threads of a
+  // token read (and write) consecutive chunks with each instruction, whole
+  // cache lines.  Every row load of its k <= KM slots is issued before the
+  // first product, and registers are held for KM slots only.
   static_assert(CW == 8 || CW == 16 || (CW == 32 && BF16), "columns per thread");
   static_assert(KM == 2 || KM == 4 || KM == 8, "slots per token");
-  constexpr int NV = BF16 ? CW / 8 : CW / 4;  // 16-byte loads per row chunk
-  const int cpt = d / CW;                      // chunks per token (d % CW == 0)
+  constexpr int EPC = BF16 ? 8 : 4;            // elements per 16-byte chunk
+  constexpr int NV = CW / EPC;                 // chunks per thread
+  const int cpt = d / CW;                      // threads per token (d % CW == 0)
   const int64_t gidx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t t = gidx / cpt;
   if (t >= T) return;
-  const int c0 = (int)(gidx % cpt) * CW;
+  const int j = (int)(gidx % cpt);
   int rw[8];
   float wt[8];
   const int n = combine_slots(topi, topw, inv, t, k, rw, wt);
@@ -2931,9 +2934,9 @@ combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
 #pragma unroll
   for (int s = 0; s < KM; ++s)
     if (s < n) {
-      const char* src = (const char*)yperm + ((int64_t)rw[s] * d + c0) * (BF16 ? 2 : 4);
+      const char* src = (const char*)yperm + (int64_t)rw[s] * d * (BF16 ? 2 : 4);
 #pragma unroll
-      for (int v = 0; v < NV; ++v) yv[s][v] = ldg16(src + v * 16);
+      for (int v = 0; v < NV; ++v) yv[s][v] = ldg16(src + (int64_t)(v * cpt + j) * 16);
     }
   float acc[CW];
 #pragma unroll
@@ -2963,20 +2966,21 @@ combine_kernel(const void* __restrict__ yperm, const int64_t* __restrict__ topi,
       }
     }
   if constexpr (BF16) {
-    uint4* dst = (uint4*)((uint16_t*)out + t * d + c0);
+    uint4* dst = (uint4*)((uint16_t*)out + t * d);
 #pragma unroll
-    for (int v = 0; v < CW / 8; ++v) {
+    for (int v = 0; v < NV; ++v) {
       uint4 o;
       o.x = f2bf(acc[v * 8 + 0]) | (f2bf(acc[v * 8 + 1]) << 16);
       o.y = f2bf(acc[v * 8 + 2]) | (f2bf(acc[v * 8 + 3]) << 16);
       o.z = f2bf(acc[v * 8 + 4]) | (f2bf(acc[v * 8 + 5]) << 16);
       o.w = f2bf(acc[v * 8 + 6]) | (f2bf(acc[v * 8 + 7]) << 16);
-      dst[v] = o;
+      dst[v * cpt + j] = o;
     }
   } else {
-    float4* dst = (float4*)((float*)out + t * d + c0);
+    float4* dst = (float4*)((float*)out + t * d);
 #pragma unroll
-    for (int v = 0; v < CW / 4; ++v) dst[v] = make_float4(acc[v * 4], acc[v * 4 + 1], acc[v * 4 + 2], acc[v * 4 + 3]);
+    for (int v = 0; v < NV; ++v)
+      dst[v * cpt + j] = make_float4(acc[v * 4], acc[v * 4 + 1], acc[v * 4 + 2], acc[v * 4 + 3]);
   }
 }
 
