@@ -518,7 +518,8 @@ def test_tile_layout_entry():
     (200, 256, 640, 16, 2, torch.bfloat16),    # short segments: 32-row register-staged tiles
     (64, 1024, 2560, 8, 2, torch.bfloat16),    # decode: streaming kernels, combine in the down tail
     (20, 1024, 1024, 8, 2, torch.bfloat16),    # decode, the 2-block down instance
-    (40, 256, 640, 8, 2, torch.bfloat16),      # decode, the split-K fallback kernel
+    (40, 256, 640, 8, 2, torch.bfloat16),      # decode, 2-wave streaming instances
+    (40, 1152, 1152, 4, 2, torch.bfloat16),    # decode, the split-K fallback kernel (18 K blocks)
 ])
 def test_tiled_layout_equals_reference_layout(T, d, h, E, k, dtype):
     """The same layer through the C-ABI on FP8Linear's layout (raw codes) and on
