@@ -2041,21 +2041,47 @@ __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, con
 
   // the segment's activation rows, this wave's K slice
   uint4 a0[NRT][KBW], a1[NRT][KBW];
+  // this wave's 2 KB tile for turning whole-line row loads into the MFMA
+  // operand layout: 16 rows x 8 16-byte slots, slot c of row r at c ^ (r >> 1)
+  // (conflict-free for the writes, 8 lanes per row, and for the reads, one
+  // row per lane of each 16)
+  __shared__ uint4 s_rows[DS_WMAX][16 * 8];
   auto load_a = [&](int j) {
     int e, r0, nr;
     ds_locate(sg, j, e, r0, nr);
     if (nr > 0) {  // uniform (always true unless a caller asks for empty segments)
+      // Whole 128-byte lines: a0 holds row rt*16 + (lane >> 3), a1 row
+      // rt*16 + 8 + (lane >> 3), 16-byte chunk lane & 7 of each K block (the
+      // MFMA layout, row lane & 15 and chunks 2g / 2g+1, reads each line in
+      // halves: twice the requests).
+      const int wr = lane >> 3, wc = lane & 7;
 #pragma unroll
       for (int rt = 0; rt < NRT; ++rt) {
-        const int64_t lr = r0 + min(rt * 16 + (lane & 15), nr - 1);
-        const int64_t xr = SWIGLU ? (int64_t)ridx[lr] : lr;
-        const uint16_t* ar = (const uint16_t*)p.x + xr * p.ldx + kb0 * 64 + kq;
+        const int64_t lr0 = r0 + min(rt * 16 + wr, nr - 1);
+        const int64_t lr1 = r0 + min(rt * 16 + 8 + wr, nr - 1);
+        const int64_t xr0 = SWIGLU ? (int64_t)ridx[lr0] : lr0;
+        const int64_t xr1 = SWIGLU ? (int64_t)ridx[lr1] : lr1;
+        const uint16_t* ar0 = (const uint16_t*)p.x + xr0 * p.ldx + kb0 * 64 + wc * 8;
+        const uint16_t* ar1 = (const uint16_t*)p.x + xr1 * p.ldx + kb0 * 64 + wc * 8;
 #pragma unroll
         for (int b = 0; b < KBW; ++b) {
-          a0[rt][b] = ldg16(ar + b * 64);
-          a1[rt][b] = ldg16(ar + b * 64 + 8);
+          a0[rt][b] = ldg16(ar0 + b * 64);
+          a1[rt][b] = ldg16(ar1 + b * 64);
         }
       }
+      // to the MFMA layout through the tile (one wave's LDS operations run in
+      // order, so each read sees the writes before it)
+      uint4* tile = s_rows[ks];
+      const int rr = lane & 15, g = lane >> 4;
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int b = 0; b < KBW; ++b) {
+          tile[wr * 8 + (wc ^ (wr >> 1))] = a0[rt][b];
+          tile[(8 + wr) * 8 + (wc ^ ((8 + wr) >> 1))] = a1[rt][b];
+          a0[rt][b] = tile[rr * 8 + ((2 * g) ^ (rr >> 1))];
+          a1[rt][b] = tile[rr * 8 + ((2 * g + 1) ^ (rr >> 1))];
+        }
     } else {
 #pragma unroll
       for (int rt = 0; rt < NRT; ++rt)
