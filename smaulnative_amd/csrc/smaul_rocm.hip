@@ -2361,8 +2361,13 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd, CnrArgs cr) {
   }
   const int32_t* ridx = FUSED ? (const int32_t*)s_perm : p.row_idx;
   const int64_t U = (int64_t)sg.total * ctn;
-  const int u0 = (int)((int64_t)blockIdx.x * U / gridDim.x);
-  const int u1 = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
+  // Workgroup b runs on XCD b % 8: the 8 XCDs take contiguous eighths of the
+  // unit list, so a segment's activation rows are read into one or two L2s
+  // rather than all eight.
+  const int G = (int)gridDim.x;
+  const int gx = G % 8 == 0 ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+  const int u0 = (int)((int64_t)gx * U / G);
+  const int u1 = (int)((int64_t)(gx + 1) * U / G);
   constexpr bool COH = TAIL != TAIL_NONE;
   static_assert(!COH || !SWIGLU, "the combine follows the down projection");
   if constexpr (!COH) {
