@@ -2156,20 +2156,19 @@ __device__ __forceinline__ void ds_body(const GemmArgs& p, const DsSegs& sg, con
         }
       }
     }
-    // partials: red[buf][ks][h][rt][r][lane]
+    // partials: red[buf][ks][h][rt][lane][r], one 16-byte write per (h, rt)
     float* rb = red + buf * per_buf;
 #pragma unroll
     for (int h = 0; h < NH; ++h)
 #pragma unroll
       for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) rb[((ks * NH + h) * NRT + rt) * 256 + r * 64 + lane] = acc[h][rt][r];
+        *(f32x4_t*)&rb[((ks * NH + h) * NRT + rt) * 256 + lane * 4] = acc[h][rt];
     __syncthreads();
     int e, r0, nr;
     ds_locate(sg, j, e, r0, nr);
     const int ct = u - j * ctn;
     for (int q = threadIdx.x; q < NRT * 256; q += nthr) {
-      const int rt = q >> 8, r = (q >> 6) & 3, ln = q & 63;
+      const int rt = q >> 8, ln = (q >> 2) & 63, r = q & 3;
       const int lr = rt * 16 + (ln >> 4) * 4 + r;
       // all partials are read before the first add (independent LDS reads in
       // flight together), then summed in K-split order
