@@ -561,6 +561,31 @@ def test_swiffn_tiled_layout_equals_reference_layout(rows, d, h):
     assert torch.equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("d,h,tile,tiled", [(256, 640, 64, True), (256, 640, 32, False), (208, 640, 64, False)])
+def test_expert_cache_layout_choice(d, h, tile, tiled):
+    """RocmBackend's expert cache writes the tiled layout (and says so in its
+    flags) only for tile 64 with d, h multiples of 64; the tiled copies hold
+    what smaul_fp8_tile_layout writes, and the layer matches the oracle either
+    way."""
+    from smaulnative_amd import _lib
+    print(f"case expert cache d={d} h={h} tile={tile}", flush=True)
+    x, gw, gb, experts = make_moe(6060 + d + tile, 300, d, h, 4, 2, tile=tile)
+    ex = to_dev_experts(experts)
+    ent = be()._expert_entry(ex, ex[0][0].device, d, h, tile)
+    assert bool(ent["flags"] & _lib.FLAG_TILED_LAYOUT) == tiled
+    assert ent["flags"] & _lib.FLAG_CANONICAL_CODES and ent["flags"] & _lib.FLAG_ALIGNED_CODES
+    if tiled:
+        want = tiled_copies(ex)
+        for e in range(len(ex)):
+            for j in range(6):
+                got = ent["copies"][e * 6 + j]
+                assert got is not None and torch.equal(got.reshape(-1), want[e][j].reshape(-1))
+    ref = oracle.moe_forward(x, gw, gb, experts, 2, tile)
+    out, prob, topi, counts = gpu_moe(x, gw, gb, experts, 2, tile)
+    assert torch.equal(topi.reshape(-1, 2), ref.topi.reshape(-1, 2))
+    assert rel_l2(out.float(), ref.out.float()) < 2e-3
+
+
 def test_tiled_layout_rejected_where_unsupported():
     """The tiled flag needs tile 64 and widths that are multiples of 64, and
     smaul_fp8_linear never takes it."""
