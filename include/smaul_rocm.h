@@ -89,7 +89,7 @@ int smaul_fp8_canonicalize(const uint8_t* codes, uint8_t* out, int64_t n, hipStr
  * of scales instead of one line per column.  No counterpart in the
  * reference: it is the device repack step of a caller that keeps expert
  * weights resident (RocmBackend's expert cache).  K % 64 == 0; code buffers
- * 16-byte aligned; not in place.
+ * 16-byte aligned; the outputs must not overlap the inputs.
  */
 int smaul_fp8_tile_layout(const uint8_t* codes, const float* scales, uint8_t* codes_out, float* scales_out,
                           int64_t N, int64_t K, hipStream_t stream);

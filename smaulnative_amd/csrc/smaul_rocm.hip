@@ -4588,8 +4588,14 @@ int smaul_fp8_tile_layout(const uint8_t* codes, const float* scales, uint8_t* co
   if (!codes || !scales || !codes_out || !scales_out) return fail(SMAUL_ERR_INVALID, "tile_layout: null pointer");
   if (!aligned16(codes) || !aligned16(codes_out))
     return fail(SMAUL_ERR_INVALID, "tile_layout: code buffers must be 16-byte aligned");
-  if (codes == codes_out || scales == scales_out) return fail(SMAUL_ERR_INVALID, "tile_layout: not in place");
   const int64_t nv = N * K / 16, ns = N * (K / 64);
+  // the copy reads other columns than it writes: overlapping buffers would race
+  auto overlap = [](const void* a, const void* b, int64_t bytes) {
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return x < y + (uintptr_t)bytes && y < x + (uintptr_t)bytes;
+  };
+  if (overlap(codes, codes_out, N * K) || overlap(scales, scales_out, ns * 4))
+    return fail(SMAUL_ERR_INVALID, "tile_layout: the output buffers must not overlap the inputs");
   const unsigned bc = (unsigned)std::min<int64_t>(8192, std::max<int64_t>(1, (nv + 255) / 256));
   const unsigned bs = (unsigned)std::min<int64_t>(8192, std::max<int64_t>(1, (ns + 255) / 256));
   hipLaunchKernelGGL(tile_codes_kernel, dim3(bc), dim3(256), 0, stream, codes, codes_out, N, K);

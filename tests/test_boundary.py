@@ -70,6 +70,15 @@ def test_library_validates_without_touching_the_gpu():
     rc = lib.smaul_moe_forward_chain(*head, 0, 4, 64, 128, 8, 2, 64, 0, None, 1e-6, 16, 0,
                                      16, None, 65, 2, None, None, None, None)
     assert rc == _lib.SMAUL_ERR_INVALID and "router" in _lib.last_error()
+    # the tiled relayout: K % 64, and outputs that overlap their inputs (the
+    # addresses are never dereferenced: the checks come before any launch)
+    a, b = 1 << 32, 1 << 33
+    assert lib.smaul_fp8_tile_layout(a, b, a + (1 << 20), b + (1 << 20), 4, 96, None) == _lib.SMAUL_ERR_INVALID
+    assert "multiple of 64" in _lib.last_error()
+    N, K = 8, 128
+    for co, so in ((a, b + (1 << 20)), (a + 512, b + (1 << 20)), (a + (1 << 20), b + 4)):
+        rc = lib.smaul_fp8_tile_layout(a, b, co, so, N, K, None)
+        assert rc == _lib.SMAUL_ERR_INVALID and "overlap" in _lib.last_error()
 
 
 def _host_topk(vals, k):

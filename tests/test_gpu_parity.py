@@ -510,6 +510,21 @@ def test_tile_layout_entry():
     canon = torch.where((codes & 0x7F) == 0x7F, codes - 1, codes)
     assert torch.equal(c2.cpu().reshape(-1), canon.reshape(N, K // 64, 64).permute(1, 0, 2).reshape(-1))
     assert torch.equal(s2.cpu().reshape(-1), sc.t().reshape(-1))
+    # input and output in adjacent halves of one allocation: accepted (only
+    # overlapping ranges are rejected), same result
+    from smaulnative_amd import _lib
+    lib = _lib.load()
+    nc, ns = N * K, N * (K // 64)
+    cb = torch.zeros(2 * nc, dtype=torch.uint8, device=DEV)
+    sb = torch.zeros(2 * ns, dtype=torch.float32, device=DEV)
+    cb[:nc] = codes.reshape(-1).to(DEV)
+    sb[:ns] = sc.reshape(-1).to(DEV)
+    rc = lib.smaul_fp8_tile_layout(cb.data_ptr(), sb.data_ptr(), cb.data_ptr() + nc, sb.data_ptr() + ns * 4, N, K,
+                                   torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "fp8_tile_layout")
+    torch.cuda.synchronize()
+    assert torch.equal(cb[nc:].cpu(), c2.cpu().reshape(-1)) and torch.equal(sb[ns:].cpu(), s2.cpu().reshape(-1))
+    assert torch.equal(cb[:nc].cpu(), codes.reshape(-1))  # the input is left as it was
 
 
 @pytest.mark.parametrize("T,d,h,E,k,dtype", [
