@@ -310,6 +310,31 @@ int smaul_moe_forward_chain(const void* x, int act_dtype, const float* gate_w, c
                             hipStream_t stream);
 
 /*
+ * Give-ups of the fused decode combine's bounded wait.  In the decode regime
+ * the first workgroups of the down-projection kernel to finish wait (a
+ * bounded poll) for the others before they combine.  If that wait gives up
+ * (another process holding the compute units for tens of milliseconds), the
+ * call still returns SMAUL_OK, but every token the waiting workgroup owns is
+ * poisoned instead of combined: out (and norm_out) rows NaN, and for a next
+ * router next_prob / next_topw NaN and next_topi -1.  Each give-up also adds
+ * one to a per-device counter, which this entry reads: it enqueues on
+ * `stream` a copy of the current device's count into *out (device int32)
+ * and, with reset != 0, subtracts what it copied.  No sync.  No counterpart
+ * in the reference (its combine, model.py:582-585, has no wait); callers
+ * that need to know a decode call completed check *out == 0.
+ */
+int smaul_wait_timeouts(int32_t* out, int reset, hipStream_t stream);
+
+/*
+ * Test hook for the wait above (no counterpart in the reference): later
+ * decode-regime calls from any thread wait for `extra_arrivals` more
+ * workgroups than the grid holds and poll at most `spin_limit` times, so a
+ * test can make every wait give up while every kernel still exits normally.
+ * (0, 1 << 20) restores the defaults.  Not for use beside other work.
+ */
+int smaul_debug_tail_wait(int extra_arrivals, int spin_limit);
+
+/*
  * Linear-attention recurrence of SmaulLinear, per (batch, head):
  *   kn_t = k_t / max(||k_t||, 1e-6),  S_t = S_{t-1} + kn_t (x) v_t,
  *   z_t = z_{t-1} + kn_t,  y_t = (q_t @ S_t) / max(q_t . z_t, eps).
@@ -357,8 +382,9 @@ int smaul_fp8_quantize_tiles(const float* w, int64_t out_f, int64_t in_f, int64_
  * decode(w, s), fp32.  Replaces the reference's native fp8_backward_input
  * (kernel/fp8_cpu.cpp:167-259; backend entry kernel/compute.py:145-153).
  * g fp32 [rows, out_f] row-major; w uint8 [out_f, in_f]; s fp32
- * [out_f, ceil(in_f/tile)]; any tile > 0.  The sum runs in another fp32 order
- * than the reference's, so results agree to fp32 rounding, not bitwise.
+ * [out_f, ceil(in_f/tile)]; any tile > 0; in_f, out_f >= 0 (out_f == 0
+ * writes zeros).  The sum runs in another fp32 order than the reference's, so
+ * results agree to fp32 rounding, not bitwise.
  */
 int smaul_fp8_backward_input(const float* g, const uint8_t* w, const float* s, float* dx, int64_t rows,
                              int64_t in_f, int64_t out_f, int64_t tile, hipStream_t stream);

@@ -60,6 +60,8 @@ SIGNATURES = {
     "smaul_attn_step": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_float, _P]),
     "smaul_fp8_quantize_tiles": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P]),
     "smaul_fp8_backward_input": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    "smaul_wait_timeouts": (_I, [_P, _I, _P]),
+    "smaul_debug_tail_wait": (_I, [_I, _I]),
     "smaul_selftest_topk": (_I, [_P, _I64, _I64, _P]),
 }
 

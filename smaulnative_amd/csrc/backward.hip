@@ -113,11 +113,13 @@ extern "C" {
 
 int smaul_fp8_backward_input(const float* g, const uint8_t* w, const float* s, float* dx, int64_t rows,
                              int64_t in_f, int64_t out_f, int64_t tile, hipStream_t stream) {
-  if (tile <= 0 || in_f <= 0 || out_f <= 0 || rows < 0)
-    return fail(SMAUL_ERR_INVALID, "fp8_backward_input: tile/in_f/out_f must be positive, got %lld/%lld/%lld",
+  // in_f / out_f may be 0, as in the reference (fp8_cpu.cpp:227-228): no
+  // columns, or an empty sum (dx all zeros, g / w / s not read)
+  if (tile <= 0 || in_f < 0 || out_f < 0 || rows < 0)
+    return fail(SMAUL_ERR_INVALID, "fp8_backward_input: need tile > 0 and in_f, out_f, rows >= 0, got %lld/%lld/%lld",
                 (long long)tile, (long long)in_f, (long long)out_f);
-  if (rows == 0) return SMAUL_OK;
-  if (!g || !w || !s || !dx) return fail(SMAUL_ERR_INVALID, "fp8_backward_input: null pointer");
+  if (rows == 0 || in_f == 0) return SMAUL_OK;
+  if (!dx || (out_f > 0 && (!g || !w || !s))) return fail(SMAUL_ERR_INVALID, "fp8_backward_input: null pointer");
   const int64_t gx = (in_f + BW_T - 1) / BW_T, gy = (rows + BW_T - 1) / BW_T;
   if (gx > 2147483647LL || gy > 65535) return fail(SMAUL_ERR_UNSUPPORTED, "fp8_backward_input: grid too large");
   hipLaunchKernelGGL(fp8_backward_input_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, stream, g, w, s, dx,

@@ -31,6 +31,7 @@
 #include <stdarg.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <cmath>
 #include <stdlib.h>
@@ -2226,8 +2227,8 @@ struct DsDispatch {
 };
 
 // The combine + norm + next router fused into the tail of the decode down
-// kernel (CNR): the inputs of combine_norm_route_kernel, and the sync words
-// [arrivals, spin timeouts], cleared by the gate/up kernel of the same layer.
+// kernel (CNR): the inputs of combine_norm_route_kernel, and the arrival
+// count (sync[0]), cleared by the gate/up kernel of the same layer.
 struct CnrArgs {
   const int64_t* topi;
   const float* topw;
@@ -2244,11 +2245,21 @@ struct CnrArgs {
   int nE, nk;
   int32_t* sync;
   int64_t ybytes;
+  // the arrival count the combining workgroups wait for is gridDim.x +
+  // wait_extra (0 in use; smaul_debug_tail_wait raises it so that a test can
+  // make the wait give up), polled at most spin_limit times
+  int wait_extra;
+  int spin_limit;
 };
 constexpr int CNR_TAIL_TOK = 8;         // tokens per combining workgroup (one per wave)
 template <int NCH, int EMAX, bool EXACT, int KSW, int TOK, bool COH>
 struct CnrBlock;
 constexpr int CNR_SPIN_LIMIT = 1 << 20;  // polls of the arrival count before giving up
+
+// Bounded waits that gave up, per device since the library was loaded (or the
+// last reset by smaul_wait_timeouts).  Incremented only on a give-up, so the
+// normal path never touches it.
+__device__ int32_t g_wait_timeouts = 0;
 
 // The dispatch of the fused gate/up kernel (FUSED below): wave 0 ranks the
 // T <= 64 tokens per expert into s_perm / s_off (LDS), workgroup 0 also
@@ -2273,23 +2284,61 @@ __device__ __forceinline__ void ds_fused_dispatch(const GemmArgs& p, const DsDis
     }
     if (lane == 0) s_off[p.E] = off;
     if (blockIdx.x == 0) dispatch_one_wave(ti, tw, valid, lane, dd.o, p.E, dd.k);
-    if (blockIdx.x == 0 && lane < 2 && dd.sync) dd.sync[lane] = 0;
+    if (blockIdx.x == 0 && lane == 0 && dd.sync) dd.sync[0] = 0;
   }
   __syncthreads();
   ds_finish(lane < p.E ? s_off[lane] : 0, lane < p.E ? s_off[lane + 1] : 0, lane, sg);
 }
 
-// Bounded wait of thread 0 until *ctr reaches target (device scope); past
-// CNR_SPIN_LIMIT polls it counts a timeout in *err and gives up.
-__device__ __forceinline__ void ds_spin(const int32_t* ctr, int target, int32_t* err) {
+// Bounded wait of the workgroup until *ctr reaches target (device scope),
+// polled by thread 0 at most `limit` times.  Returns true when the target was
+// reached; false when the wait gave up, which is counted in g_wait_timeouts.
+// Ends with a workgroup barrier.
+__device__ __forceinline__ bool ds_wait_all(const int32_t* ctr, int target, int limit) {
+  __shared__ int s_reached;
   if (threadIdx.x == 0) {
-    int spins = 0;
+    int spins = 0, reached = 1;
     while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      if (++spins > CNR_SPIN_LIMIT) {
-        __hip_atomic_fetch_add(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (++spins > limit) {
+        __hip_atomic_fetch_add(&g_wait_timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        reached = 0;
         break;
       }
       __builtin_amdgcn_s_sleep(2);
+    }
+    s_reached = reached;
+  }
+  __syncthreads();
+  return s_reached != 0;
+}
+
+// A combining workgroup whose wait gave up must not combine rows that other
+// workgroups may not have written: wave w instead writes NaN over token t0 +
+// w's out and norm_out rows (bf16, d <= 1024) and, for a next router, NaN
+// prob / topw and topi -1 (an id that no dispatch takes).
+__device__ __forceinline__ void cnr_poison(const CnrArgs& cr, int64_t t0, bool route) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = t0 + (threadIdx.x >> 6);
+  if (t >= cr.T) return;
+  const uint32_t nan2 = 0x7fc07fc0u;  // two bf16 NaNs
+  const uint4 nan8 = make_uint4(nan2, nan2, nan2, nan2);
+  const int nch = cr.d / 16;
+  for (int c = lane; c < nch; c += 64) {
+    uint4* o = (uint4*)((char*)cr.out + (t * cr.d + c * 16) * 2);
+    o[0] = nan8;
+    o[1] = nan8;
+    if (cr.norm_out) {
+      uint4* n = (uint4*)((char*)cr.norm_out + (t * cr.d + c * 16) * 2);
+      n[0] = nan8;
+      n[1] = nan8;
+    }
+  }
+  if (route) {
+    const float qnan = __uint_as_float(0x7fc00000u);
+    if (lane < cr.nE) cr.no.prob[t * cr.nE + lane] = qnan;
+    if (lane < cr.nk) {
+      cr.no.topi[t * cr.nk + lane] = -1;
+      cr.no.topw[t * cr.nk + lane] = qnan;
     }
   }
 }
@@ -2298,9 +2347,10 @@ __device__ __forceinline__ void ds_spin(const int32_t* ctr, int target, int32_t*
 // its own device-scope output stores, count itself in *arr; the first
 // ceil(T / 8) to arrive prefetch what the combine needs besides y, wait for
 // all gridDim.x arrivals and run the combine + norm + next router of 8
-// tokens each.  Every workgroup returns from it.
+// tokens each (or, when the wait gives up, poison those tokens).  Every
+// workgroup returns from it.
 template <int CEMAX, bool CEXACT>
-__device__ __forceinline__ void cnr_tail(const CnrArgs& cr, const void* y, int32_t* arr, int32_t* err) {
+__device__ __forceinline__ void cnr_tail(const CnrArgs& cr, const void* y, int32_t* arr) {
   __shared__ int s_arrival;
   __builtin_amdgcn_s_waitcnt(0);  // this wave's output stores have completed
   __syncthreads();
@@ -2314,14 +2364,16 @@ __device__ __forceinline__ void cnr_tail(const CnrArgs& cr, const void* y, int32
   b.prefetch_slots(cr.topi, cr.topw, cr.inv, cr.weight, cr.T, cr.d, cr.k, t0);
   b.prefetch_router(cr.ngw, cr.ngb, cr.nE, cr.d);
   b.prepare_router(cr.nE, cr.d);
-  ds_spin(arr, (int)gridDim.x, err);
-  __syncthreads();
+  if (!ds_wait_all(arr, (int)gridDim.x + cr.wait_extra, cr.spin_limit)) {  // uniform
+    cnr_poison(cr, t0, true);
+    return;
+  }
   b.finish(y, cr.ybytes, cr.out, cr.weight, cr.eps, cr.norm_out, cr.T, cr.d, cr.ngw, cr.ngb, cr.no, cr.nE, cr.nk, t0);
 }
 
 // The same tail without a next router (defined after CombineNormRow)
 template <bool NORM>
-__device__ void cn_tail(const CnrArgs& cr, const void* y, int32_t* arr, int32_t* err);
+__device__ void cn_tail(const CnrArgs& cr, const void* y, int32_t* arr);
 
 // FUSED (gate/up only): every workgroup ranks the T <= 64 tokens per expert
 // itself into LDS (one wave, ballot ranks in token order, the same rule as
@@ -2334,7 +2386,9 @@ __device__ void cn_tail(const CnrArgs& cr, const void* y, int32_t* arr, int32_t*
 // own device-scope output stores, then counts itself in sync[0]; the first
 // ceil(T / 8) workgroups to arrive load what the combine needs besides the
 // outputs (slots, router weights), wait (a bounded poll: the others are
-// already running) until all have arrived, and each then combines 8 tokens,
+// already running; a wait that gives up poisons its tokens, cnr_poison, and
+// counts itself in g_wait_timeouts) until all have arrived, and each then
+// combines 8 tokens,
 // reading the outputs device-coherently: TAIL_CNR also normalises them and
 // runs the next layer's router (replacing the combine_norm_route_kernel
 // launch, with the same arithmetic: CnrBlock), TAIL_CN normalises
@@ -2377,8 +2431,8 @@ decode_stream_kernel(GemmArgs p, int nw, DsDispatch dd, CnrArgs cr) {
     if (__ballot(sg.rows > 16) != 0) ds_body<SWIGLU, CANON, KBW, 2, COH>(p, sg, ridx, u0, u1, ctn, red, nw);
     else ds_body<SWIGLU, CANON, KBW, 1, COH>(p, sg, ridx, u0, u1, ctn, red, nw);
   }
-  if constexpr (TAIL == TAIL_CNR) cnr_tail<CEMAX, CEXACT>(cr, p.y, cr.sync, cr.sync + 1);
-  if constexpr (TAIL == TAIL_CN || TAIL == TAIL_C) cn_tail<TAIL == TAIL_CN>(cr, p.y, cr.sync, cr.sync + 1);
+  if constexpr (TAIL == TAIL_CNR) cnr_tail<CEMAX, CEXACT>(cr, p.y, cr.sync);
+  if constexpr (TAIL == TAIL_CN || TAIL == TAIL_C) cn_tail<TAIL == TAIL_CN>(cr, p.y, cr.sync);
 }
 
 // K blocks per wave of the streaming decode kernel for K/64 = nkb blocks
@@ -3377,7 +3431,7 @@ struct CombineNormRow {
 // one wave per token, with CombineNormRow (the arithmetic of combine_kernel,
 // and with NORM of combine_norm_kernel), reading y device-coherently.
 template <bool NORM>
-__device__ void cn_tail(const CnrArgs& cr, const void* y, int32_t* arr, int32_t* err) {
+__device__ void cn_tail(const CnrArgs& cr, const void* y, int32_t* arr) {
   __shared__ int s_arrival;
   __builtin_amdgcn_s_waitcnt(0);  // this wave's output stores have completed
   __syncthreads();
@@ -3394,8 +3448,10 @@ __device__ void cn_tail(const CnrArgs& cr, const void* y, int32_t* arr, int32_t*
     cn.slots(cr.topi, cr.topw, cr.inv, t, cr.k);
     if (NORM) cn.load_weight(cr.weight, cr.d, lane);
   }
-  ds_spin(arr, (int)gridDim.x, err);
-  __syncthreads();
+  if (!ds_wait_all(arr, (int)gridDim.x + cr.wait_extra, cr.spin_limit)) {  // uniform
+    cnr_poison(cr, (int64_t)a * CNR_TAIL_TOK, false);
+    return;
+  }
   if (mine) {
     cn.template combine<true, NORM>(y, cr.eps, cr.d, lane, cr.ybytes);
     if constexpr (NORM) {
@@ -4320,6 +4376,21 @@ static int finish_combine(const void* yperm, int act_dtype, const int64_t* topi,
   return smaul_rms_norm(out, act_dtype, nrm->weight, nrm->out, T, d, nrm->eps, stream);
 }
 
+// The fused decode tail's wait: arrivals beyond the grid and the poll limit
+// (smaul_debug_tail_wait; 0 and CNR_SPIN_LIMIT in use)
+static std::atomic<int> g_tail_wait_extra{0};
+static std::atomic<int> g_tail_spin_limit{CNR_SPIN_LIMIT};
+static void tail_wait_settings(int& extra, int& limit) {
+  extra = g_tail_wait_extra.load(std::memory_order_relaxed);
+  limit = g_tail_spin_limit.load(std::memory_order_relaxed);
+}
+
+__global__ void wait_timeouts_kernel(int32_t* out, int reset) {
+  const int32_t v = __hip_atomic_load(&g_wait_timeouts, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  *out = v;
+  if (reset) __hip_atomic_fetch_sub(&g_wait_timeouts, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
                             const uint8_t* const* gate_w8, const float* const* gate_s,
                             const uint8_t* const* up_w8, const float* const* up_s,
@@ -4451,6 +4522,7 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
                    nrm ? nrm->out : nullptr, T, (int)d, (int)k, nullptr, nullptr, RouteOut{}, 0, 0, sync,
                    R * d * el};
     }
+    tail_wait_settings(cr.wait_extra, cr.spin_limit);
     DsDispatch dd{topi, topw, od, (int)T, (int)k, (cnr || cn) ? sync : nullptr};
     rc = canon ? launch_decode_stream<true, true>(a, &dd, stream) : launch_decode_stream<true, false>(a, &dd, stream);
     if (rc) return rc;
@@ -4566,6 +4638,19 @@ int smaul_moe_forward_chain(const void* x, int act_dtype, const float* gate_w, c
   return moe_forward_impl(x, act_dtype, gate_w, gate_b, gate_w8, gate_s, up_w8, up_s, down_w8, down_s, out, prob,
                           topi, topw, counts, workspace, workspace_bytes, T, d, h, E, k, tile, flags, &nrm,
                           routed != 0, next_gate_w ? &nr : nullptr, stream);
+}
+
+int smaul_wait_timeouts(int32_t* out, int reset, hipStream_t stream) {
+  if (!out) return fail(SMAUL_ERR_INVALID, "wait_timeouts: null out");
+  hipLaunchKernelGGL(wait_timeouts_kernel, dim3(1), dim3(1), 0, stream, out, reset);
+  return check_launch("wait_timeouts_kernel");
+}
+
+int smaul_debug_tail_wait(int extra_arrivals, int spin_limit) {
+  if (extra_arrivals < 0 || spin_limit < 1) return fail(SMAUL_ERR_INVALID, "debug_tail_wait: need extra >= 0, limit >= 1");
+  g_tail_wait_extra.store(extra_arrivals, std::memory_order_relaxed);
+  g_tail_spin_limit.store(spin_limit, std::memory_order_relaxed);
+  return SMAUL_OK;
 }
 
 int smaul_fp8_canonicalize(const uint8_t* codes, uint8_t* out, int64_t n, hipStream_t stream) {

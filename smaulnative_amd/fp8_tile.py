@@ -24,6 +24,7 @@ selects the torch path (kernel/compute.py:246-263).
 from __future__ import annotations
 
 import math
+import threading
 import warnings
 
 import torch
@@ -98,6 +99,7 @@ def decode_block(w, s, o0, o1, in_f, tile=TILE, dtype=torch.float32):
 GRAD_DTYPE = torch.bfloat16   # storage of the accumulated weight gradient (kernel/fp8_tile.py:26)
 _GRAD_ROWS = 64               # weight-gradient rows added (and rounded) per step
 _REQUANT_ELEMS = 1 << 24      # fp32 values decoded at once by requant (64 MB)
+_GW_LOCK = threading.Lock()   # one for every module: it also keeps modules picklable
 
 
 class _FP8Matmul(torch.autograd.Function):
@@ -127,11 +129,14 @@ class _FP8Matmul(torch.autograd.Function):
             # reference's optimizers read and clear (kernel/fp8_tile.py:172-197):
             # each 64-row block of g^T x is formed in fp32 and rounded once
             xr = x.reshape(-1, in_f).float()
-            if m._gw is None or m._gw.device != g.device:
-                m._gw = torch.zeros(out_f, in_f, dtype=GRAD_DTYPE, device=g.device)
-            for o0 in range(0, out_f, _GRAD_ROWS):
-                o1 = min(o0 + _GRAD_ROWS, out_f)
-                m._gw[o0:o1].add_(g[:, o0:o1].t() @ xr)
+            with _GW_LOCK:  # backward passes on several threads add to one _gw
+                if m._gw is None:
+                    m._gw = torch.zeros(out_f, in_f, dtype=GRAD_DTYPE, device=g.device)
+                elif m._gw.device != g.device:  # the module moved: keep what it accumulated
+                    m._gw = m._gw.to(g.device)
+                for o0 in range(0, out_f, _GRAD_ROWS):
+                    o1 = min(o0 + _GRAD_ROWS, out_f)
+                    m._gw[o0:o1].add_(g[:, o0:o1].t() @ xr)
         return gx, None, None, None, None, None, None
 
 

@@ -7,10 +7,11 @@ diagnostic attributes read by training logs and retention reports:
 
 The whole layer (router, dispatch, the expert SwiGLU GEMMs, combine) is one
 call to the backend's ``moe_forward``; the per-expert Python loop with a host
-sync per expert (model.py:574-582) is gone.  In training (grad enabled and
-the module in train mode) the layer runs as device torch ops around the
-experts' FP8Linear kernels instead, so autograd reaches the router and the
-experts' weight gradients (``_forward_train``).  ``expert_token_counts`` and
+sync per expert (model.py:574-582) is gone.  When autograd must record the
+layer (grad mode on and the input or a parameter requiring grad, in train and
+eval mode alike) it runs as device torch ops around the experts' FP8Linear
+kernels instead, so gradients reach the input, the router and the experts'
+weight gradients (``_forward_train``).  ``expert_token_counts`` and
 ``last_executed`` are materialised from the device counts only when read, so
 a decode step does not force a device->host sync per layer.
 
@@ -53,6 +54,17 @@ class MoEConfig:
                              f"num_experts ({self.num_experts})")
 
 
+def _needs_grad(module: nn.Module, x: torch.Tensor) -> bool:
+    """Whether the forward must record autograd: grad mode on and x or a
+    parameter of ``module`` requiring grad, in train and eval mode alike (as
+    with the reference's autograd function, kernel/fp8_tile.py:162-170; the
+    module's training flag only decides whether FP8Linear accumulates ``_gw``).
+    The fused device entries keep no activations, so they run only otherwise."""
+    if not torch.is_grad_enabled():
+        return False
+    return x.requires_grad or any(p.requires_grad for p in module.parameters())
+
+
 class SwiFFN(nn.Module):
     """model.py:282-290: down((silu(gate(x).float()) * up(x).float()).to(x.dtype))."""
 
@@ -67,7 +79,7 @@ class SwiFFN(nn.Module):
 
     def forward(self, x):
         be = get_backend()
-        if hasattr(be, "swiffn_forward") and not (torch.is_grad_enabled() and self.training):
+        if hasattr(be, "swiffn_forward") and not _needs_grad(self, x):
             xf = x if x.is_floating_point() else x.float()
             return be.swiffn_forward(xf, self.buffers6(), self.gate.tile)
         odt = x.dtype if x.is_floating_point() else torch.float32
@@ -131,8 +143,7 @@ class SwiFFN_MoE(nn.Module):
         be = get_backend()
         if not hasattr(be, "moe_forward"):
             raise RuntimeError(f"compute backend {be.name!r} has no moe_forward entry")
-        if torch.is_grad_enabled() and (x.requires_grad or self.gate.weight.requires_grad) \
-                and self.training:
+        if _needs_grad(self, x):
             return self._forward_train(x)
         experts = [ex.buffers6() for ex in self.experts]
         out, prob, topi, counts = be.moe_forward(x, self.gate.weight, self.gate.bias, experts,

@@ -43,10 +43,16 @@ def _stream_handle(device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _call_weak(method_ref, *args):
-    m = method_ref()
-    if m is not None:
-        m(*args)
+class _CacheEntry(dict):
+    """One expert-cache entry (a dict that can be weakly referenced)."""
+
+
+def _drop_entry(backend_ref, key, entry_ref):
+    """Finalizer of a source buffer: evict its cache entry if both still live.
+    It holds only weak references, so it keeps neither alive."""
+    be, ent = backend_ref(), entry_ref()
+    if be is not None and ent is not None:
+        be._evict(key, ent)
 
 
 def _need_device(name: str, *tensors):
@@ -300,7 +306,9 @@ class RocmBackend:
         ``copy_``), the copies are refreshed in place on the current stream,
         so the table -- and any HIP graph that captured it -- keeps pointing
         at valid, current data.  When any of the buffers is freed, its entry
-        (and the copies it owns, one byte per weight) is dropped at once.
+        (and the copies it owns, one byte per weight) is dropped at once; so
+        is an entry whose buffers got new storage (a new key for the same
+        tensors).  The finalizers hold only weak references to the entry.
         """
         lib = _lib.load()
         flat = []
@@ -334,8 +342,8 @@ class RocmBackend:
                   (torch.empty(t.numel(), dtype=torch.float32, device=device) if tiled else None)
                   for i, t in enumerate(flat)]
         flags = _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES | (_lib.FLAG_TILED_LAYOUT if tiled else 0)
-        ent = {"copies": copies, "refs": [weakref.ref(t) for t in flat], "versions": versions, "tiled": tiled,
-               "flags": flags}
+        ent = _CacheEntry(copies=copies, refs=[weakref.ref(t) for t in flat], versions=versions, tiled=tiled,
+                          flags=flags)
         self._refresh(ent, flat, lib, device)
         E = len(experts)
         rows = [[0] * E for _ in range(6)]
@@ -345,11 +353,17 @@ class RocmBackend:
             rows[idx][e] = (src if src is not None else t).data_ptr()
         ent["ptrs"] = rows
         ent["table"] = torch.tensor(rows, dtype=torch.int64).to(device)
+        ids = {id(t) for t in flat}
         with self._lock:
+            # A buffer whose storage was swapped (``sc.data = sc.data.float()``)
+            # has a new address, so a new key: drop the entries made for it.
+            for k in [k for k, e in self._ptr_cache.items()
+                      if any(id(r()) in ids for r in e["refs"] if r() is not None)]:
+                del self._ptr_cache[k]
             self._ptr_cache[key] = ent
-        evict = weakref.WeakMethod(self._evict)
+        me, er = weakref.ref(self), weakref.ref(ent)
         for t in flat:
-            weakref.finalize(t, _call_weak, evict, key, ent)
+            weakref.finalize(t, _drop_entry, me, key, er)
         return ent
 
     def prepare_experts(self, experts, d, h, tile):
@@ -571,6 +585,24 @@ class RocmBackend:
                                     out.data_ptr(), x2.shape[0], d, eps, _stream_handle(x.device))
         _lib.check(rc, "rms_norm")
         return out.reshape(x.shape)
+
+    def wait_timeouts(self, device=None, reset=False) -> int:
+        """Give-ups of the decode combine's bounded wait on ``device`` since the
+        library was loaded or last reset (``reset=True`` clears what it reads).
+
+        In the decode regime the combine runs in the tail of the down kernel,
+        whose first workgroups wait for the others.  A wait that gives up
+        writes NaN over the tokens it owns (and -1 over their next top-k ids)
+        instead of combining rows that may not have been written, and counts
+        itself here.  The count is read back to the host, so this call waits
+        for the work already queued on the current stream."""
+        lib = _lib.load()
+        dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        buf = torch.empty(1, dtype=torch.int32, device=dev)
+        with torch.cuda.device(dev):
+            rc = lib.smaul_wait_timeouts(buf.data_ptr(), int(bool(reset)), _stream_handle(dev))
+        _lib.check(rc, "wait_timeouts")
+        return int(buf.item())
 
     def moe_forward(self, x, gate_w, gate_b, experts, top_k, tile):
         """SwiFFN_MoE.forward on the device.

@@ -72,3 +72,19 @@ def test_fp8linear_training_step(dtype):
     ulp = gw.float().abs() * 2.0 ** -7
     terms = 2 * (g.abs().t() @ xr.abs())
     assert bool((diff <= 2 * ulp + terms * 2.0 ** -18).all())
+
+
+def test_backward_input_zero_sizes_abi():
+    """in_f or out_f of 0 are accepted, as by the reference kernel
+    (fp8_cpu.cpp:227-228): out_f == 0 is an empty sum (dx all zeros, g / w / s
+    not read), in_f == 0 leaves nothing to write."""
+    from smaulnative_amd import _lib
+    lib = _lib.load()
+    print("case backward_input zero sizes", flush=True)
+    stream = torch.cuda.current_stream().cuda_stream
+    dx = torch.full((3, 5), 7.0, device=DEV)
+    _lib.check(lib.smaul_fp8_backward_input(None, None, None, dx.data_ptr(), 3, 5, 0, 64, stream), "out_f 0")
+    _lib.check(lib.smaul_fp8_backward_input(None, None, None, None, 3, 0, 4, 64, stream), "in_f 0")
+    torch.cuda.synchronize()
+    assert torch.equal(dx.cpu(), torch.zeros(3, 5))
+    assert lib.smaul_fp8_backward_input(None, None, None, dx.data_ptr(), 3, -1, 4, 64, stream) == _lib.SMAUL_ERR_INVALID

@@ -601,6 +601,29 @@ def test_expert_cache_layout_choice(d, h, tile, tiled):
     assert rel_l2(out.float(), ref.out.float()) < 2e-3
 
 
+def test_expert_cache_entries_released():
+    """An expert-cache entry lives only while the cache holds it: a buffer
+    whose storage is swapped (``sc.data = ...``, a new address for the same
+    tensor) drops the entry made for its old storage, and freeing a buffer
+    drops its entry; neither keeps the copies alive through the finalizers."""
+    import gc
+    import weakref
+    print("case expert cache entries released", flush=True)
+    d, h = 256, 640
+    _, _, _, experts = make_moe(5151, 8, d, h, 2, 1)
+    ex = [list(e) for e in to_dev_experts(experts)]
+    b = be()
+    old = weakref.ref(b._expert_entry(ex, ex[0][0].device, d, h, 64))
+    ex[0][1].data = ex[0][1].data.clone()  # new storage, same tensor object
+    new = weakref.ref(b._expert_entry(ex, ex[0][0].device, d, h, 64))
+    gc.collect()
+    assert old() is None and new() is not None
+    del ex[1]
+    ex[0] = None
+    gc.collect()
+    assert new() is None
+
+
 def test_tiled_layout_rejected_where_unsupported():
     """The tiled flag needs tile 64 and widths that are multiples of 64, and
     smaul_fp8_linear never takes it."""
@@ -839,3 +862,57 @@ def test_moe_chain_repeated(T, h, nE):
             assert torch.equal(a.cpu(), b.cpu()), it
         for a, b in zip(ref_r, got[5]):
             assert torch.equal(a.cpu(), b.cpu()), it
+
+
+@pytest.mark.parametrize("mode", ["chain", "norm", "plain"])
+def test_decode_tail_wait_give_up_is_loud(mode):
+    """The decode combine in the down kernel's tail waits (bounded) for every
+    workgroup of the launch.  Forced from the host to give up -- the test hook
+    asks for one arrival more than the grid holds and allows 64 polls, so
+    every kernel still exits normally -- each combining workgroup must poison
+    its tokens (NaN out / norm_out rows, NaN next prob / topw, next topi -1)
+    instead of combining, and count itself in smaul_wait_timeouts.  The
+    layer's own routing and counts are unaffected, and the next call with the
+    default wait is whole again."""
+    from smaulnative_amd import _lib
+    lib = _lib.load()
+    T, d, h, E, k = 64, 1024, 2560, 8, 2
+    print(f"case tail wait give-up mode={mode} T={T}", flush=True)
+    x, gw, gb, ex = make_moe(4242, T, d, h, E, k, dtype=torch.bfloat16)
+    _, gwb, gbb, _ = make_moe(4243, 1, d, h, E, k, dtype=torch.bfloat16)
+    dx, dgw, dgb, dex = x.to(DEV), gw.to(DEV), gb.to(DEV), to_dev_experts(ex)
+    nxt = (gwb.to(DEV), gbb.to(DEV), k)
+
+    def call():
+        if mode == "chain":
+            return be().moe_forward_norm(dx, dgw, dgb, dex, k, 64, None, 1e-6, next_router=nxt)
+        if mode == "norm":
+            return be().moe_forward_norm(dx, dgw, dgb, dex, k, 64, None, 1e-6)
+        return be().moe_forward(dx, dgw, dgb, dex, k, 64)
+
+    be().wait_timeouts(DEV, reset=True)
+    ref = call()
+    assert be().wait_timeouts(DEV) == 0
+    _lib.check(lib.smaul_debug_tail_wait(1, 64), "debug_tail_wait")
+    try:
+        got = call()
+        torch.cuda.synchronize()
+    finally:
+        _lib.check(lib.smaul_debug_tail_wait(0, 1 << 20), "debug_tail_wait")
+    # ceil(T / 8) combining workgroups, each gave up once
+    assert be().wait_timeouts(DEV, reset=True) == (T + 7) // 8
+    assert torch.isnan(got[0].float()).all()
+    for a, b in zip(ref[1:4], got[1:4]):  # prob, topi, counts of this layer
+        assert torch.equal(a.cpu(), b.cpu())
+    if mode != "plain":
+        assert torch.isnan(got[4].float()).all()
+    if mode == "chain":
+        nprob, ntopi, ntopw = got[5]
+        assert torch.isnan(nprob).all() and torch.isnan(ntopw).all()
+        assert (ntopi == -1).all()
+    again = call()
+    torch.cuda.synchronize()
+    assert be().wait_timeouts(DEV) == 0
+    flat = lambda r: [t for v in r for t in (v if isinstance(v, tuple) else (v,))]
+    for a, b in zip(flat(ref), flat(again)):
+        assert torch.equal(a.cpu(), b.cpu())

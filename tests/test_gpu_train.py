@@ -88,3 +88,44 @@ def test_moe_training_step_gradients(E, k):
             else:
                 assert lin._gw is not None and lin._gw.dtype == torch.bfloat16
                 assert rel(lin._gw.float(), ws[e][n].grad) < 1e-1, (e, n)
+
+
+def test_eval_mode_keeps_input_gradient():
+    """In eval mode with grad on, SwiFFN_MoE and SwiFFN still record autograd
+    (as the reference's FP8Linear function does, kernel/fp8_tile.py:162-170):
+    the input gradient equals the train-mode one bit for bit, and no expert
+    accumulates _gw (that is the training flag's only effect).  Under no_grad
+    the fused entries run and return outputs without a graph."""
+    from smaulnative_amd import SwiFFN
+    print("case eval-mode input gradient", flush=True)
+    torch.manual_seed(5)
+    cfg = MoEConfig(d_model=128, ffn_mult=2.5, tile=64, num_experts=4, num_experts_per_tok=2)
+    moe = SwiFFN_MoE(cfg).to(DEV)
+    x = torch.randn(2, 24, 128, device=DEV).to(torch.bfloat16)
+    c = torch.randn(2, 24, 128, device=DEV)
+    grads = {}
+    for mode in ("train", "eval"):
+        moe.train(mode == "train")
+        for ex in moe.experts:
+            for n in ("gate", "up", "down"):
+                getattr(ex, n)._gw = None
+        xi = x.clone().requires_grad_(True)
+        out = moe(xi)
+        assert out.grad_fn is not None, mode
+        (out.float() * c).sum().backward()
+        grads[mode] = xi.grad.clone()
+        gws = [getattr(ex, n)._gw for ex in moe.experts for n in ("gate", "up", "down")]
+        if mode == "eval":
+            assert all(g is None for g in gws)
+        else:
+            assert any(g is not None for g in gws)
+    assert torch.equal(grads["train"], grads["eval"])
+    with torch.no_grad():
+        assert moe(x).grad_fn is None
+
+    ffn = SwiFFN(cfg).to(DEV).eval()
+    xi = x.clone().requires_grad_(True)
+    y = ffn(xi)
+    assert y.grad_fn is not None
+    (y.float() * c).sum().backward()
+    assert xi.grad is not None and torch.isfinite(xi.grad.float()).all() and float(xi.grad.abs().max()) > 0
