@@ -19,15 +19,20 @@ Extra objects on the same JSON line:
   trace of the same launches;
 - ``cpu_baseline``: the reference CPU path on this host's cores -- the
   reference's own fp8_cpu.cpp (built under oracle/_ref) inside the torch MoE
-  loop of model.py:557-585 -- on bounded samples of the config-3 and config-5
-  tokens, at the process's affinity core count and at the reference default
-  max(1, cpu_count // 2) threads (kernel/compute.py:86), median of 3 runs;
+  loop of model.py:557-585 -- for every config on a bounded sample (config 3
+  and 5 tokens, config 1's layer, config 2's rows, the first 6 of config 4's
+  24 layers), at the process's affinity core count and at the reference
+  default max(1, cpu_count // 2) threads (kernel/compute.py:86), timed as
+  benchmark.py:51-59 does (3 warm-ups, median of 10; 1 and 3 at config 5);
 - ``decode``: config 4 (64 tokens x 24 MoE layers), one step replayed as a HIP
-  graph, with achieved HBM bytes/s against the 8 TB/s peak;
+  graph, with achieved HBM bytes/s against the 8 TB/s peak, chained and
+  unchained, and the give-ups of the fused combine's bounded wait;
 - ``c5``: config 5 (the large skewed layer, T=65536 d=2048 h=5120 E=16), run
   before the config-3 timed region so that region starts under sustained load
   rather than in the clock transient after idle;
-- ``c2``: config 2 (one dense SwiGLU FFN, 4096 x 512 -> 2 x 1280 -> 512).
+- ``c2``: config 2 (one dense SwiGLU FFN, 4096 x 512 -> 2 x 1280 -> 512), and
+  FP8Linear's GEMM (fp8_forward) at the same shapes with fp32 and bf16 x;
+- ``c1``: the config-1 MoE layer shape (512 tokens, d=512, E=4).
 Only one GPU is measured: ``--gpus`` above 1 exits with a message.
 """
 from __future__ import annotations
@@ -158,33 +163,79 @@ def c5_bench(be, steps, warmup):
     return res, cpu_inputs
 
 
-def c2_bench(be, steps, warmup):
-    """Config 2: one dense SwiGLU FFN, 4096 x 512 -> 2 x 1280 (gate+up, one launch) -> 512."""
+def event_median_ms(fn, n, warmup):
+    """Median device time (ms) of fn over n back-to-back calls, each between two
+    HIP events on the current stream, after `warmup` untimed calls."""
     import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for e0, e1 in evs:
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+
+
+def c2_bench(be, steps, warmup):
+    """Config 2: one dense SwiGLU FFN, 4096 x 512 -> 2 x 1280 (gate+up, one launch) -> 512.
+
+    Also the FP8Linear GEMM (fp8_forward, kernel/fp8_tile.py:163-170, the call
+    the unchanged model makes for each projection) at the same shapes: gate,
+    up and down as three calls, with fp32 x (what the reference's _Fn.forward
+    passes) and with bf16 x."""
+    import torch
+    import torch.nn.functional as F
     rows, d, h = 4096, 512, 1280
     gen = torch.Generator().manual_seed(1234 + 1)
-    x = torch.randn(rows, d, generator=gen).to(torch.bfloat16).to("cuda")
+    x32 = torch.randn(rows, d, generator=gen)
+    x = x32.to(torch.bfloat16).to("cuda")
     bufs = []
     for (o, i) in ((h, d), (h, d), (d, h)):
         bufs += [t.to("cuda") for t in quantized(torch.randn(o, i, generator=gen) * 0.02)]
     bufs = tuple(bufs)
-    for _ in range(warmup):
-        be.swiffn_forward(x, bufs, 64)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
     n = max(steps, 50)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
-    for e0, e1 in evs:
-        e0.record(stream)
-        be.swiffn_forward(x, bufs, 64)
-        e1.record(stream)
-    torch.cuda.synchronize()
-    ms = statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+    ms = event_median_ms(lambda: be.swiffn_forward(x, bufs, 64), n, warmup)
     flops = 6.0 * rows * d * h
-    return {"workload": "C2 dense SwiGLU FFN: 4096 x 512 -> 2 x 1280 (fused gate+up) -> 512, bf16, tile 64",
-            "tokens_per_s": rows / (ms * 1e-3), "ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
-            "mfma_frac": flops / (ms * 1e-3) / PEAK_BF16_FLOPS, "flops_per_step": flops,
-            "timing": f"median of {n} back-to-back calls, each between two HIP events on the launch stream"}
+    res = {"workload": "C2 dense SwiGLU FFN: 4096 x 512 -> 2 x 1280 (fused gate+up) -> 512, bf16, tile 64",
+           "tokens_per_s": rows / (ms * 1e-3), "ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+           "mfma_frac": flops / (ms * 1e-3) / PEAK_BF16_FLOPS, "flops_per_step": flops,
+           "timing": f"median of {n} back-to-back calls, each between two HIP events on the launch stream"}
+    lin = {}
+    for name, xx in (("f32_x", x32.to("cuda")), ("bf16_x", x)):
+        g = be.fp8_forward(xx, bufs[0], bufs[1], d, h, 64)
+        u = be.fp8_forward(xx, bufs[2], bufs[3], d, h, 64)
+        hh = (F.silu(g) * u).to(xx.dtype)
+
+        def three():
+            be.fp8_forward(xx, bufs[0], bufs[1], d, h, 64)
+            be.fp8_forward(xx, bufs[2], bufs[3], d, h, 64)
+            be.fp8_forward(hh, bufs[4], bufs[5], h, d, 64)
+        lms = event_median_ms(three, n, warmup)
+        lin[name] = {"ms_per_step": lms, "tflops": flops / (lms * 1e-3) / 1e12,
+                     "mfma_frac": flops / (lms * 1e-3) / PEAK_BF16_FLOPS}
+    res["fp8_linear"] = dict(lin, workload="fp8_forward (FP8Linear's GEMM, fp32 output) for gate 4096x512->1280, "
+                                           "up 4096x512->1280 and down 4096x1280->512: three calls per step "
+                                           "(the SwiGLU product between them is not timed)")
+    return res, (x, bufs)
+
+
+def c1_bench(be, steps, warmup):
+    """The config-1 MoE layer shape: T=512 tokens (batch 2 x ctx 256), d=512,
+    h=1280, E=4, top-2, no router bias (model.py:537).  Launch-bound."""
+    import torch
+    T, d, h, E, k = 512, 512, 1280, 4, 2
+    x, gw, _, experts = make_layer(1234, T, d, h, E, 0.0, "cpu")
+    xd, gwd = x.to("cuda"), gw.to("cuda")
+    exd = [tuple(t.to("cuda") for t in e) for e in experts]
+    ms = event_median_ms(lambda: be.moe_forward(xd, gwd, None, exd, k, 64), max(steps, 50), warmup)
+    fl = sum(layer_flops(T, d, h, E, k).values())
+    return {"workload": "C1 MoE layer shape: T=512 d=512 h=1280 E=4 top-2 tile 64, bf16, no router bias",
+            "tokens_per_s": T / (ms * 1e-3), "ms_per_step": ms, "layer_mfma_frac": fl / (ms * 1e-3) / PEAK_BF16_FLOPS,
+            "flops_per_step": fl}, (x, gw, None, experts)
 
 
 def cpu_model():
@@ -198,63 +249,134 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
-def cpu_time_moe(x, gw, gb, experts, k, threads, target_s, max_tokens):
-    """Median of 3 timed passes of the reference CPU path over the first n tokens,
-    n sized so that one pass takes about target_s (benchmark.py:51-59 method)."""
-    import torch
+def cpu_med(fn, warm, runs):
+    """benchmark.py:51-59: `warm` untimed calls, then the median of `runs` perf_counter timings (s)."""
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def cpu_gemm(threads):
+    """The CPU fp8 GEMM: the reference's own fp8_cpu.cpp (oracle/_ref) when built, else the C restatement."""
     import oracle
+    if oracle.ref_module() is not None:
+        return oracle.fp8_forward_ref, "reference"
+    return (lambda xx, w, s, i, o, t: oracle.fp8_forward(xx, w, s, i, o, t, threads=threads)), "port"
+
+
+def sized(run_n, n_max, target_s, n0):
+    """Sample size: n doubles from n0 (capped at n_max) until one pass of run_n(n) takes about target_s."""
+    n = min(n0, n_max)
+    while True:
+        t0 = time.perf_counter()
+        run_n(n)
+        dt = time.perf_counter() - t0
+        if dt >= 0.5 * target_s or n >= n_max:
+            return n
+        n = int(min(n_max, max(2 * n, n * target_s / max(dt, 1e-4))))
+
+
+def set_threads(threads):
+    import torch
     torch.set_num_threads(threads)
     os.environ["OMP_NUM_THREADS"] = str(threads)
-    ref = oracle.ref_module()
-    gemm = oracle.fp8_forward_ref if ref is not None else (
-        lambda xx, w, s, i, o, t: oracle.fp8_forward(xx, w, s, i, o, t, threads=threads))
-    kind = "reference" if ref is not None else "port"
-    ow = [oracle.ExpertWeights(*e) for e in experts]
-    oracle.moe_forward(x[:64], gw, gb, ow, k, 64, gemm=gemm)  # warm-up
-    n = min(256, max_tokens)
-    while True:  # grow the sample until one pass takes about target_s
-        t0 = time.perf_counter()
-        oracle.moe_forward(x[:n], gw, gb, ow, k, 64, gemm=gemm)
-        dt = time.perf_counter() - t0
-        if dt >= 0.5 * target_s or n >= max_tokens:
-            break
-        n = int(min(max_tokens, max(2 * n, n * target_s / max(dt, 1e-4))))
-    runs = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        oracle.moe_forward(x[:n], gw, gb, ow, k, 64, gemm=gemm)
-        runs.append(time.perf_counter() - t0)
-    med = statistics.median(runs)
-    return {"tokens_per_s": n / med, "tokens": n, "median_s": med, "threads": threads}, kind
 
 
-def cpu_baseline(c3_inputs, c5_inputs, k, target_s=2.5):
-    """The reference CPU path on this host, config 3 (headline) and config 5 samples."""
+def cpu_moe_leg(x, gw, gb, experts, k, threads, target_s, warm, runs):
+    """The reference MoE layer (model.py:557-585 torch loop around the fp8 GEMM)
+    on the first n tokens, n sized so one pass takes about target_s."""
+    import oracle
+    set_threads(threads)
+    gemm, kind = cpu_gemm(threads)
+    ow = [oracle.ExpertWeights(*[t.cpu() for t in e]) for e in experts]
+    run = lambda n: oracle.moe_forward(x[:n], gw, gb, ow, k, 64, gemm=gemm)
+    n = sized(run, x.shape[0], target_s, 256)
+    med = cpu_med(lambda: run(n), warm, runs)
+    return {"tokens_per_s": n / med, "tokens": n, "median_s": med, "threads": threads,
+            "timing": f"{warm} warm-up + median of {runs}"}, kind
+
+
+def cpu_c2_leg(x, bufs, threads, target_s):
+    """SwiFFN.forward (model.py:289-290) with the reference GEMM on the first n rows."""
+    import oracle
+    set_threads(threads)
+    gemm, _ = cpu_gemm(threads)
+    ex = oracle.ExpertWeights(*[t.cpu() for t in bufs])
+    xc = x.cpu()
+    run = lambda n: oracle.swiffn_forward(xc[:n], ex, 64, gemm=gemm)
+    n = sized(run, xc.shape[0], target_s, 256)
+    med = cpu_med(lambda: run(n), 3, 10)
+    return {"tokens_per_s": n / med, "tokens": n, "median_s": med, "threads": threads,
+            "timing": "3 warm-up + median of 10"}
+
+
+def cpu_c4_leg(layers, x0, k, threads, n_layers):
+    """The first n_layers of the config-4 chain (64 tokens each, unit-RMS norm
+    between layers) with the reference MoE layer; the per-step time scales
+    that by 24 / n_layers."""
+    import torch
+    import oracle
+    set_threads(threads)
+    gemm, _ = cpu_gemm(threads)
+    sample = [(gw.cpu(), gb.cpu(), [oracle.ExpertWeights(*[t.cpu() for t in e]) for e in ex])
+              for gw, gb, ex in layers[:n_layers]]
+    xc = x0.cpu()
+
+    def run():
+        xl = xc
+        for gw, gb, ow in sample:
+            o = oracle.moe_forward(xl, gw, gb, ow, k, 64, gemm=gemm).out.float()
+            xl = (o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    med = cpu_med(run, 3, 10)
+    step = med * len(layers) / n_layers
+    return {"tokens_per_s": xc.shape[0] / step, "s_per_step": step, "threads": threads,
+            "sample": f"first {n_layers} of the {len(layers)} layers, median of 10 after 3 warm-ups, "
+                      f"scaled to {len(layers)} layers"}
+
+
+def cpu_baseline(legs, k):
+    """The reference CPU path on this host for every config: at the process's
+    affinity core count and at the reference default max(1, cpu_count // 2)
+    threads (kernel/compute.py:86)."""
     import torch
     import oracle
     aff = oracle.default_threads()
     dflt = max(1, (os.cpu_count() or 2) // 2)
-    x, gw, gb, experts = c3_inputs
-    main, kind = cpu_time_moe(x, gw, gb, experts, k, aff, target_s, x.shape[0])
+    threads = sorted({aff, dflt}, reverse=True)
+    x, gw, gb, experts = legs["c3"]
+    per = {}
+    main = None
+    kind = "port"
+    for th in threads:
+        # samples below a few thousand tokens leave the reference kernel's
+        # 32-row tasks short of work per expert: size one pass to about 1 s
+        r, kind = cpu_moe_leg(x, gw, gb, experts, k, th, 2.0, 3, 10)
+        per[str(th)] = r
+        main = main or r
     res = {"value": main["tokens_per_s"], "unit": "tokens/s", "cores": aff, "kind": kind,
-           "sample": f"first {main['tokens']} of the config-3 tokens, median of 3 passes of "
-                     f"{main['median_s']:.2f} s; "
+           "sample": f"first {main['tokens']} of the config-3 tokens, 3 warm-up passes then the median of 10 "
+                     f"({main['median_s']:.2f} s); "
                      + ("reference kernel/fp8_cpu.cpp (oracle/_ref)" if kind == "reference"
                         else "C restatement of fp8_cpu.cpp") + " in the model.py:557-585 torch MoE loop",
-           "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count()}
-    if dflt != aff:
-        alt, _ = cpu_time_moe(x, gw, gb, experts, k, dflt, target_s, x.shape[0])
-        res["at_reference_default_threads"] = alt
-    else:
-        res["at_reference_default_threads"] = dict(main)
-    if c5_inputs is not None:
-        x5, gw5, gb5, ex5 = c5_inputs
-        ex5 = [tuple(t.cpu() for t in e) for e in ex5]
-        c5 = {}
-        for th in sorted({aff, dflt}):
-            r, _ = cpu_time_moe(x5, gw5, gb5, ex5, k, th, target_s, x5.shape[0])
-            c5[str(th)] = r
-        res["c5"] = c5
+           "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(), "c3": per,
+           "at_reference_default_threads": per[str(dflt)]}
+    if legs.get("c5") is not None:
+        x5, gw5, gb5, ex5 = legs["c5"]
+        res["c5"] = {str(th): cpu_moe_leg(x5, gw5, gb5, ex5, k, th, 3.0, 1, 3)[0] for th in threads}
+    if legs.get("c1") is not None:
+        x1, gw1, gb1, ex1 = legs["c1"]
+        res["c1"] = {str(th): cpu_moe_leg(x1, gw1, gb1, ex1, k, th, 0.1, 3, 10)[0] for th in threads}
+    if legs.get("c2") is not None:
+        x2, bufs = legs["c2"]
+        res["c2"] = {str(th): cpu_c2_leg(x2, bufs, th, 0.3) for th in threads}
+    if legs.get("c4") is not None:
+        lay, x0 = legs["c4"]
+        res["c4"] = {str(th): cpu_c4_leg(lay, x0, k, th, 6) for th in threads}
     torch.set_num_threads(aff)
     return res
 
@@ -267,6 +389,7 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
     its own input with a router kernel)."""
     import torch
     dev = torch.device("cuda")
+    be.wait_timeouts(dev, reset=True)
     lay = []
     for l in range(layers):
         x, gw, gb, ex = make_layer(4000 + l, T, d, h, E, 0.5, dev, gen_device="cuda")
@@ -323,6 +446,9 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
         step()
     torch.cuda.synchronize()
     dt_eager = (time.perf_counter() - t0) / max(1, steps // 4)
+    # give-ups of the fused combine's bounded wait over every decode call above
+    # (each would have poisoned its tokens instead of combining them)
+    timeouts = be.wait_timeouts(dev, reset=True)
     expert_bytes = 3 * d * h * (1 + 4 / 64)
     nbytes = 0.0
     for c in counts:
@@ -336,7 +462,8 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
             "ms_per_step_unchained": dt_plain * 1e3,
             "bytes_per_step": nbytes, "hbm_GBps": nbytes / dt / 1e9,
             "hbm_frac": nbytes / dt / PEAK_HBM_BPS, "hbm_frac_unchained": nbytes / dt_plain / PEAK_HBM_BPS,
-            "graph_matches_eager": ok and ok_plain, "chain_matches_unfused": chain_ok}
+            "graph_matches_eager": ok and ok_plain, "chain_matches_unfused": chain_ok,
+            "sync_timeouts": timeouts}, (lay, x0)
 
 
 def read_traffic():
@@ -455,23 +582,27 @@ def main():
     }
     if c5_res is not None:
         res["c5"] = c5_res
+    legs = {"c3": (x, gw, gb, experts), "c5": c5_inputs}
+
+    def leg(name, fn):
+        log(f"bench: {name}")
+        try:
+            r, inputs = fn()
+            res[name] = r
+            legs[name] = inputs
+        except Exception as exc:  # report, keep the headline
+            res[name] = {"error": f"{type(exc).__name__}: {exc}"}
     if not args.no_c2:
-        log("bench: config 2")
-        try:
-            res["c2"] = c2_bench(be, args.steps, args.warmup)
-        except Exception as exc:
-            res["c2"] = {"error": f"{type(exc).__name__}: {exc}"}
+        leg("c2", lambda: c2_bench(be, args.steps, args.warmup))
+    leg("c1", lambda: c1_bench(be, args.steps, args.warmup))
     if not args.no_decode:
-        log("bench: decode (config 4)")
-        try:
-            res["decode"] = decode_bench(be, max(5, args.steps), args.warmup)
-        except Exception as exc:
-            res["decode"] = {"error": f"{type(exc).__name__}: {exc}"}
+        leg("decode", lambda: decode_bench(be, max(5, args.steps), args.warmup))
+        legs["c4"] = legs.pop("decode", None)
     gc.enable()
     if not args.no_cpu:
         log("bench: CPU baseline")
         try:
-            res["cpu_baseline"] = cpu_baseline((x, gw, gb, experts), c5_inputs, k)
+            res["cpu_baseline"] = cpu_baseline(legs, k)
         except Exception as exc:
             res["cpu_baseline"] = {"error": f"{type(exc).__name__}: {exc}"}
     print(json.dumps(res), flush=True)

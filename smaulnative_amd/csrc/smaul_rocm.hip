@@ -710,9 +710,13 @@ struct DmaGemmCfg {
   static_assert(LDS <= 160 * 1024, "LDS budget");
 };
 
-template <int BM, int BN, int WM, int WN, int NSTAGE, bool SWIGLU, bool CANON, bool REMAP>
+// OUT_F32 (not SWIGLU): the fp32 sums are stored as they are (the dense
+// fp8_forward contract), straight from the MFMA layout; otherwise they are
+// rounded to bf16 and stored through LDS.
+template <int BM, int BN, int WM, int WN, int NSTAGE, bool SWIGLU, bool CANON, bool REMAP, bool OUT_F32 = false>
 __global__ void __launch_bounds__(WM * WN * 64, 2)
 fp8_gemm_dma_kernel(GemmArgs p) {
+  static_assert(!(OUT_F32 && SWIGLU), "the SwiGLU epilogue rounds to bf16");
   using C = DmaGemmCfg<BM, BN, WM, WN, NSTAGE, SWIGLU>;
   constexpr int NW = C::NW, BNO = C::BNO, TM = C::TM, TN = C::TN, TNO = C::TNO, FM = C::FM, FN = C::FN,
                 FNO = C::FNO, A_BYTES = C::A_BYTES, B_BYTES = C::B_BYTES, STAGE = C::STAGE,
@@ -933,6 +937,21 @@ fp8_gemm_dma_kernel(GemmArgs p) {
     nbuf = nbuf + 1 == NSTAGE ? 0 : nbuf + 1;
   }
   wait_vm<0>();
+  if constexpr (OUT_F32) {
+    // A lane holds column l32 of each 32x32 tile, rows (r/4)*8 + g*4 + r%4:
+    // each store instruction writes 128 contiguous bytes of two rows.
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int lr = wm * TM + i * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
+          if (lr < rows_here)
+            ((float*)p.y)[(int64_t)(row0 + lr) * p.ldy + n0 + wn * TN + j * 32 + l32] = acc[i][j][r];
+        }
+    return;
+  }
   __syncthreads();  // every wave is done with the stage buffers
 
   // ---- epilogue: through LDS, then 16-byte row stores ----------------------
@@ -3734,16 +3753,68 @@ struct CfgDmaGU {  // gate+up with the SwiGLU epilogue: 128 rows x 128 outputs
 struct CfgDmaDown {  // down projection: 128 rows x 256 outputs
   static constexpr int BM = 128, BN = 256, WM = 1, WN = 4, NSTAGE = 2;
 };
+// Smaller tiles for dense GEMMs whose 128x256 grid would leave most of the
+// 512 workgroup slots (two per CU) empty: every workgroup of such a grid runs
+// in the first round, so the launch takes one tile's whole latency, and a
+// smaller tile shortens it.  Deeper pipelines cover the DMA latency that the
+// second workgroup of a CU no longer hides.
+struct CfgDmaGU64 {  // 64 rows x 64 outputs (gate+up), 2 x 2 waves of 32 rows x 32 outputs
+  static constexpr int BM = 64, BN = 128, WM = 2, WN = 2, NSTAGE = 3;
+};
+struct CfgDma64x128 {  // 64 rows x 128 outputs
+  static constexpr int BM = 64, BN = 128, WM = 1, WN = 4, NSTAGE = 3;
+};
+struct CfgDma32x128 {  // 32 rows x 128 outputs
+  static constexpr int BM = 32, BN = 128, WM = 1, WN = 4, NSTAGE = 4;
+};
 
-template <class CF, bool SWIGLU, bool CANON>
+template <class CF, bool SWIGLU, bool CANON, bool OUT_F32 = false>
 int launch_gemm_dma(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
   constexpr int BNO = SWIGLU ? CF::BN / 2 : CF::BN;
   const int64_t n_tiles = (a.N + BNO - 1) / BNO;
   if (m_tiles <= 0 || n_tiles <= 0) return SMAUL_OK;
   if (m_tiles > 65535 || n_tiles > 65535) return fail(SMAUL_ERR_UNSUPPORTED, "gemm grid too large");
-  hipLaunchKernelGGL((fp8_gemm_dma_kernel<CF::BM, CF::BN, CF::WM, CF::WN, CF::NSTAGE, SWIGLU, CANON, true>),
-                     dim3((unsigned)n_tiles, (unsigned)m_tiles), dim3(CF::WM * CF::WN * 64), 0, stream, a);
+  hipLaunchKernelGGL(
+      (fp8_gemm_dma_kernel<CF::BM, CF::BN, CF::WM, CF::WN, CF::NSTAGE, SWIGLU, CANON, true, OUT_F32>),
+      dim3((unsigned)n_tiles, (unsigned)m_tiles), dim3(CF::WM * CF::WN * 64), 0, stream, a);
   return check_launch("fp8_gemm_dma_kernel");
+}
+
+// The dense (one-segment) LDS-DMA GEMM with its tile chosen by grid size:
+// the 128-row tile where its grid fills the workgroup slots (two per CU),
+// else 64 x 128 (gate+up: 64 x 64 outputs), or 32 x 128 where even that
+// leaves CUs without a workgroup; -1 when N is not a multiple of 128.
+// Measured at config 2 (kernel trace, 4096 rows): gate+up 22.0 -> 18.3 us,
+// down (K 1280, N 512) 24.2 -> 11.7 us; 32 x 128 tiles there: 11.4 us.
+enum DenseTile { DT_128x256 = 0, DT_64x128_GU = 1, DT_64x128 = 2, DT_32x128 = 3 };
+int pick_dense_tile(bool swiglu, int64_t rows, int64_t N) {
+  if (N % 128 != 0) return -1;
+  const int64_t cus = cu_count();
+  auto tiles = [&](int64_t bm, int64_t bno) { return ((rows + bm - 1) / bm) * (N / bno); };
+  if (swiglu) return tiles(128, 128) >= 2 * cus ? DT_128x256 : DT_64x128_GU;
+  if (N % 256 == 0 && tiles(128, 256) >= 2 * cus) return DT_128x256;
+  return tiles(64, 128) >= cus ? DT_64x128 : DT_32x128;
+}
+
+template <bool SWIGLU, bool CANON, bool OUT_F32>
+int launch_dense_dma(const GemmArgs& a, int tile, hipStream_t stream) {
+  const int64_t rows = a.R;
+  switch (tile) {
+    case DT_128x256:
+      return launch_gemm_dma<CfgDmaGU, SWIGLU, CANON, OUT_F32>(a, (rows + 127) / 128, stream);
+    case DT_64x128_GU:
+      if constexpr (SWIGLU) return launch_gemm_dma<CfgDmaGU64, SWIGLU, CANON, OUT_F32>(a, (rows + 63) / 64, stream);
+      break;
+    case DT_64x128:
+      if constexpr (!SWIGLU) return launch_gemm_dma<CfgDma64x128, SWIGLU, CANON, OUT_F32>(a, (rows + 63) / 64, stream);
+      break;
+    case DT_32x128:
+      if constexpr (!SWIGLU) return launch_gemm_dma<CfgDma32x128, SWIGLU, CANON, OUT_F32>(a, (rows + 31) / 32, stream);
+      break;
+    default:
+      break;
+  }
+  return fail(SMAUL_ERR_INVALID, "dense gemm: no tile for this shape");
 }
 
 // The LDS-DMA kernel needs bf16 activations, 64-wide scale tiles, K a
@@ -3836,6 +3907,11 @@ int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* 
   const bool vec = (in_f % 16 == 0) && aligned16(x) && aligned16(w);
   const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
   const bool small = rows <= 64;
+  // bf16 x, 64-wide tiles and 16-byte aligned code rows: the LDS-DMA kernel
+  // with its tile sized to the grid, fp32 sums stored as they are
+  const int dt = small ? -1 : pick_dense_tile(false, rows, out_f);
+  if (dt >= 0 && vec && dma_gemm_ok(a, x_dtype, flags | SMAUL_FLAG_ALIGNED_CODES, rows, 128))
+    return canon ? launch_dense_dma<false, true, true>(a, dt, stream) : launch_dense_dma<false, false, true>(a, dt, stream);
   if (x_dtype == SMAUL_DTYPE_BF16) {
     const int64_t bm = small ? CfgSmall::BM : CfgBig::BM;
     const int64_t mt = (rows + bm - 1) / bm;
@@ -4166,14 +4242,13 @@ static int dense_gemm(bool swiglu, const void* act, int act_dtype, const uint8_t
   a.E = 1;
   a.tiled = (flags & SMAUL_FLAG_TILED_LAYOUT) != 0;
   const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
-  const int64_t bno = swiglu ? CfgDmaGU::BN / 2 : CfgDmaDown::BN;
-  if (dma_gemm_ok(a, act_dtype, flags | SMAUL_FLAG_ALIGNED_CODES, rows, bno)) {
-    const int64_t mt = (rows + CfgBig::BM - 1) / CfgBig::BM;
+  const int dt = pick_dense_tile(swiglu, rows, N);
+  if (dt >= 0 && dma_gemm_ok(a, act_dtype, flags | SMAUL_FLAG_ALIGNED_CODES, rows, 128)) {
     if (swiglu)
-      return canon ? launch_gemm_dma<CfgDmaGU, true, true>(a, mt, stream)
-                   : launch_gemm_dma<CfgDmaGU, true, false>(a, mt, stream);
-    return canon ? launch_gemm_dma<CfgDmaDown, false, true>(a, mt, stream)
-                 : launch_gemm_dma<CfgDmaDown, false, false>(a, mt, stream);
+      return canon ? launch_dense_dma<true, true, false>(a, dt, stream)
+                   : launch_dense_dma<true, false, false>(a, dt, stream);
+    return canon ? launch_dense_dma<false, true, false>(a, dt, stream)
+                 : launch_dense_dma<false, false, false>(a, dt, stream);
   }
   const bool small = rows <= 64;
   if (act_dtype == SMAUL_DTYPE_BF16) {

@@ -107,6 +107,33 @@ def test_fp8_linear_bf16_inputs_vs_oracle(rows, in_f, out_f, tile):
     assert rel_max(y, ref) < 2e-6, rel_max(y, ref)
 
 
+@pytest.mark.parametrize("rows,in_f,out_f,raw_codes", [
+    (4096, 512, 1280, False),   # C2 gate: 64x128 tiles
+    (4096, 1280, 512, False),   # C2 down: 32x128 tiles
+    (300, 256, 384, False),     # ragged last row tile
+    (16384, 1024, 2560, False), # 128x256 tiles
+    (512, 256, 256, True),      # every code, 0x7F/0xFF decoded on the fly
+])
+def test_fp8_linear_bf16_dma_tiles(rows, in_f, out_f, raw_codes):
+    """bf16 x with 64-wide tiles and out_f a multiple of 128 runs the LDS-DMA
+    kernel with fp32 output, its tile sized to the grid.  A sample of rows
+    (first, middle, last) against the oracle at the bf16-input bar."""
+    print(f"case fp8_linear dma rows={rows} in_f={in_f} out_f={out_f} raw={raw_codes}", flush=True)
+    gen = torch.Generator().manual_seed(rows + in_f * 3 + out_f)
+    x = torch.randn(rows, in_f, generator=gen).to(torch.bfloat16)
+    if raw_codes:
+        w = torch.randint(0, 256, (out_f, in_f), generator=gen, dtype=torch.int64).to(torch.uint8)
+        s = torch.rand(out_f, in_f // 64, generator=gen) * 0.01 + 1e-3
+    else:
+        w, s = oracle.quantize_tiles(torch.randn(out_f, in_f, generator=gen) * 0.02, 64)
+    y = be().fp8_forward(x.to(DEV), w.to(DEV), s.to(DEV), in_f, out_f, 64).cpu()
+    idx = torch.cat([torch.arange(0, min(rows, 96)), torch.arange(rows // 2, rows // 2 + 33),
+                     torch.arange(max(0, rows - 65), rows)]).unique()
+    ref = oracle.fp8_forward(x[idx].float(), w, s, in_f, out_f, 64)
+    assert torch.isfinite(y).all()
+    assert rel_max(y[idx], ref) < 2e-6, rel_max(y[idx], ref)
+
+
 def test_fp8_linear_special_codes():
     # every one of the 256 codes, including 0x7F/0xFF (+-448, NaN in OCP),
     # 0x80 (-0) and the subnormals, against the reference codebook
