@@ -14,7 +14,11 @@ is never run); the quantizer is the reference's torch path.
 Stored: idx, logits of forward (model.py:726-748) at five positions, each
 layer's MoE top-k and expert counts, and the logits of prefill over the
 first 255 tokens (model.py:774-786) followed by one step (model.py:788-810).
-Nothing else: the GPU test regenerates the weights from the same recipe.
+For each layer's SwiFFN_MoE in that forward, also its exact input (the bf16
+x that Block hands to self.ffn, model.py:646), its output fx and its
+last_prob, so the MoE layer can be checked on the reference's own inputs
+(bf16 stored as int16 bit patterns).  The GPU test regenerates the weights
+from the same recipe.
 
 Also stored, as the scale for the GPU test's tolerance: how far the same
 reference model moves when only the fp32 summation order of its fp8 GEMM
@@ -62,12 +66,26 @@ def main():
     sd, idx = draw_state(ref_fp8.quantize_tiles)
     m.load_state_dict(sd, strict=True)
     out = {"idx": idx.numpy(), "positions": np.array(POSITIONS, dtype=np.int64)}
+    seen = {}
+
+    def capture(l):
+        def hook(mod, inp, res):
+            if l not in seen:  # the first forward only
+                seen[l] = True
+                assert inp[0].dtype == torch.bfloat16 and res.dtype == torch.bfloat16
+                out[f"layer{l}_moe_x"] = inp[0].detach().contiguous().view(torch.int16).numpy()
+                out[f"layer{l}_moe_fx"] = res.detach().contiguous().view(torch.int16).numpy()
+                out[f"layer{l}_moe_prob"] = mod.last_prob.detach().float().numpy()
+        return hook
+    hooks = [blk.ffn.register_forward_hook(capture(l)) for l, blk in enumerate(m.blocks)]
     with torch.no_grad():
         logits, _ = m(idx)
         out["forward_logits"] = logits[:, POSITIONS, :].numpy()
         for l, blk in enumerate(m.blocks):
             out[f"layer{l}_topi"] = blk.ffn.last_topi.numpy()
             out[f"layer{l}_counts"] = np.array(blk.ffn.expert_token_counts, dtype=np.int64)
+    for hk in hooks:
+        hk.remove()
     pl, states = m.prefill(idx[:, :-1])
     sl, _ = m.step(idx[:, -1:], states)
     out["prefill_logits"] = pl.numpy()

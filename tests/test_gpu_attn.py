@@ -162,3 +162,37 @@ def test_model_c1_forward_prefill_step_vs_reference():
         e = float((a.cpu().double() - r).norm() / r.norm())
         print(f"{name} logits rel_l2 {e:.3e}", flush=True)
         assert e < 2 * floor
+
+
+@pytest.mark.parametrize("layer", [0, 1])
+def test_model_c1_moe_layer_on_reference_inputs(layer):
+    """Each config-1 MoE layer on the reference model's own input: the exact
+    bf16 x its Block handed to self.ffn (model.py:646), through SwiFFN_MoE on
+    the rocm backend.  Routing bit-exact (top-k and counts equal), last_prob
+    within 1e-5 relative, output within rel-L2 2e-3 of the reference layer's
+    fx (golden_model_c1.npz)."""
+    from test_oracle import c1_layer_case
+    from smaulnative_amd import MoEConfig, SwiFFN_MoE
+    from _model import C1
+    print(f"case C1 MoE layer {layer} on the reference's inputs", flush=True)
+    x, gw, experts, fx, prob, topi, counts = c1_layer_case(layer)
+    moe = SwiFFN_MoE(MoEConfig(d_model=C1["d"], ffn_mult=C1["ffn_mult"], tile=C1["tile"],
+                               num_experts=C1["experts"], num_experts_per_tok=C1["top_k"]))
+    with torch.no_grad():
+        moe.gate.weight.copy_(gw)
+        for e, ex in enumerate(moe.experts):
+            for n in ("gate", "up", "down"):
+                getattr(ex, n).w8.copy_(getattr(experts[e], n + "_w"))
+                getattr(ex, n).sc.copy_(getattr(experts[e], n + "_s"))
+    moe = moe.to(DEV).eval()
+    with torch.no_grad():
+        y = moe(x.reshape(C1["batch"], C1["ctx"], -1).to(DEV))
+    got_topi = moe.last_topi.reshape(-1, C1["top_k"]).cpu()
+    assert torch.equal(got_topi, topi), int((got_topi != topi).any(-1).sum())
+    assert moe.expert_token_counts == counts
+    p = moe.last_prob.reshape(-1, C1["experts"]).cpu().double()
+    assert float(((p - prob.double()).abs() / prob.double().abs().clamp_min(1e-30)).max()) < 1e-5
+    y = y.reshape(-1, C1["d"]).cpu().double()
+    err = float((y - fx.double()).norm() / fx.double().norm())
+    print(f"layer {layer}: routing bit-exact, rel_l2 {err:.3e}", flush=True)
+    assert err <= 2e-3

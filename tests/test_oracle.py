@@ -295,3 +295,37 @@ def test_backward_input_bit_exact_with_reference_kernel(rows, in_f, out_f, tile)
     assert torch.equal(dx, ref)
     bf = g.double() @ oracle.decode_full(w, s, tile).double()
     assert float((dx.double() - bf).abs().max() / bf.abs().max()) < 1e-5
+
+
+def c1_layer_case(layer):
+    """Layer `layer` of the config-1 model in golden_model_c1.npz: the exact
+    bf16 input the reference Block handed to its SwiFFN_MoE, the layer's
+    output, last_prob, top-k and counts, and the layer's weights (regenerated
+    by tests/_model.draw_state, as the fixture's model was loaded)."""
+    from _model import C1, draw_state
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden_model_c1.npz"))
+    sd, _ = draw_state(oracle.quantize_tiles)
+    d, E = C1["d"], C1["experts"]
+    p = f"blocks.{layer}.ffn."
+    experts = [oracle.ExpertWeights(*[sd[p + f"experts.{e}.{n}.{t}"] for n in ("gate", "up", "down")
+                                      for t in ("w8", "sc")]) for e in range(E)]
+    x = torch.from_numpy(g[f"layer{layer}_moe_x"]).view(torch.bfloat16).reshape(-1, d)
+    fx = torch.from_numpy(g[f"layer{layer}_moe_fx"]).view(torch.bfloat16).reshape(-1, d)
+    prob = torch.from_numpy(g[f"layer{layer}_moe_prob"]).reshape(-1, E)
+    topi = torch.from_numpy(g[f"layer{layer}_topi"]).reshape(-1, C1["top_k"])
+    counts = g[f"layer{layer}_counts"].tolist()
+    return x, sd[p + "gate.weight"], experts, fx, prob, topi, counts
+
+
+@pytest.mark.parametrize("layer", [0, 1])
+def test_moe_oracle_matches_reference_layer_in_model(layer):
+    """The oracle's MoE layer (the C restatement of fp8_cpu.cpp in the
+    model.py:557-585 loop) on the exact input the reference model's layer saw
+    reproduces that layer's output, probabilities, top-k and counts bit for
+    bit (golden_model_c1.npz, written by the reference SmaulLinear)."""
+    from _model import C1
+    x, gw, experts, fx, prob, topi, counts = c1_layer_case(layer)
+    r = oracle.moe_forward(x, gw, None, experts, C1["top_k"], C1["tile"])
+    assert torch.equal(r.topi, topi) and r.counts == counts
+    assert torch.equal(r.prob, prob)
+    assert torch.equal(r.out, fx)
