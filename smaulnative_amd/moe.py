@@ -166,11 +166,13 @@ class SwiFFN_MoE(nn.Module):
         fused moe_forward path has no backward, so training runs this one.
         """
         d = x.shape[-1]
+        lead = x.shape[:-1]
         xs = x.reshape(-1, d)
         prob = torch.softmax(self.gate(xs.float()), -1)
-        self.last_prob = prob
+        # kept with x's leading dimensions, as the reference's are (model.py:558-565)
+        self.last_prob = prob.view(*lead, self.num_experts)
         topv, topi = torch.topk(prob, self.top_k, -1)
-        self.last_topi = topi.detach()
+        self.last_topi = topi.detach().view(*lead, self.top_k)
         total = topv.sum(-1, keepdim=True)
         topv = torch.where(total < 1e-6, torch.full_like(topv, 1.0 / self.top_k), topv / total.clamp_min(1e-9))
         out = torch.zeros(xs.shape, dtype=torch.float32, device=xs.device)
