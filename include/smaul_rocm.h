@@ -362,6 +362,21 @@ int smaul_attn_step(float* S, float* z, const float* q, const float* k, const fl
                     int64_t H, int64_t D, float eps, hipStream_t stream);
 
 /*
+ * Backward of the linear-attention recurrence: dQ, dK, dV [B,T,H,D] (K raw,
+ * so dK includes the key normalisation's backward) from the upstream
+ * gradient dY and the forward's Q, K, V, Y and DEN.  Replaces the reference's
+ * native two-pass kernel kernel/attn_cpu.cpp attn_backward (:227-368),
+ * reached through the backend entry kernel/compute.py:314-322 from
+ * model.py:249,262; results are bit-identical to it.  All fp32 contiguous;
+ * 0 < D <= 2048, eps positive and finite (the forward's).  For D > 128 the
+ * per-task state lives in `workspace` (smaul_attn_workspace_size(B, H, D, 0)
+ * bytes; 0 otherwise).
+ */
+int smaul_attn_backward(const float* dY, const float* Q, const float* K, const float* V, const float* Y,
+                        const float* DEN, float* dQ, float* dK, float* dV, int64_t B, int64_t T, int64_t H, int64_t D,
+                        float eps, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
  * Tiled E4M3 quantizer: per (row, tile) scale = max(max(finite |w|, 1e-12) /
  * 448, 1e-12) and code = order[first i with bounds[i] >= n] for n =
  * clamp(nan_to_num(w / scale), -448, 448), code 0 where n == 0.  Replaces the

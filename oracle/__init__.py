@@ -162,6 +162,8 @@ def _load_lib():
         lib.oracle_attn_forward.restype = ctypes.c_int
         lib.oracle_attn_step.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int64] * 3 + [ctypes.c_float]
         lib.oracle_attn_step.restype = ctypes.c_int
+        lib.oracle_attn_backward.argtypes = [ctypes.c_void_p] * 9 + [ctypes.c_int64] * 4 + [ctypes.c_float]
+        lib.oracle_attn_backward.restype = ctypes.c_int
         _lib = lib
     return _lib
 
@@ -364,6 +366,20 @@ def attn_step(S, z, q, k, v, eps=1e-6):
 
 
 _ref_attn_mod = None
+
+
+def attn_backward(dY, Q, K, V, Y, DEN, eps=1e-6):
+    """attn_cpu.cpp attn_backward (:227-368): (dQ, dK, dV) fp32 [B,T,H,D] from
+    the upstream gradient dY, the forward's inputs (K raw) and its Y, DEN."""
+    dYc, Qc, Kc, Vc, Yc, DENc = (t.detach().cpu().float().contiguous() for t in (dY, Q, K, V, Y, DEN))
+    B, T, H, D = Qc.shape
+    dQ, dK, dV = torch.empty_like(Qc), torch.empty_like(Qc), torch.empty_like(Qc)
+    rc = _load_lib().oracle_attn_backward(dYc.data_ptr(), Qc.data_ptr(), Kc.data_ptr(), Vc.data_ptr(), Yc.data_ptr(),
+                                          DENc.data_ptr(), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(), B, T, H, D,
+                                          eps)
+    if rc != 0:
+        raise RuntimeError(f"oracle_attn_backward failed ({rc})")
+    return dQ, dK, dV
 
 
 def ref_attn_module():

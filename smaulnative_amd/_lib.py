@@ -58,6 +58,7 @@ SIGNATURES = {
     "smaul_attn_workspace_size": (_I64, [_I64, _I64, _I64, _I]),
     "smaul_attn_forward": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P]),
     "smaul_attn_step": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_float, _P]),
+    "smaul_attn_backward": (_I, [_P] * 9 + [_I64, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P]),
     "smaul_fp8_quantize_tiles": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P]),
     "smaul_fp8_backward_input": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "smaul_wait_timeouts": (_I, [_P, _I, _P]),

@@ -1,8 +1,9 @@
 // attn.hip -- the linear-attention recurrence of SmaulLinear on MI355X (gfx950).
 //
 // Replaces the reference's native CPU kernels kernel/attn_cpu.cpp
-// (attn_forward :144-212, attn_step :421-492) behind the backend entries
-// attn_forward / attn_step (kernel/compute.py:265-309).  Per (batch, head):
+// (attn_forward :144-212, attn_step :421-492, attn_backward :227-368) behind
+// the backend entries attn_forward / attn_step / attn_backward
+// (kernel/compute.py:265-322).  Per (batch, head):
 //   kn_t = k_t / max(||k_t||, 1e-6)          ||k_t|| accumulated in double
 //   S_t = S_{t-1} + kn_t (x) v_t,  z_t = z_{t-1} + kn_t
 //   num_t = q_t @ S_t,  den_t = max(q_t . z_t, eps),  y_t = num_t / den_t
@@ -206,6 +207,178 @@ attn_step_kernel(float* __restrict__ S, float* __restrict__ z, const float* __re
                    eps, z + o);
 }
 
+// ---------------------------------------------------------------------------
+// backward (attn_cpu.cpp:227-368)
+// ---------------------------------------------------------------------------
+// Per (b, h) task, two passes over time:
+//   A (forward): the recurrence again, then dnum = dy / den, dden = -(dy . y)
+//     / den and dq = S dnum + dden z;
+//   B (reverse): the adjoints Dm of S and dz of z, Dm += dnum (x) q, dz += dden
+//     q, dv = Dm^T kn, dk~ = Dm v + dz, then the key-normalisation backward
+//     dk = dk~ / nc - k (k . dk~) / nc^3 (sums in double).
+// Bit-identical to the reference kernel: every sum runs in its order.  The
+// column sums (num, dv) belong to the thread owning column j and run over i;
+// den, (dy . y) and the double sums are sequential, computed by every thread
+// that needs them (or thread 0); the row sums (dq, dk~) belong to the thread
+// owning row i and run over j the way the reference's 8-lane AVX loop does
+// (dot8_lanes).  The state S / Dm is in LDS for D <= 128 (rows padded to D +
+// 1 floats, so the row walks of consecutive threads fall in different banks),
+// else in the workspace; q/k/v/dy/y are staged CH steps at a time.
+
+// The reference's dot of a row with a vector (attn_cpu.cpp:31-35 and the AVX
+// loops feeding hsum8): lane l sums a[j] * b[j] over j = l, l + 8, ... below
+// the last multiple of 8, from +0; the lanes are added left to right; the
+// remainder follows in order.
+__device__ __forceinline__ float dot8_lanes(const float* a, const float* b, int D) {
+  float acc[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
+  int j = 0;
+  for (; j + 8 <= D; j += 8) {
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[l] = acc[l] + a[j + l] * b[j + l];
+  }
+  float s = acc[0];
+#pragma unroll
+  for (int l = 1; l < 8; ++l) s = s + acc[l];
+  for (; j < D; ++j) s = s + a[j] * b[j];
+  return s;
+}
+
+template <int DMAX, int CH, int NT, bool LDS_STATE>
+__global__ void __launch_bounds__(NT)
+attn_bwd_kernel(const float* __restrict__ dY, const float* __restrict__ Q, const float* __restrict__ K,
+                const float* __restrict__ V, const float* __restrict__ Y, const float* __restrict__ DEN,
+                float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ state_g,
+                int64_t T, int H, int D, float eps) {
+  __shared__ float s_state[LDS_STATE ? DMAX * (DMAX + 1) : 1];
+  __shared__ float s_q[CH][DMAX], s_k[CH][DMAX], s_v[CH][DMAX], s_dy[CH][DMAX], s_y[CH][DMAX];
+  __shared__ float s_kn[DMAX], s_z[DMAX], s_dnum[DMAX], s_t[DMAX];
+  __shared__ float s_inv[CH], s_den[CH], s_sc[2];
+  const int64_t task = blockIdx.x;
+  const int64_t b = task / H, h = task % H;
+  const int tid = threadIdx.x;
+  float* st = LDS_STATE ? s_state : state_g + task * (int64_t)D * D;
+  const int64_t LD = LDS_STATE ? D + 1 : D;
+  const int64_t rs = (int64_t)H * D;         // stride between time steps
+  const int64_t base = (b * T * H + h) * D;  // (b, t = 0, h)
+  auto clear_state = [&]() {
+    for (int64_t e = tid; e < (int64_t)D * LD; e += NT) st[e] = 0.0f;
+    for (int i = tid; i < D; i += NT) s_z[i] = 0.0f;
+  };
+  // steps [t0, t0 + nt) of q/k/v/dy (and y, with_y) into the staging rows,
+  // their key norms' reciprocals (and DEN) alongside
+  auto stage = [&](int64_t t0, int nt, bool with_y) {
+    for (int e = tid; e < nt * D; e += NT) {
+      const int tt = e / D, j = e - tt * D;
+      const int64_t o = base + (t0 + tt) * rs + j;
+      s_q[tt][j] = Q[o];
+      s_k[tt][j] = K[o];
+      s_v[tt][j] = V[o];
+      s_dy[tt][j] = dY[o];
+      if (with_y) s_y[tt][j] = Y[o];
+    }
+    __syncthreads();
+    for (int tt = tid; tt < nt; tt += NT) {
+      s_inv[tt] = attn_inv_norm(s_k[tt], D);
+      if (with_y) s_den[tt] = DEN[(b * T + t0 + tt) * H + h];
+    }
+    __syncthreads();
+  };
+
+  // ---- pass A: dQ ----------------------------------------------------------
+  clear_state();
+  __syncthreads();
+  for (int64_t t0 = 0; t0 < T; t0 += CH) {
+    const int nt = (int)(T - t0 < CH ? T - t0 : CH);
+    stage(t0, nt, false);
+    for (int tt = 0; tt < nt; ++tt) {
+      const int64_t o = base + (t0 + tt) * rs;
+      for (int i = tid; i < D; i += NT) {
+        const float kn = s_k[tt][i] * s_inv[tt];
+        s_kn[i] = kn;
+        s_z[i] = s_z[i] + kn;
+      }
+      __syncthreads();
+      for (int j = tid; j < D; j += NT) {  // column j: S update, num, den
+        const float vj = s_v[tt][j];
+        float num = 0.0f, den = 0.0f;
+        for (int i = 0; i < D; ++i) {
+          const float qi = s_q[tt][i];
+          const float sv = st[i * LD + j] + s_kn[i] * vj;
+          st[i * LD + j] = sv;
+          num = num + qi * sv;
+          den = den + qi * s_z[i];
+        }
+        const float denc = den < eps ? eps : den;
+        s_t[j] = num / denc;                       // y_j
+        s_dnum[j] = s_dy[tt][j] * (1.0f / denc);
+        if (j == 0) s_sc[0] = denc;
+      }
+      __syncthreads();
+      const float inv = 1.0f / s_sc[0];
+      float yd = 0.0f;
+      for (int j = 0; j < D; ++j) yd = yd + s_dy[tt][j] * s_t[j];
+      const float dden = -yd * inv;
+      for (int i = tid; i < D; i += NT)  // row i: dq
+        dQ[o + i] = dot8_lanes(st + i * LD, s_dnum, D) + dden * s_z[i];
+      __syncthreads();
+    }
+  }
+
+  // ---- pass B, reverse in time: dK, dV -----------------------------------
+  clear_state();  // Dm and dz
+  __syncthreads();
+  for (int64_t t1 = T; t1 > 0; t1 -= CH) {
+    const int64_t t0 = t1 - CH > 0 ? t1 - CH : 0;
+    const int nt = (int)(t1 - t0);
+    stage(t0, nt, true);
+    for (int tt = nt - 1; tt >= 0; --tt) {
+      const int64_t o = base + (t0 + tt) * rs;
+      const float invd = 1.0f / s_den[tt];
+      for (int i = tid; i < D; i += NT) {
+        s_kn[i] = s_k[tt][i] * s_inv[tt];
+        s_dnum[i] = s_dy[tt][i] * invd;
+      }
+      __syncthreads();
+      float yd = 0.0f;
+      for (int j = 0; j < D; ++j) yd = yd + s_dy[tt][j] * s_y[tt][j];
+      const float dden = -yd * invd;
+      for (int j = tid; j < D; j += NT) {  // column j: Dm update, dv
+        const float dn = s_dnum[j];
+        float col = 0.0f;
+        for (int i = 0; i < D; ++i) {
+          const float dm = st[i * LD + j] + dn * s_q[tt][i];
+          st[i * LD + j] = dm;
+          col = col + dm * s_kn[i];
+        }
+        dV[o + j] = col;
+      }
+      for (int i = tid; i < D; i += NT) s_z[i] = s_z[i] + dden * s_q[tt][i];  // dz
+      __syncthreads();
+      for (int i = tid; i < D; i += NT) s_t[i] = s_z[i] + dot8_lanes(st + i * LD, s_v[tt], D);  // dk~
+      __syncthreads();
+      if (tid == 0) {
+        double n2 = 0.0, kd = 0.0;
+        for (int i = 0; i < D; ++i) {
+          const double ki = (double)s_k[tt][i];
+          n2 = n2 + ki * ki;
+          kd = kd + ki * (double)s_t[i];
+        }
+        const float n = (float)__builtin_sqrt(n2);
+        const float nc = (!__builtin_isfinite(n) || n < 1e-6f) ? 1e-6f : n;
+        float sc = (float)(kd / ((double)nc * nc * nc));
+        if (!__builtin_isfinite(sc)) sc = 0.0f;
+        s_sc[0] = sc;
+        s_sc[1] = 1.0f / nc;
+      }
+      __syncthreads();
+      for (int i = tid; i < D; i += NT) dK[o + i] = s_t[i] * s_sc[1] - s_k[tt][i] * s_sc[0];
+      __syncthreads();
+    }
+  }
+}
+
 int check_attn_shape(int64_t B, int64_t T, int64_t H, int64_t D, float eps, const char* what) {
   if (B < 0 || T < 0 || H < 0 || D <= 0)
     return fail(SMAUL_ERR_INVALID, "%s: bad shape [%lld,%lld,%lld,%lld]", what, (long long)B, (long long)T,
@@ -272,6 +445,34 @@ int smaul_attn_step(float* S, float* z, const float* q, const float* k, const fl
   hipLaunchKernelGGL(attn_step_kernel, dim3((unsigned)(B * H)), dim3(ATTN_GTHREADS), 0, stream, S, z, q, k, v, y,
                      (int)D, eps);
   return check_launch("attn_step_kernel");
+}
+
+int smaul_attn_backward(const float* dY, const float* Q, const float* K, const float* V, const float* Y,
+                        const float* DEN, float* dQ, float* dK, float* dV, int64_t B, int64_t T, int64_t H, int64_t D,
+                        float eps, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  int rc = check_attn_shape(B, T, H, D, eps, "attn_backward");
+  if (rc) return rc;
+  if (B == 0 || H == 0 || T == 0) return SMAUL_OK;
+  if (!dY || !Q || !K || !V || !Y || !DEN || !dQ || !dK || !dV)
+    return fail(SMAUL_ERR_INVALID, "attn_backward: null pointer");
+  const dim3 grid((unsigned)(B * H));
+  if (D <= 64) {
+    hipLaunchKernelGGL((attn_bwd_kernel<64, 16, 64, true>), grid, dim3(64), 0, stream, dY, Q, K, V, Y, DEN, dQ, dK,
+                       dV, nullptr, T, (int)H, (int)D, eps);
+    return check_launch("attn_bwd_kernel");
+  }
+  if (D <= 128) {
+    hipLaunchKernelGGL((attn_bwd_kernel<128, 16, 128, true>), grid, dim3(128), 0, stream, dY, Q, K, V, Y, DEN, dQ,
+                       dK, dV, nullptr, T, (int)H, (int)D, eps);
+    return check_launch("attn_bwd_kernel");
+  }
+  const int64_t need = smaul_attn_workspace_size(B, H, D, 0);
+  if (workspace_bytes < need || !workspace)
+    return fail(SMAUL_ERR_INVALID, "attn_backward: workspace %lld < %lld bytes", (long long)workspace_bytes,
+                (long long)need);
+  hipLaunchKernelGGL((attn_bwd_kernel<ATTN_DMAX, 1, ATTN_GTHREADS, false>), grid, dim3(ATTN_GTHREADS), 0, stream, dY,
+                     Q, K, V, Y, DEN, dQ, dK, dV, (float*)workspace, T, (int)H, (int)D, eps);
+  return check_launch("attn_bwd_kernel");
 }
 
 }  // extern "C"

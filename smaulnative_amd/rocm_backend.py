@@ -20,9 +20,10 @@ Behaviour differences from the reference CPU backend, all deliberate:
 - ``fp8_quantize_tiles`` quantizes HIP tensors on the device (bit-identical
   codes and scales); for host tensors it returns ``None``, which the contract
   defines as "run the torch quantizer" (compute.py:246-263, fp8_tile.py:96-113);
-- ``fp8_backward_input`` (the FP8Linear input gradient) runs on the device;
-  the attention backward and ``sparse_grad_v`` (Rawr) are not built and
-  raise ``NotImplementedError``.
+- ``fp8_backward_input`` (the FP8Linear input gradient) and ``attn_backward``
+  (the recurrence's two-pass backward, bit-identical to attn_cpu.cpp) run on
+  the device; ``sparse_grad_v`` (Rawr) is not built and raises
+  ``NotImplementedError``.
 """
 from __future__ import annotations
 
@@ -278,7 +279,34 @@ class RocmBackend:
         return y, S, z
 
     def attn_backward(self, dY, Q, K, V, Y, DEN, eps):
-        raise NotImplementedError("rocm backend: attn_backward (training) is not implemented")
+        """(dQ, dK, dV) fp32 [B,T,H,D] of the recurrence (compute.py:314-322,
+        attn_cpu.cpp:227-368, bit-identical), from the upstream gradient dY and
+        the forward's Q, K (raw), V, Y and DEN.  The reference falls back to
+        autograd through its torch recurrence when DEN is missing; here the
+        forward is run again on the device for it, so the kernel is the same."""
+        lib = _lib.load()
+        if DEN is None:
+            Y, DEN = self.attn_forward(Q, K, V, eps, True)[:2]
+        self._attn_check("attn_backward", eps, (dY, Q, K, V, Y, DEN))
+        if Q.dim() != 4 or any(t.shape != Q.shape for t in (K, V, dY, Y)):
+            raise RuntimeError("attn_backward: Q/K/V/dY/Y must be [B,T,H,D] with matching shapes")
+        B, T, H, D = Q.shape
+        if tuple(DEN.shape) != (B, T, H):
+            raise RuntimeError(f"attn_backward: DEN must be [{B},{T},{H}], got {tuple(DEN.shape)}")
+        if D <= 0 or D > 2048:
+            raise RuntimeError(f"attn_backward: D={D} out of the supported range (0, 2048]")
+        dYc, Qc, Kc, Vc, Yc, DENc = (t if t.is_contiguous() else t.contiguous() for t in (dY, Q, K, V, Y, DEN))
+        dev = Q.device
+        dQ, dK, dV = torch.empty_like(Qc), torch.empty_like(Qc), torch.empty_like(Qc)
+        ws_bytes = lib.smaul_attn_workspace_size(B, H, D, 0)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+        with torch.cuda.device(dev):
+            rc = lib.smaul_attn_backward(dYc.data_ptr(), Qc.data_ptr(), Kc.data_ptr(), Vc.data_ptr(), Yc.data_ptr(),
+                                         DENc.data_ptr(), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(), B, T, H, D,
+                                         float(eps), None if ws is None else ws.data_ptr(), ws_bytes,
+                                         _stream_handle(dev))
+        _lib.check(rc, "attn_backward")
+        return dQ, dK, dV
 
     def sparse_grad_v(self, dout, x, cols, values, budget=1 << 22):
         raise NotImplementedError("rocm backend: sparse_grad_v is not implemented")

@@ -138,8 +138,11 @@ def test_backend_surface_and_no_fallback():
         be.fp8_forward(torch.zeros(2, 64), w, s, 64, 8, 64)  # CPU tensors: raise, never fall back
     with pytest.raises(RuntimeError, match="HIP device"):
         be.fp8_backward_input(torch.zeros(2, 8), w, s, 64, 8, 64)  # the device backward, no host fallback
+    q = torch.zeros(1, 2, 1, 8)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        be.attn_backward(q, q, q, q, q, torch.ones(1, 2, 1), 1e-6)  # the device backward, no host fallback
     with pytest.raises(NotImplementedError):
-        be.attn_backward(None, None, None, None, None, None, 1e-6)
+        be.sparse_grad_v(None, None, None, None)
     assert be.fp8_quantize_tiles(torch.zeros(8, 64), 64) is None
 
 

@@ -329,3 +329,73 @@ def test_moe_oracle_matches_reference_layer_in_model(layer):
     assert torch.equal(r.topi, topi) and r.counts == counts
     assert torch.equal(r.prob, prob)
     assert torch.equal(r.out, fx)
+
+
+@pytest.mark.skipif(oracle.ref_attn_module() is None, reason="oracle/_ref (reference attn_cpu.cpp) not built")
+@pytest.mark.parametrize("B,T,H,D", [(2, 37, 3, 64), (1, 5, 2, 13), (1, 24, 2, 128), (1, 3, 1, 200),
+                                     (1, 0, 2, 8), (1, 40, 1, 7), (1, 1, 1, 1)])
+def test_attn_backward_oracle_matches_reference_kernel(B, T, H, D):
+    """The backward (attn_cpu.cpp:227-368) bit-exact against the reference's own
+    kernel (oracle/_ref), including the 8-lane sums of dq and dk and the
+    scalar remainders (D = 13, 7, 1)."""
+    Q, K, V = _attn_inputs(B, T, H, D, B * 977 + T * 13 + D)
+    dY = torch.randn(B, T, H, D, generator=torch.Generator().manual_seed(D + T))
+    Y, DEN, _, _ = oracle.attn_forward(Q, K, V)
+    got = oracle.attn_backward(dY, Q, K, V, Y, DEN)
+    ref = oracle.ref_attn_module().attn_backward(dY, Q, K, V, Y, DEN, 1e-6)
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+
+
+def test_attn_backward_oracle_zero_keys_and_large_eps():
+    """All-zero keys hit the 1e-6 clamp of the key norm (and its guarded
+    nc^3 division); a large eps clamps every den.  Bit-exact with the
+    reference kernel where it is built, finite always."""
+    Q, K, V = _attn_inputs(1, 9, 2, 16, 3)
+    K[:, 2:5] = 0.0
+    dY = torch.randn(1, 9, 2, 16, generator=torch.Generator().manual_seed(4))
+    for eps in (1e-6, 50.0):
+        Y, DEN, _, _ = oracle.attn_forward(Q, K, V, eps)
+        got = oracle.attn_backward(dY, Q, K, V, Y, DEN, eps)
+        assert all(torch.isfinite(g).all() for g in got)
+        ref = oracle.ref_attn_module()
+        if ref is not None:
+            for a, b in zip(got, ref.attn_backward(dY, Q, K, V, Y, DEN, eps)):
+                assert torch.equal(a, b)
+
+
+def test_attn_backward_oracle_vs_autograd_and_planted_mistake():
+    """Within fp32 rounding of autograd (float64) through the textbook
+    recurrence (model.py:199-233); a planted mistake -- the key norm treated
+    as a constant, dropping the normalisation's backward term from dK -- is
+    not."""
+    Q, K, V = _attn_inputs(2, 30, 2, 24, 8)
+    dY = torch.randn(2, 30, 2, 24, generator=torch.Generator().manual_seed(9))
+    Y, DEN, _, _ = oracle.attn_forward(Q, K, V)
+    dQ, dK, dV = oracle.attn_backward(dY, Q, K, V, Y, DEN)
+
+    def grads(detach_norm):
+        q, k, v = (t.double().requires_grad_(True) for t in (Q, K, V))
+        B, T, H, D = q.shape
+        S = torch.zeros(B, H, D, D, dtype=torch.float64)
+        z = torch.zeros(B, H, D, dtype=torch.float64)
+        ys = []
+        for t in range(T):
+            kt = k[:, t]
+            nrm = kt.norm(dim=-1, keepdim=True).clamp_min(1e-6)
+            kt = kt / (nrm.detach() if detach_norm else nrm)
+            S = S + kt.unsqueeze(-1) @ v[:, t].unsqueeze(-2)
+            z = z + kt
+            num = (q[:, t].unsqueeze(-2) @ S).squeeze(-2)
+            den = (q[:, t] * z).sum(-1, keepdim=True).clamp_min(1e-6)
+            ys.append(num / den)
+        torch.stack(ys, 1).backward(dY.double())
+        return q.grad, k.grad, v.grad
+
+    def rel(a, b):
+        return float((a.double() - b).abs().max() / b.abs().max())
+    ref = grads(False)
+    for a, b in zip((dQ, dK, dV), ref):
+        assert rel(a, b) < 1e-4
+    planted = grads(True)
+    assert rel(dK, planted[1]) > 1e-2
