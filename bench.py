@@ -2,6 +2,7 @@
 """MoE-layer benchmark on one MI355X (BASELINE.json metric).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--no-c5] [--no-c2]
+    python bench.py --peaks      (only the measured MFMA and HBM ceilings)
 
 Headline (``value``): tokens/s of one SmaulMoE layer at config 3 -- prefill,
 T=16384 tokens, d=1024, expert hidden h=2560, E=8 experts, top-2, tile 64,
@@ -466,6 +467,44 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
             "sync_timeouts": timeouts}, (lay, x0)
 
 
+def peaks():
+    """Measured ceilings: the dense bf16 MFMA rate of v_mfma_f32_32x32x16_bf16
+    (smaul_peak_mfma: 8 independent chains per wave, 1 and 2 waves per SIMD)
+    and the HBM read rate of 16-byte loads over a 4 GiB buffer, far beyond the
+    256 MB Infinity Cache (smaul_peak_stream).  Median of 10 after 3 warm-ups,
+    HIP events on the launch stream."""
+    import torch
+    from smaulnative_amd import _lib
+    lib = _lib.load()
+    dev = torch.device("cuda")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    st = torch.cuda.current_stream(dev).cuda_stream
+    res = {"cus": cus}
+    iters = 4096
+    best = 0.0
+    for per_cu in (1, 2):  # workgroups of 4 waves per CU: 1 or 2 waves per SIMD
+        wg = cus * per_cu
+        out = torch.empty(wg * 4, dtype=torch.float32, device=dev)
+        ms = event_median_ms(lambda: _lib.check(lib.smaul_peak_mfma(out.data_ptr(), wg, iters, st), "peak_mfma"),
+                             10, 3)
+        tf = wg * 4 * iters * 8 * 32768.0 / (ms * 1e-3) / 1e12
+        res[f"mfma_bf16_tflops_{per_cu}_waves_per_simd"] = tf
+        best = max(best, tf)
+    res["mfma_bf16_tflops"] = best
+    res["mfma_frac_of_2500"] = best / 2500.0
+    nbytes = 4 << 30
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    ms = event_median_ms(lambda: _lib.check(lib.smaul_peak_stream(buf.data_ptr(), nbytes, sink.data_ptr(), cus * 8,
+                                                                  st), "peak_stream"), 10, 3)
+    res["hbm_read_GBps"] = nbytes / (ms * 1e-3) / 1e9
+    res["hbm_frac_of_8000"] = res["hbm_read_GBps"] / 8000.0
+    res["method"] = ("median of 10 launches after 3 warm-ups, HIP events on the launch stream; MFMA: 4096 rounds "
+                     "of 8 independent 32x32x16 bf16 MFMAs per wave; HBM: a 4 GiB read with 16-byte loads, "
+                     f"{cus * 8} workgroups of 256 threads")
+    return res
+
+
 def read_traffic():
     """HBM bytes per gate_up launch from the committed rocprofv3 --pmc summary, if any."""
     p = os.path.join(HERE, "profiles", "moe_kernels_hbm_traffic.txt")
@@ -489,6 +528,9 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-c5", action="store_true")
     ap.add_argument("--no-c2", action="store_true")
+    ap.add_argument("--peaks", action="store_true",
+                    help="only measure the MFMA and HBM-read ceilings (smaul_peak_mfma / smaul_peak_stream), "
+                         "print them as one JSON line and exit")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 3 device-to-device copies of BYTES (calibrates rocprofv3 "
                          "FETCH_SIZE/WRITE_SIZE against a kernel of known traffic), then exit")
@@ -501,6 +543,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": src.numel() * 4}), flush=True)
+        return
+    if args.peaks:
+        sys.path.insert(0, HERE)
+        print(json.dumps({"peaks": peaks()}), flush=True)
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -405,6 +405,19 @@ int smaul_fp8_backward_input(const float* g, const uint8_t* w, const float* s, f
                              int64_t in_f, int64_t out_f, int64_t tile, hipStream_t stream);
 
 /*
+ * Measured ceilings for the roofline figures (bench.py --peaks); no
+ * counterpart in the reference and not on the MoE path.
+ * smaul_peak_mfma: `workgroups` x 4 waves, each issuing `iters` rounds of 8
+ *   independent v_mfma_f32_32x32x16_bf16 (32768 flop each); out holds one
+ *   float per wave.
+ * smaul_peak_stream: reads `bytes` (a multiple of 16) from src with 16-byte
+ *   loads, grid-stride over `workgroups` x 256 threads; out (one uint32) is
+ *   written only in a case that does not occur.
+ */
+int smaul_peak_mfma(float* out, int workgroups, int iters, hipStream_t stream);
+int smaul_peak_stream(const void* src, int64_t bytes, uint32_t* out, int workgroups, hipStream_t stream);
+
+/*
  * Host-side self-test of the top-k selection order used by the router (no GPU
  * involved): writes the k indices the router would select for `vals` [n].
  * Exposed only so the CPU test suite can check the order against torch.topk.

@@ -63,6 +63,8 @@ SIGNATURES = {
     "smaul_fp8_backward_input": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "smaul_wait_timeouts": (_I, [_P, _I, _P]),
     "smaul_debug_tail_wait": (_I, [_I, _I]),
+    "smaul_peak_mfma": (_I, [_P, _I, _I, _P]),
+    "smaul_peak_stream": (_I, [_P, _I64, _P, _I, _P]),
     "smaul_selftest_topk": (_I, [_P, _I64, _I64, _P]),
 }
 

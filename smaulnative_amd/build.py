@@ -23,7 +23,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
-SOURCES = [os.path.join(CSRC, n) for n in ("smaul_rocm.hip", "attn.hip", "quant.hip", "backward.hip")]
+SOURCES = [os.path.join(CSRC, n) for n in ("smaul_rocm.hip", "attn.hip", "quant.hip", "backward.hip", "peaks.hip")]
 OUT = os.path.join(HERE, "libsmaul_rocm.so")
 OBJDIR = os.path.join(HERE, "_build")
 
