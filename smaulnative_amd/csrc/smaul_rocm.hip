@@ -695,12 +695,12 @@ struct DmaGemmCfg {
   static constexpr int B_INS = B_BYTES / 1024 / NW;
   static constexpr int S_INS = BN / 64;                  // 256 B scale DMAs per stage, waves 0..S_INS-1
   static constexpr int DMA_MIN = A_INS + B_INS;          // DMAs per stage issued by every wave
-  static constexpr int OUT_LD = BNO + 8;                 // epilogue LDS row (bf16 elements)
   // Row tiles per L2 group of the tile order (the remap below): gate/up walks
   // 4 row tiles x all column tiles, down 8 (measured best for each at the
   // C5 shape, d = 2048 / h = 5120, and no different at C3).
   static constexpr int GM = SWIGLU ? 4 : GROUP_M;
-  static constexpr int LDS = (NSTAGE * STAGE > BM * OUT_LD * 2) ? NSTAGE * STAGE : BM * OUT_LD * 2;
+  static constexpr int OUT_LD = BNO + 8;                 // plain epilogue LDS row (bf16 elements)
+  static constexpr int LDS = (SWIGLU || NSTAGE * STAGE > BM * OUT_LD * 2) ? NSTAGE * STAGE : BM * OUT_LD * 2;
   static_assert(TM % 32 == 0 && TNO % 32 == 0, "wave tile must be a multiple of 32");
   static_assert(A_INS >= 1 && A_BYTES % (1024 * NW) == 0, "A staging split");
   static_assert(B_INS >= 1 && B_BYTES % (1024 * NW) == 0, "B staging split");
@@ -712,7 +712,8 @@ struct DmaGemmCfg {
 
 // OUT_F32 (not SWIGLU): the fp32 sums are stored as they are (the dense
 // fp8_forward contract), straight from the MFMA layout; otherwise they are
-// rounded to bf16 and stored through LDS.
+// rounded to bf16 and stored through LDS (plain) or, with the SwiGLU
+// epilogue, as 8-byte row pieces after an exchange inside each quad of lanes.
 template <int BM, int BN, int WM, int WN, int NSTAGE, bool SWIGLU, bool CANON, bool REMAP, bool OUT_F32 = false>
 __global__ void __launch_bounds__(WM * WN * 64, 2)
 fp8_gemm_dma_kernel(GemmArgs p) {
@@ -952,46 +953,88 @@ fp8_gemm_dma_kernel(GemmArgs p) {
         }
     return;
   }
-  __syncthreads();  // every wave is done with the stage buffers
 
-  // ---- epilogue: through LDS, then 16-byte row stores ----------------------
+  if constexpr (!SWIGLU) {
+    // ---- plain epilogue: through LDS, then 16-byte row stores ---------------
+    // (measured faster than the register exchange below for 256 outputs per
+    // workgroup: half as many store instructions, whole 512-byte rows)
+    // A lane holds column l32 of each 32x32 tile, rows (r/4)*8 + g*4 + r%4;
+    // the tile is rounded to bf16, written to LDS as [row][col] and stored
+    // row by row.
+    __syncthreads();  // every wave is done with the stage buffers
+    constexpr int OUT_LD = C::OUT_LD;
+    uint16_t* so = (uint16_t*)smem;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int j = 0; j < FNO; ++j) {
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const uint32_t o = pack_bf16(acc[i][j][r], acc[i][j][r + 1]);
+          const int lr = wm * TM + i * 32 + (r >> 2) * 8 + g * 4 + (r & 3);  // r even: rows lr, lr+1
+          const int lc = wn * TNO + j * 32 + l32;
+          so[lr * OUT_LD + lc] = (uint16_t)(o & 0xffffu);
+          so[(lr + 1) * OUT_LD + lc] = (uint16_t)(o >> 16);
+        }
+      }
+    }
+    __syncthreads();
+    constexpr int CPR = BNO / 8;  // 16-byte chunks per output row
+    for (int c = tid; c < BM * CPR; c += NW * 64) {
+      const int row = c / CPR, ch = c - row * CPR;
+      if (row < rows_here)
+        *(uint4*)((uint16_t*)p.y + (int64_t)(row0 + row) * p.ldy + n0 + ch * 8) =
+            *(const uint4*)(so + row * OUT_LD + ch * 8);
+    }
+    return;
+  }
+
+  // ---- SwiGLU epilogue: bf16 rows stored from registers ---------------------
   // A lane holds column l32 of each 32x32 tile, rows (r/4)*8 + g*4 + r%4.
-  // The tile is rounded to bf16 (SwiGLU: gate and up rounded first, as the
-  // reference's FP8Linear outputs are, then silu(gate)*up rounded again),
-  // written to LDS as [row][col] and stored row by row.
-  constexpr int OUT_LD = C::OUT_LD;
-  uint16_t* so = (uint16_t*)smem;
+  // Gate and up are rounded to bf16 first, as the reference's FP8Linear
+  // outputs are, then silu(gate)*up is rounded again.  Two exchanges inside
+  // each quad of lanes (DPP quad permutes, no LDS, no barrier) turn a lane's
+  // four rows x one column into one row x four columns: lane 4m+s ends with
+  // row (r/4)*8 + g*4 + s, columns 4m..4m+3, so the 8 lanes of a row store 64
+  // contiguous bytes and the WN waves complete the row.
+  const int qs = lane & 3;
+  const bool hi2 = (lane & 2) != 0;
+  // v_perm selectors for the lane ^ 1 step (src0 = partner, src1 = own):
+  // even lanes take own bytes 0-1 then partner bytes 0-1, odd lanes partner
+  // bytes 2-3 then own bytes 2-3
+  const uint32_t psel = (lane & 1) ? 0x03020706u : 0x05040100u;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
 #pragma unroll
     for (int j = 0; j < FNO; ++j) {
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        float v0, v1;
-        if constexpr (SWIGLU) {
-          const uint32_t gb = pack_bf16(acc[i][j][r], acc[i][j][r + 1]);
-          const uint32_t ub = pack_bf16(acc[i][j + FNO][r], acc[i][j + FNO][r + 1]);
-          v0 = silu_f(bf2f(gb & 0xffffu)) * bf2f(ub & 0xffffu);
-          v1 = silu_f(bf2f(gb >> 16)) * bf2f(ub >> 16);
-        } else {
-          v0 = acc[i][j][r];
-          v1 = acc[i][j][r + 1];
+      for (int a = 0; a < 4; ++a) {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = a * 4 + q;
+          const uint32_t gu = pack_bf16(acc[i][j][r], acc[i][j + FNO][r]);  // gate, up rounded to bf16
+          const float gr = __builtin_bit_cast(float, gu << 16);
+          const float ur = __builtin_bit_cast(float, gu & 0xffff0000u);
+          v[q] = silu_f(gr) * ur;
         }
-        const uint32_t o = pack_bf16(v0, v1);
-        const int lr = wm * TM + i * 32 + (r >> 2) * 8 + g * 4 + (r & 3);  // r even: rows lr, lr+1
-        const int lc = wn * TNO + j * 32 + l32;
-        so[lr * OUT_LD + lc] = (uint16_t)(o & 0xffffu);
-        so[(lr + 1) * OUT_LD + lc] = (uint16_t)(o >> 16);
+        const uint32_t d0 = pack_bf16(v[0], v[1]);  // rows +0 (low half), +1 (high half), column l32
+        const uint32_t d1 = pack_bf16(v[2], v[3]);  // rows +2, +3
+        // lane ^ 1: even lanes take rows +0 / +2 of columns (c, c+1), odd
+        // lanes rows +1 / +3 of columns (c-1, c)
+        const uint32_t e0 =
+            __builtin_amdgcn_perm((uint32_t)__builtin_amdgcn_mov_dpp((int)d0, 0xB1, 0xF, 0xF, false), d0, psel);
+        const uint32_t e1 =
+            __builtin_amdgcn_perm((uint32_t)__builtin_amdgcn_mov_dpp((int)d1, 0xB1, 0xF, 0xF, false), d1, psel);
+        // lane ^ 2: lanes s < 2 keep row +s (e0) and take columns 4m+2..4m+3
+        // of it; lanes s >= 2 keep row +s (e1) and take columns 4m..4m+1
+        const uint32_t rv = (uint32_t)__builtin_amdgcn_mov_dpp((int)(hi2 ? e0 : e1), 0x4E, 0xF, 0xF, false);
+        const uint2 o = make_uint2(hi2 ? rv : e0, hi2 ? e1 : rv);
+        const int lr = wm * TM + i * 32 + a * 8 + g * 4 + qs;
+        if (lr < rows_here)
+          *(uint2*)((uint16_t*)p.y + (int64_t)(row0 + lr) * p.ldy + n0 + wn * TNO + j * 32 + (l32 & ~3)) = o;
       }
     }
-  }
-  __syncthreads();
-  constexpr int CPR = BNO / 8;  // 16-byte chunks per output row
-  for (int c = tid; c < BM * CPR; c += NW * 64) {
-    const int row = c / CPR, ch = c - row * CPR;
-    if (row < rows_here)
-      *(uint4*)((uint16_t*)p.y + (int64_t)(row0 + row) * p.ldy + n0 + ch * 8) =
-          *(const uint4*)(so + row * OUT_LD + ch * 8);
   }
 }
 
@@ -3819,11 +3862,13 @@ int launch_dense_dma(const GemmArgs& a, int tile, hipStream_t stream) {
 
 // The LDS-DMA kernel needs bf16 activations, 64-wide scale tiles, K a
 // multiple of 64, N a multiple of the workgroup's output columns, 16-byte
-// aligned code rows and activation rows, and byte offsets that fit its 32-bit
-// per-lane offsets.
+// aligned code rows and activation rows, 8-byte aligned output row pieces (its
+// epilogue stores four bf16 columns at a time), and byte offsets that fit its
+// 32-bit per-lane offsets.
 bool dma_gemm_ok(const GemmArgs& a, int act_dtype, int flags, int64_t x_rows, int64_t bno) {
   if (act_dtype != SMAUL_DTYPE_BF16 || a.tile != 64 || (a.K & 63) != 0 || a.N % bno != 0) return false;
   if (!(flags & SMAUL_FLAG_ALIGNED_CODES) || !aligned16(a.x) || (a.ldx & 7) != 0) return false;
+  if (((uintptr_t)a.y & 7u) != 0 || (a.ldy & 3) != 0) return false;
   const int64_t lim = (int64_t)1 << 31;
   return x_rows * a.ldx * 2 < lim && a.N * a.K < lim && a.N * a.nt < lim;
 }
