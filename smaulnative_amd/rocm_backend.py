@@ -76,30 +76,40 @@ class RocmBackend:
         self._ptr_cache: dict = {}
 
     # ---- compute.py:77-103 ------------------------------------------------
-    def configure(self, threads=None):
-        """Host thread count for torch's CPU-side work; same rules as the reference."""
+    @staticmethod
+    def _resolve_threads(threads):
+        """An explicit count wins, then SMAUL_CPU_THREADS, then half the host's cores
+        (at least one); a value that is not a number raises ValueError."""
+        env = os.environ.get("SMAUL_CPU_THREADS")
+        if threads is None and env:
+            source, threads, parse = "SMAUL_CPU_THREADS", env, lambda v: int(float(v))  # "4.0" is accepted
+        else:
+            source, parse = "threads", int
         if threads is None:
-            env = os.environ.get("SMAUL_CPU_THREADS")
-            if env:
-                try:
-                    threads = int(float(env))
-                except (TypeError, ValueError):
-                    raise ValueError(f"SMAUL_CPU_THREADS must be an integer, got {env!r}")
-            else:
-                threads = max(1, (os.cpu_count() or 2) // 2)
+            return max(1, (os.cpu_count() or 2) // 2)
         try:
-            threads = int(threads)
+            n = parse(threads)
         except (TypeError, ValueError):
-            raise ValueError(f"threads must be an integer, got {threads!r}")
-        threads = max(1, threads)
-        os.environ["OMP_NUM_THREADS"] = str(threads)
-        os.environ["MKL_NUM_THREADS"] = str(threads)
-        torch.set_num_threads(threads)
+            raise ValueError(f"{source}: expected a whole number of threads, got {threads!r}") from None
+        return max(1, n)
+
+    def configure(self, threads=None):
+        """Set the host thread count for torch's CPU-side work and return it.
+
+        The device path does not use host threads; this keeps the backend
+        interface whole (train.py and benchmark.py call it).  OMP/MKL variables
+        are overwritten, not defaulted, so an explicit count beats a stale
+        exported value for native code loaded afterwards.
+        """
+        n = self._resolve_threads(threads)
+        for var in ("OMP_NUM_THREADS", "MKL_NUM_THREADS"):
+            os.environ[var] = str(n)
+        torch.set_num_threads(n)
         try:
             torch.set_num_interop_threads(1)
-        except RuntimeError:
+        except RuntimeError:  # already fixed once torch has run parallel work
             pass
-        return threads
+        return n
 
     @property
     def has_native(self):
