@@ -71,6 +71,24 @@ int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* 
                      int64_t tile, int flags, hipStream_t stream);
 
 /*
+ * smaul_fp8_linear with a caller workspace, for fp32 x (what the reference's
+ * FP8Linear passes, kernel/fp8_tile.py:168; same reference entry as
+ * smaul_fp8_linear: kernel/compute.py:125-135, kernel/fp8_cpu.cpp:100-141).
+ * With fp32 x, tile 64, in_f a multiple of 64, rows > 64 and 16-byte aligned
+ * x / w / workspace, x is split into bf16 hi and lo planes in the workspace
+ * (x = hi + lo within 2^-18 |x|) and the LDS-DMA GEMM runs over both planes
+ * (fp32 sums of exact bf16 x E4M3 products, per-tile scales applied per
+ * plane).  Otherwise, or with a workspace smaller than
+ * smaul_fp8_linear_workspace_size, it is smaul_fp8_linear.  Same arguments,
+ * results and errors as smaul_fp8_linear within fp32 summation order.
+ */
+int64_t smaul_fp8_linear_workspace_size(int64_t rows, int64_t in_f, int x_dtype);
+int smaul_fp8_linear_ws(const void* x, int x_dtype, const uint8_t* w, const float* s,
+                        void* y, int y_dtype, int64_t rows, int64_t in_f, int64_t out_f,
+                        int64_t tile, int flags, void* workspace, int64_t workspace_bytes,
+                        hipStream_t stream);
+
+/*
  * Device repack cache of the codes: out = codes with 0x7F -> 0x7E and
  * 0xFF -> 0xFE (the same values, +-448, in the reference codebook
  * kernel/fp8_tile.py:43-44; 0x7F/0xFF are NaN in the OCP E4M3FN encoding the

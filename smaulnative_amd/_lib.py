@@ -32,6 +32,8 @@ SIGNATURES = {
     "smaul_version": (_I, []),
     "smaul_last_error": (ctypes.c_char_p, []),
     "smaul_fp8_linear": (_I, [_P, _I, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I, _P]),
+    "smaul_fp8_linear_workspace_size": (_I64, [_I64, _I64, _I]),
+    "smaul_fp8_linear_ws": (_I, [_P, _I, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I, _P, _I64, _P]),
     "smaul_fp8_canonicalize": (_I, [_P, _P, _I64, _P]),
     "smaul_fp8_tile_layout": (_I, [_P, _P, _P, _P, _I64, _I64, _P]),
     "smaul_moe_router": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),

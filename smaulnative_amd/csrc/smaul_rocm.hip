@@ -154,6 +154,11 @@ struct GemmArgs {
   int64_t R;
   int E;
   int tiled;                   // codes/scales in the tiled layout (SMAUL_FLAG_TILED_LAYOUT)
+  // Weight K blocks when the activations carry two K planes (the LDS-DMA
+  // GEMM of fp32 x split into bf16 hi and lo halves, K = 2 * kw): stage kt
+  // reads activation block kt and weight / scale block kt mod (kw / 64).
+  // 0: the weights span K.
+  int64_t kw;
 };
 
 // Where an expert's codes and scales for column n and 64-wide K block kb
@@ -166,7 +171,7 @@ struct WLayout {
   int64_t wc, wk, sc, sk;
 };
 __device__ __forceinline__ WLayout wlayout(const GemmArgs& p) {
-  return p.tiled ? WLayout{64, p.N * 64, 1, p.N} : WLayout{p.K, 64, p.nt, 1};
+  return p.tiled ? WLayout{64, p.N * 64, 1, p.N} : WLayout{p.kw ? p.kw : p.K, 64, p.nt, 1};
 }
 
 // The expert segment of m-tile mt of a grouped GEMM, with all of its loads
@@ -809,14 +814,16 @@ fp8_gemm_dma_kernel(GemmArgs p) {
   // per-lane offsets stay fixed.  Every wave issues DMA_MIN = A_INS + B_INS
   // loads per stage, waves < S_INS one more (the scales, issued first).
   const uint32_t lds0 = lds_offset(&smem[0]);
+  const int kwb = (int)(p.kw >> 6);  // weight K blocks of a two-plane activation (0: none)
   auto dma_stage = [&](int kt, int buf) {
     const uint32_t lbase = lds0 + (uint32_t)(buf * STAGE);
-    if (S_INS == NW || wave < S_INS) dma4(s_src + kt * L.sk, s_off, lbase + A_BYTES + B_BYTES + wave * 256);
+    const int kb = kt >= kwb && kwb > 0 ? kt - kwb : kt;  // the weight block of activation block kt
+    if (S_INS == NW || wave < S_INS) dma4(s_src + kb * L.sk, s_off, lbase + A_BYTES + B_BYTES + wave * 256);
     const char* xa = (const char*)p.x + kt * 128;
 #pragma unroll
     for (int a = 0; a < A_INS; ++a) dma16(xa, a_off[a], lbase + (wave * A_INS + a) * 1024);
 #pragma unroll
-    for (int b = 0; b < B_INS; ++b) dma16(b_src(b) + kt * L.wk, b_off, lbase + A_BYTES + (wave * B_INS + b) * 1024);
+    for (int b = 0; b < B_INS; ++b) dma16(b_src(b) + kb * L.wk, b_off, lbase + A_BYTES + (wave * B_INS + b) * 1024);
   };
 
   // ---- fragment addresses (fixed over K) -----------------------------------
@@ -3967,6 +3974,81 @@ int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* 
   const int64_t mt = (rows + bm - 1) / bm;
   return small ? gemm_dispatch_dense<CfgSmall, 2>(a, vec, canon, mt, stream)
                : gemm_dispatch_dense<CfgBigF32, 2>(a, vec, canon, mt, stream);
+}
+
+namespace {
+
+// fp32 activations -> two bf16 planes side by side (split_bf16): out row r
+// holds hi(x[r, :]) in columns [0, K) and lo(x[r, :]) in [K, 2K).  One thread
+// per 8 consecutive values: two 16-byte loads, one 16-byte store per plane.
+__global__ void __launch_bounds__(256) split_planes_kernel(const float* __restrict__ x, uint16_t* __restrict__ out,
+                                                           int64_t rows, int64_t K) {
+  const int64_t per_row = K >> 3;
+  const int64_t n = rows * per_row;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / per_row, c = (i - r * per_row) * 8;
+    const float4 v0 = *(const float4*)(x + r * K + c);
+    const float4 v1 = *(const float4*)(x + r * K + c + 4);
+    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    uint32_t h[8], l[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) split_bf16(v[q], h[q], l[q]);
+    uint16_t* o = out + r * 2 * K + c;
+    *(uint4*)o = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+    *(uint4*)(o + K) = make_uint4(l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16));
+  }
+}
+
+// The two-plane LDS-DMA path of smaul_fp8_linear_ws applies (fp32 x, tile
+// 64, shapes the DMA GEMM takes): the dense tile, else -1.
+int planes_tile(int x_dtype, const void* x, const uint8_t* w, int64_t rows, int64_t in_f, int64_t out_f,
+                int64_t tile, int flags) {
+  if (x_dtype != SMAUL_DTYPE_F32 || tile != 64 || rows <= 64 || in_f % 64 != 0) return -1;
+  if ((flags & SMAUL_FLAG_TILED_LAYOUT) || !aligned16(x) || !aligned16(w) || in_f % 16 != 0) return -1;
+  return pick_dense_tile(false, rows, out_f);
+}
+
+}  // namespace
+
+int64_t smaul_fp8_linear_workspace_size(int64_t rows, int64_t in_f, int x_dtype) {
+  if (rows < 0 || in_f < 0) return -1;
+  return x_dtype == SMAUL_DTYPE_F32 ? rows * in_f * 4 : 0;
+}
+
+int smaul_fp8_linear_ws(const void* x, int x_dtype, const uint8_t* w, const float* s, void* y, int y_dtype,
+                        int64_t rows, int64_t in_f, int64_t out_f, int64_t tile, int flags, void* workspace,
+                        int64_t workspace_bytes, hipStream_t stream) {
+  const int dt = (rows > 0 && y && s && y_dtype == SMAUL_DTYPE_F32 && kmode_of(tile) >= 0)
+                     ? planes_tile(x_dtype, x, w, rows, in_f, out_f, tile, flags)
+                     : -1;
+  if (dt < 0 || !workspace || !aligned16(workspace) ||
+      workspace_bytes < smaul_fp8_linear_workspace_size(rows, in_f, x_dtype))
+    return smaul_fp8_linear(x, x_dtype, w, s, y, y_dtype, rows, in_f, out_f, tile, flags, stream);
+  GemmArgs a{};
+  a.x = workspace;  // [rows][2 * in_f] bf16: hi plane, then lo plane
+  a.row_idx = nullptr;
+  a.ldx = 2 * in_f;
+  a.w = w;
+  a.s = s;
+  a.y = y;
+  a.ldy = out_f;
+  a.K = 2 * in_f;
+  a.kw = in_f;
+  a.N = out_f;
+  a.nt = in_f / 64;
+  a.tile = 64;
+  a.R = rows;
+  a.E = 1;
+  if (!dma_gemm_ok(a, SMAUL_DTYPE_BF16, flags | SMAUL_FLAG_ALIGNED_CODES, rows, 128))
+    return smaul_fp8_linear(x, x_dtype, w, s, y, y_dtype, rows, in_f, out_f, tile, flags, stream);
+  const int64_t n8 = rows * (in_f / 8);
+  const int64_t blocks = std::min<int64_t>((n8 + 255) / 256, 4096);
+  hipLaunchKernelGGL(split_planes_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (const float*)x,
+                     (uint16_t*)workspace, rows, in_f);
+  const int rc = check_launch("split_planes_kernel");
+  if (rc != SMAUL_OK) return rc;
+  const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
+  return canon ? launch_dense_dma<false, true, true>(a, dt, stream) : launch_dense_dma<false, false, true>(a, dt, stream);
 }
 
 // router launch shape for E experts: (tokens per wave, expert register width)

@@ -156,10 +156,15 @@ class RocmBackend:
         y = torch.empty(rows, out_f, dtype=torch.float32, device=x.device)
         if rows == 0:
             return y
+        # fp32 x (what FP8Linear passes) goes through a workspace of bf16 hi/lo
+        # planes so the LDS-DMA GEMM can take it; bf16 x needs none
+        nws = lib.smaul_fp8_linear_workspace_size(rows, in_f, _ACT[xc.dtype])
+        ws = torch.empty(max(nws, 0), dtype=torch.uint8, device=x.device) if nws > 0 else None
         with torch.cuda.device(x.device):
-            rc = lib.smaul_fp8_linear(xc.data_ptr(), _ACT[xc.dtype], wc.data_ptr(), sc.data_ptr(),
-                                      y.data_ptr(), _lib.DTYPE_F32, rows, in_f, out_f, tile, 0,
-                                      _stream_handle(x.device))
+            rc = lib.smaul_fp8_linear_ws(xc.data_ptr(), _ACT[xc.dtype], wc.data_ptr(), sc.data_ptr(),
+                                         y.data_ptr(), _lib.DTYPE_F32, rows, in_f, out_f, tile, 0,
+                                         None if ws is None else ws.data_ptr(), max(nws, 0),
+                                         _stream_handle(x.device))
         _lib.check(rc, "fp8_forward")
         return y
 

@@ -134,6 +134,71 @@ def test_fp8_linear_bf16_dma_tiles(rows, in_f, out_f, raw_codes):
     assert rel_max(y[idx], ref) < 2e-6, rel_max(y[idx], ref)
 
 
+@pytest.mark.parametrize("rows,in_f,out_f,tile", [
+    (4096, 512, 1280, 64),      # C2 gate: two bf16 planes through the 64x128 DMA tiles
+    (4096, 1280, 512, 64),      # C2 down: 32x128 tiles
+    (300, 256, 384, 64),        # ragged last row tile
+    (2048, 1024, 2560, 64),     # 128x256 tiles
+    (64, 512, 256, 64),         # rows <= 64: the register-staged split kernel
+    (512, 256, 200, 64),        # out_f not a multiple of 128: register-staged
+    (300, 384, 256, 128),       # tile 128: register-staged
+])
+def test_fp8_linear_fp32_two_planes(rows, in_f, out_f, tile):
+    """fp32 x (what FP8Linear passes) through fp8_forward: split into bf16 hi and
+    lo planes in the workspace and run by the LDS-DMA GEMM over both planes, or
+    the register-staged kernel where the shape does not fit it.  Rows sampled
+    against the oracle at the fp32-input bar (test_linear_fp8.py:170-183)."""
+    print(f"case fp8_linear fp32 rows={rows} in_f={in_f} out_f={out_f} tile={tile}", flush=True)
+    gen = torch.Generator().manual_seed(rows * 5 + in_f + out_f * 7 + tile)
+    x = torch.randn(rows, in_f, generator=gen)
+    x[0, :7] = torch.tensor([0.0, -0.0, 1e-30, -3e4, 2.0 ** -133, 1.0 + 2.0 ** -20, 65504.0])
+    w, s = oracle.quantize_tiles(torch.randn(out_f, in_f, generator=gen) * 0.02, tile)
+    y = be().fp8_forward(x.to(DEV), w.to(DEV), s.to(DEV), in_f, out_f, tile).cpu()
+    idx = torch.cat([torch.arange(0, min(rows, 96)), torch.arange(rows // 2, min(rows, rows // 2 + 33)),
+                     torch.arange(max(0, rows - 65), rows)]).unique()
+    ref = oracle.fp8_forward(x[idx], w, s, in_f, out_f, tile)
+    assert torch.isfinite(y).all()
+    assert rel_max(y[idx], ref) < 1e-5, rel_max(y[idx], ref)
+
+
+def test_fp8_linear_ws_abi_fallbacks():
+    """smaul_fp8_linear_ws through the C-ABI: the two-plane path with a large
+    enough workspace and smaul_fp8_linear itself without one (or one too
+    small), both within the fp32-input bar of the oracle; bf16 x needs no
+    workspace; the size query."""
+    from smaulnative_amd import _lib
+    lib = _lib.load()
+    rows, in_f, out_f = 1024, 512, 384
+    assert lib.smaul_fp8_linear_workspace_size(rows, in_f, _lib.DTYPE_F32) == rows * in_f * 4
+    assert lib.smaul_fp8_linear_workspace_size(rows, in_f, _lib.DTYPE_BF16) == 0
+    assert lib.smaul_fp8_linear_workspace_size(-1, in_f, _lib.DTYPE_F32) == -1
+    gen = torch.Generator().manual_seed(77)
+    x = torch.randn(rows, in_f, generator=gen)
+    w, s = oracle.quantize_tiles(torch.randn(out_f, in_f, generator=gen) * 0.02, 64)
+    ref = oracle.fp8_forward(x[:80], w, s, in_f, out_f, 64)
+    xd, wd, sd = x.to(DEV), w.to(DEV), s.to(DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for nbytes in (rows * in_f * 4, rows * in_f * 4 - 16, 0):
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=DEV)
+        y = torch.full((rows, out_f), float("nan"), device=DEV)
+        rc = lib.smaul_fp8_linear_ws(xd.data_ptr(), _lib.DTYPE_F32, wd.data_ptr(), sd.data_ptr(), y.data_ptr(),
+                                     _lib.DTYPE_F32, rows, in_f, out_f, 64, 0,
+                                     ws.data_ptr() if nbytes else None, nbytes, stream)
+        assert rc == _lib.SMAUL_OK, _lib.last_error()
+        torch.cuda.synchronize()
+        assert torch.isfinite(y).all()
+        assert rel_max(y[:80].cpu(), ref) < 1e-5
+        outs.append(y.cpu())
+    # the two fallbacks are the same kernel
+    assert torch.equal(outs[1], outs[2])
+    assert rel_max(outs[0], outs[2]) < 1e-5
+    # a bad argument is reported as by smaul_fp8_linear
+    rc = lib.smaul_fp8_linear_ws(xd.data_ptr(), _lib.DTYPE_F32, wd.data_ptr(), sd.data_ptr(), None,
+                                 _lib.DTYPE_F32, rows, in_f, out_f, 64, 0, None, 0, stream)
+    assert rc == _lib.SMAUL_ERR_INVALID
+
+
 def test_fp8_linear_special_codes():
     # every one of the 256 codes, including 0x7F/0xFF (+-448, NaN in OCP),
     # 0x80 (-0) and the subnormals, against the reference codebook
