@@ -139,6 +139,7 @@ def test_fp8_linear_bf16_dma_tiles(rows, in_f, out_f, raw_codes):
     (4096, 1280, 512, 64),      # C2 down: 32x128 tiles
     (300, 256, 384, 64),        # ragged last row tile
     (2048, 1024, 2560, 64),     # 128x256 tiles
+    (512, 64, 256, 64),         # one 64-wide K block per plane
     (64, 512, 256, 64),         # rows <= 64: the register-staged split kernel
     (512, 256, 200, 64),        # out_f not a multiple of 128: register-staged
     (300, 384, 256, 128),       # tile 128: register-staged
