@@ -644,6 +644,14 @@ def main():
     if not args.no_decode:
         leg("decode", lambda: decode_bench(be, max(5, args.steps), args.warmup))
         legs["c4"] = legs.pop("decode", None)
+    # the same box's measured ceilings beside the published ones (a few seconds)
+    leg("measured_peaks", lambda: (peaks(), None))
+    mp = res.get("measured_peaks", {})
+    if "mfma_bf16_tflops" in mp:
+        roof["frac_of_measured_peak"] = roof["achieved"] / mp["mfma_bf16_tflops"]
+        res["layer_mfma_frac_of_measured_peak"] = res["layer_tflops"] / mp["mfma_bf16_tflops"]
+    if "hbm_read_GBps" in mp and isinstance(res.get("decode"), dict) and "hbm_GBps" in res["decode"]:
+        res["decode"]["hbm_frac_of_measured_peak"] = res["decode"]["hbm_GBps"] / mp["hbm_read_GBps"]
     gc.enable()
     if not args.no_cpu:
         log("bench: CPU baseline")
