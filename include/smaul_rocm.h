@@ -74,12 +74,14 @@ int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* 
  * smaul_fp8_linear with a caller workspace, for fp32 x (what the reference's
  * FP8Linear passes, kernel/fp8_tile.py:168; same reference entry as
  * smaul_fp8_linear: kernel/compute.py:125-135, kernel/fp8_cpu.cpp:100-141).
- * With fp32 x, tile 64, in_f a multiple of 64, rows > 64 and 16-byte aligned
- * x / w / workspace, x is split into bf16 hi and lo planes in the workspace
- * (x = hi + lo within 2^-18 |x|) and the LDS-DMA GEMM runs over both planes
- * (fp32 sums of exact bf16 x E4M3 products, per-tile scales applied per
- * plane).  Otherwise, or with a workspace smaller than
- * smaul_fp8_linear_workspace_size, it is smaul_fp8_linear.  Same arguments,
+ * fp32 x is computed as x = hi + lo, two bf16 terms (within 2^-18 |x|), with
+ * fp32 sums of exact bf16 x E4M3 products.  smaul_fp8_linear splits the terms
+ * in LDS inside the GEMM (tile 64, in_f a multiple of 64, out_f a multiple of
+ * 128, more than 64 rows, 16-byte aligned x and w); for more than 1024 rows
+ * this entry instead writes the two planes into the workspace in a separate
+ * pass and runs the GEMM over both (faster for long calls).  With fewer rows,
+ * other shapes, or a workspace smaller than smaul_fp8_linear_workspace_size
+ * (0 below 1025 rows or for bf16 x), it is smaul_fp8_linear.  Same arguments,
  * results and errors as smaul_fp8_linear within fp32 summation order.
  */
 int64_t smaul_fp8_linear_workspace_size(int64_t rows, int64_t in_f, int x_dtype);

@@ -686,7 +686,7 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-template <int BM, int BN, int WM, int WN, int NSTAGE, bool SWIGLU>
+template <int BM, int BN, int WM, int WN, int NSTAGE, bool SWIGLU, bool X32 = false>
 struct DmaGemmCfg {
   static constexpr int NW = WM * WN;
   static constexpr int BNO = SWIGLU ? BN / 2 : BN;       // output columns per workgroup
@@ -694,7 +694,9 @@ struct DmaGemmCfg {
   static constexpr int TN = BN / WN;                     // staged weight columns per wave
   static constexpr int TNO = SWIGLU ? TN / 2 : TN;       // output columns per wave
   static constexpr int FM = TM / 32, FN = TN / 32, FNO = TNO / 32;
-  static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 64, S_BYTES = BN * 4;
+  // X32: the activation rows arrive as fp32 (256 B per 64-wide K block) and
+  // are split in place into a bf16 hi plane and a lo plane of 128 B rows
+  static constexpr int A_BYTES = BM * 128 * (X32 ? 2 : 1), B_BYTES = BN * 64, S_BYTES = BN * 4;
   static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
   static constexpr int A_INS = A_BYTES / 1024 / NW;      // 1 KB DMA instructions per wave per stage
   static constexpr int B_INS = B_BYTES / 1024 / NW;
@@ -719,12 +721,20 @@ struct DmaGemmCfg {
 // fp8_forward contract), straight from the MFMA layout; otherwise they are
 // rounded to bf16 and stored through LDS (plain) or, with the SwiGLU
 // epilogue, as 8-byte row pieces after an exchange inside each quad of lanes.
-template <int BM, int BN, int WM, int WN, int NSTAGE, bool SWIGLU, bool CANON, bool REMAP, bool OUT_F32 = false>
+//
+// X32 (OUT_F32 only): fp32 activations.  The stage's rows are staged as fp32
+// and, after its barrier, split in place by all threads into x = hi + lo
+// (split_bf16, |x - hi - lo| <= 2^-18 |x|) in two bf16 planes of the usual
+// layout; each k-step then runs hi and lo MFMAs into the same partial, so the
+// scale multiplies s * (hi . w + lo . w) per 64-wide K block.
+template <int BM, int BN, int WM, int WN, int NSTAGE, bool SWIGLU, bool CANON, bool REMAP, bool OUT_F32 = false,
+          bool X32 = false>
 // Tiles of at most 128 x 128 staged columns fit three workgroups per CU.
 __global__ void __launch_bounds__(WM * WN * 64, (BM * BN <= 128 * 128 ? 3 : 2))
 fp8_gemm_dma_kernel(GemmArgs p) {
   static_assert(!(OUT_F32 && SWIGLU), "the SwiGLU epilogue rounds to bf16");
-  using C = DmaGemmCfg<BM, BN, WM, WN, NSTAGE, SWIGLU>;
+  static_assert(!X32 || OUT_F32, "fp32 activations are the fp8_forward path");
+  using C = DmaGemmCfg<BM, BN, WM, WN, NSTAGE, SWIGLU, X32>;
   constexpr int NW = C::NW, BNO = C::BNO, TM = C::TM, TN = C::TN, TNO = C::TNO, FM = C::FM, FN = C::FN,
                 FNO = C::FNO, A_BYTES = C::A_BYTES, B_BYTES = C::B_BYTES, STAGE = C::STAGE,
                 A_INS = C::A_INS, B_INS = C::B_INS, S_INS = C::S_INS;
@@ -777,14 +787,23 @@ fp8_gemm_dma_kernel(GemmArgs p) {
   // lane%8, which holds logical chunk (lane%8) ^ swz_a(row).  Rows past the
   // segment end load the segment's last row: MFMA output rows depend only on
   // their own A row and those rows are never stored.
+  // X32: instruction q stages fp32 rows 4q..4q+3 unswizzled (lane -> row
+  // 4q + lane/16, 16-byte chunk lane%16); the split writes the swizzled planes.
   uint32_t a_off[A_INS];
 #pragma unroll
   for (int a = 0; a < A_INS; ++a) {
-    const int r = (wave * A_INS + a) * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ swz_a(r);
-    const int64_t lr = row0 + (r < rows_here ? r : rows_here - 1);
-    const int64_t xr = p.row_idx ? (int64_t)p.row_idx[lr] : lr;
-    a_off[a] = (uint32_t)(xr * p.ldx * 2 + c * 16);
+    if constexpr (X32) {
+      const int r = (wave * A_INS + a) * 4 + (lane >> 4);
+      const int64_t lr = row0 + (r < rows_here ? r : rows_here - 1);
+      const int64_t xr = p.row_idx ? (int64_t)p.row_idx[lr] : lr;
+      a_off[a] = (uint32_t)(xr * p.ldx * 4 + (lane & 15) * 16);
+    } else {
+      const int r = (wave * A_INS + a) * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ swz_a(r);
+      const int64_t lr = row0 + (r < rows_here ? r : rows_here - 1);
+      const int64_t xr = p.row_idx ? (int64_t)p.row_idx[lr] : lr;
+      a_off[a] = (uint32_t)(xr * p.ldx * 2 + c * 16);
+    }
   }
   // B instruction q stages weight columns 16q..16q+15 (64 B each).  The host
   // guarantees N % BNO == 0, so every staged column exists, the gate and up
@@ -820,7 +839,7 @@ fp8_gemm_dma_kernel(GemmArgs p) {
     const uint32_t lbase = lds0 + (uint32_t)(buf * STAGE);
     const int kb = kt >= kwb && kwb > 0 ? kt - kwb : kt;  // the weight block of activation block kt
     if (S_INS == NW || wave < S_INS) dma4(s_src + kb * L.sk, s_off, lbase + A_BYTES + B_BYTES + wave * 256);
-    const char* xa = (const char*)p.x + kt * 128;
+    const char* xa = (const char*)p.x + kt * (X32 ? 256 : 128);
 #pragma unroll
     for (int a = 0; a < A_INS; ++a) dma16(xa, a_off[a], lbase + (wave * A_INS + a) * 1024);
 #pragma unroll
@@ -892,16 +911,23 @@ fp8_gemm_dma_kernel(GemmArgs p) {
         bfr[j][ks] = __builtin_bit_cast(bf16x8_t, make_uint4(d[4 * ks], d[4 * ks + 1], d[4 * ks + 2], d[4 * ks + 3]));
     }
     bf16x8_t af[2][4];
+    bf16x8_t afl[X32 ? 2 : 1][4];  // X32: the lo plane, BM * 128 bytes after the hi plane
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) af[0][ks] = *(const bf16x8_t*)(base + a_addr[ks]);
+    for (int ks = 0; ks < 4; ++ks) {
+      af[0][ks] = *(const bf16x8_t*)(base + a_addr[ks]);
+      if constexpr (X32) afl[0][ks] = *(const bf16x8_t*)(base + BM * 128 + a_addr[ks]);
+    }
     f32x16_t qp;
 #pragma unroll
     for (int t = 0; t < FM * FN; ++t) {
       const int i = t / FN, j = t % FN;
       if (j == 0 && i + 1 < FM) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
+        for (int ks = 0; ks < 4; ++ks) {
           af[(i + 1) & 1][ks] = *(const bf16x8_t*)(base + a_addr[ks] + (i + 1) * 32 * 128);
+          if constexpr (X32)
+            afl[(i + 1) & 1][ks] = *(const bf16x8_t*)(base + BM * 128 + a_addr[ks] + (i + 1) * 32 * 128);
+        }
       }
       // one MFMA of tile t, then four of tile t - 1's FMAs, four times over;
       // the scheduling fences keep that order
@@ -910,6 +936,7 @@ fp8_gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i & 1][ks], bfr[j][ks], q, 0, 0, 0);
+        if constexpr (X32) q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afl[i & 1][ks], bfr[j][ks], q, 0, 0, 0);
         if (t > 0) {
 #pragma unroll
           for (int r = ks * 4; r < ks * 4 + 4; ++r) acc[pi][pj][r] = __builtin_fmaf(sc[pj], qp[r], acc[pi][pj][r]);
@@ -920,6 +947,41 @@ fp8_gemm_dma_kernel(GemmArgs p) {
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[FM - 1][FN - 1][r] = __builtin_fmaf(sc[FN - 1], qp[r], acc[FM - 1][FN - 1][r]);
+  };
+
+  // X32: the split of stage buffer b's fp32 rows into the hi and lo planes, in
+  // place (every thread reads its EPT consecutive values of one row, a
+  // barrier, then writes their two bf16 halves to the swizzled planes, and a
+  // barrier publishes them).
+  auto split_stage = [&](int b) {
+    if constexpr (X32) {
+      constexpr int EPT = BM * 64 / (NW * 64), TPR = 64 / EPT;
+      static_assert(EPT % 8 == 0 && EPT * TPR == 64, "whole 16-byte chunks per thread");
+      char* base = smem + b * STAGE;
+      const int r = tid / TPR, k0 = (tid % TPR) * EPT;
+      float v[EPT];
+#pragma unroll
+      for (int q = 0; q < EPT / 4; ++q) {
+        const float4 f = *(const float4*)(base + r * 256 + (k0 + 4 * q) * 4);
+        v[4 * q] = f.x;
+        v[4 * q + 1] = f.y;
+        v[4 * q + 2] = f.z;
+        v[4 * q + 3] = f.w;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < EPT / 8; ++c) {
+        uint32_t h[8], l[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) split_bf16(v[8 * c + e], h[e], l[e]);
+        const int pc = ((k0 / 8 + c) ^ swz_a(r)) << 4;
+        *(uint4*)(base + r * 128 + pc) =
+            make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+        *(uint4*)(base + BM * 128 + r * 128 + pc) =
+            make_uint4(l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16));
+      }
+      __syncthreads();
+    }
   };
 
   // ---- the pipeline ----------------------------------------------------------
@@ -941,6 +1003,7 @@ fp8_gemm_dma_kernel(GemmArgs p) {
     __syncthreads();
     const int ks = kt + NSTAGE - 1;
     dma_stage(ks < nk ? ks : nk - 1, nbuf);
+    split_stage(buf);
     compute_stage(buf);
     buf = buf + 1 == NSTAGE ? 0 : buf + 1;
     nbuf = nbuf + 1 == NSTAGE ? 0 : nbuf + 1;
@@ -3827,14 +3890,14 @@ struct CfgDma32x128 {  // 32 rows x 128 outputs
   static constexpr int BM = 32, BN = 128, WM = 1, WN = 4, NSTAGE = 4;
 };
 
-template <class CF, bool SWIGLU, bool CANON, bool OUT_F32 = false>
+template <class CF, bool SWIGLU, bool CANON, bool OUT_F32 = false, bool X32 = false>
 int launch_gemm_dma(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
   constexpr int BNO = SWIGLU ? CF::BN / 2 : CF::BN;
   const int64_t n_tiles = (a.N + BNO - 1) / BNO;
   if (m_tiles <= 0 || n_tiles <= 0) return SMAUL_OK;
   if (m_tiles > 65535 || n_tiles > 65535) return fail(SMAUL_ERR_UNSUPPORTED, "gemm grid too large");
   hipLaunchKernelGGL(
-      (fp8_gemm_dma_kernel<CF::BM, CF::BN, CF::WM, CF::WN, CF::NSTAGE, SWIGLU, CANON, true, OUT_F32>),
+      (fp8_gemm_dma_kernel<CF::BM, CF::BN, CF::WM, CF::WN, CF::NSTAGE, SWIGLU, CANON, true, OUT_F32, X32>),
       dim3((unsigned)n_tiles, (unsigned)m_tiles), dim3(CF::WM * CF::WN * 64), 0, stream, a);
   return check_launch("fp8_gemm_dma_kernel");
 }
@@ -3855,20 +3918,22 @@ int pick_dense_tile(bool swiglu, int64_t rows, int64_t N) {
   return tiles(64, 128) >= cus ? DT_64x128 : DT_32x128;
 }
 
-template <bool SWIGLU, bool CANON, bool OUT_F32>
+template <bool SWIGLU, bool CANON, bool OUT_F32, bool X32 = false>
 int launch_dense_dma(const GemmArgs& a, int tile, hipStream_t stream) {
   const int64_t rows = a.R;
   switch (tile) {
     case DT_128x256:
-      return launch_gemm_dma<CfgDmaGU, SWIGLU, CANON, OUT_F32>(a, (rows + 127) / 128, stream);
+      return launch_gemm_dma<CfgDmaGU, SWIGLU, CANON, OUT_F32, X32>(a, (rows + 127) / 128, stream);
     case DT_64x128_GU:
       if constexpr (SWIGLU) return launch_gemm_dma<CfgDmaGU64, SWIGLU, CANON, OUT_F32>(a, (rows + 63) / 64, stream);
       break;
     case DT_64x128:
-      if constexpr (!SWIGLU) return launch_gemm_dma<CfgDma64x128, SWIGLU, CANON, OUT_F32>(a, (rows + 63) / 64, stream);
+      if constexpr (!SWIGLU)
+        return launch_gemm_dma<CfgDma64x128, SWIGLU, CANON, OUT_F32, X32>(a, (rows + 63) / 64, stream);
       break;
     case DT_32x128:
-      if constexpr (!SWIGLU) return launch_gemm_dma<CfgDma32x128, SWIGLU, CANON, OUT_F32>(a, (rows + 31) / 32, stream);
+      if constexpr (!SWIGLU)
+        return launch_gemm_dma<CfgDma32x128, SWIGLU, CANON, OUT_F32, X32>(a, (rows + 31) / 32, stream);
       break;
     default:
       break;
@@ -3881,6 +3946,15 @@ int launch_dense_dma(const GemmArgs& a, int tile, hipStream_t stream) {
 // aligned code rows and activation rows, 8-byte aligned output row pieces (its
 // epilogue stores four bf16 columns at a time), and byte offsets that fit its
 // 32-bit per-lane offsets.
+// The fp32-activation form (X32): the same shapes, fp32 rows 16-byte aligned,
+// byte offsets of 4-byte elements within 32 bits.
+bool x32_gemm_ok(const GemmArgs& a, int64_t x_rows) {
+  if (a.tile != 64 || (a.K & 63) != 0 || a.N % 128 != 0 || !aligned16(a.x) || (a.ldx & 3) != 0) return false;
+  if (((uintptr_t)a.y & 7u) != 0 || (a.ldy & 3) != 0) return false;
+  const int64_t lim = (int64_t)1 << 31;
+  return x_rows * a.ldx * 4 < lim && a.N * a.K < lim && a.N * a.nt < lim;
+}
+
 bool dma_gemm_ok(const GemmArgs& a, int act_dtype, int flags, int64_t x_rows, int64_t bno) {
   if (act_dtype != SMAUL_DTYPE_BF16 || a.tile != 64 || (a.K & 63) != 0 || a.N % bno != 0) return false;
   if (!(flags & SMAUL_FLAG_ALIGNED_CODES) || !aligned16(a.x) || (a.ldx & 7) != 0) return false;
@@ -3973,6 +4047,11 @@ int smaul_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const float* 
   const int dt = small ? -1 : pick_dense_tile(false, rows, out_f);
   if (dt >= 0 && vec && dma_gemm_ok(a, x_dtype, flags | SMAUL_FLAG_ALIGNED_CODES, rows, 128))
     return canon ? launch_dense_dma<false, true, true>(a, dt, stream) : launch_dense_dma<false, false, true>(a, dt, stream);
+  // fp32 x, 64-wide tiles: the same kernel staging fp32 rows and splitting
+  // them into bf16 hi / lo planes in LDS (X32)
+  if (dt >= 0 && vec && x_dtype == SMAUL_DTYPE_F32 && x32_gemm_ok(a, rows))
+    return canon ? launch_dense_dma<false, true, true, true>(a, dt, stream)
+                 : launch_dense_dma<false, false, true, true>(a, dt, stream);
   if (x_dtype == SMAUL_DTYPE_BF16) {
     const int64_t bm = small ? CfgSmall::BM : CfgBig::BM;
     const int64_t mt = (rows + bm - 1) / bm;
@@ -4019,15 +4098,22 @@ int planes_tile(int x_dtype, const void* x, const uint8_t* w, int64_t rows, int6
 
 }  // namespace
 
+// Up to this many rows, fp32 x takes smaul_fp8_linear's in-LDS split (X32)
+// rather than the planes pass: a separate launch costs more than it saves on
+// short calls (C-ABI timings: 512 x 512 -> 1536 12.6 vs 16.4 us, 300 x 256 ->
+// 384 8.5 vs 12.5 us; 4096 x 512 -> 1280 35.6 vs 32.7 us, 16384 x 1024 ->
+// 2560 316 vs 259 us).
+constexpr int64_t PLANES_MIN_ROWS = 1025;
+
 int64_t smaul_fp8_linear_workspace_size(int64_t rows, int64_t in_f, int x_dtype) {
   if (rows < 0 || in_f < 0) return -1;
-  return x_dtype == SMAUL_DTYPE_F32 ? rows * in_f * 4 : 0;
+  return (x_dtype == SMAUL_DTYPE_F32 && rows >= PLANES_MIN_ROWS) ? rows * in_f * 4 : 0;
 }
 
 int smaul_fp8_linear_ws(const void* x, int x_dtype, const uint8_t* w, const float* s, void* y, int y_dtype,
                         int64_t rows, int64_t in_f, int64_t out_f, int64_t tile, int flags, void* workspace,
                         int64_t workspace_bytes, hipStream_t stream) {
-  const int dt = (rows > 0 && y && s && y_dtype == SMAUL_DTYPE_F32 && kmode_of(tile) >= 0)
+  const int dt = (rows >= PLANES_MIN_ROWS && y && s && y_dtype == SMAUL_DTYPE_F32 && kmode_of(tile) >= 0)
                      ? planes_tile(x_dtype, x, w, rows, in_f, out_f, tile, flags)
                      : -1;
   if (dt < 0 || !workspace || !aligned16(workspace) ||

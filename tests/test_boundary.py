@@ -52,7 +52,8 @@ def test_library_validates_without_touching_the_gpu():
     assert rc == _lib.SMAUL_ERR_INVALID and "positive" in _lib.last_error()
     rc = lib.smaul_fp8_linear_ws(None, 0, None, None, None, 0, 4, 64, 8, 48, 0, None, 0, None)
     assert rc == _lib.SMAUL_ERR_UNSUPPORTED
-    assert lib.smaul_fp8_linear_workspace_size(100, 512, 0) == 100 * 512 * 4
+    assert lib.smaul_fp8_linear_workspace_size(2000, 512, 0) == 2000 * 512 * 4
+    assert lib.smaul_fp8_linear_workspace_size(100, 512, 0) == 0
     assert lib.smaul_fp8_linear_workspace_size(100, 512, 1) == 0
     rc = lib.smaul_moe_router(None, 1, None, None, None, None, None, 8, 64, 65, 2, None)
     assert rc == _lib.SMAUL_ERR_INVALID

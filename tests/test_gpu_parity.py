@@ -139,16 +139,20 @@ def test_fp8_linear_bf16_dma_tiles(rows, in_f, out_f, raw_codes):
     (4096, 1280, 512, 64),      # C2 down: 32x128 tiles
     (300, 256, 384, 64),        # ragged last row tile
     (2048, 1024, 2560, 64),     # 128x256 tiles
-    (512, 64, 256, 64),         # one 64-wide K block per plane
+    (512, 64, 256, 64),         # in-LDS split (<= 1024 rows), one 64-wide K block
+    (1000, 1024, 2560, 64),     # in-LDS split, 64x128 tiles
+    (1024, 64, 16384, 64),      # in-LDS split, 128x256 tiles
+    (700, 256, 384, 64),        # in-LDS split, 32x128 tiles
     (64, 512, 256, 64),         # rows <= 64: the register-staged split kernel
     (512, 256, 200, 64),        # out_f not a multiple of 128: register-staged
     (300, 384, 256, 128),       # tile 128: register-staged
 ])
 def test_fp8_linear_fp32_two_planes(rows, in_f, out_f, tile):
     """fp32 x (what FP8Linear passes) through fp8_forward: split into bf16 hi and
-    lo planes in the workspace and run by the LDS-DMA GEMM over both planes, or
-    the register-staged kernel where the shape does not fit it.  Rows sampled
-    against the oracle at the fp32-input bar (test_linear_fp8.py:170-183)."""
+    lo planes (in a workspace pass above 1024 rows, in LDS inside the GEMM
+    below) for the LDS-DMA GEMM, or the register-staged kernel where the shape
+    does not fit it.  Rows sampled against the oracle at the fp32-input bar
+    (test_linear_fp8.py:170-183)."""
     print(f"case fp8_linear fp32 rows={rows} in_f={in_f} out_f={out_f} tile={tile}", flush=True)
     gen = torch.Generator().manual_seed(rows * 5 + in_f + out_f * 7 + tile)
     x = torch.randn(rows, in_f, generator=gen)
@@ -164,13 +168,14 @@ def test_fp8_linear_fp32_two_planes(rows, in_f, out_f, tile):
 
 def test_fp8_linear_ws_abi_fallbacks():
     """smaul_fp8_linear_ws through the C-ABI: the two-plane path with a large
-    enough workspace and smaul_fp8_linear itself without one (or one too
-    small), both within the fp32-input bar of the oracle; bf16 x needs no
-    workspace; the size query."""
+    enough workspace and smaul_fp8_linear itself (the in-LDS split) without
+    one or with one too small, both within the fp32-input bar of the oracle;
+    bf16 x and short fp32 calls need no workspace; the size query."""
     from smaulnative_amd import _lib
     lib = _lib.load()
-    rows, in_f, out_f = 1024, 512, 384
+    rows, in_f, out_f = 2048, 512, 384
     assert lib.smaul_fp8_linear_workspace_size(rows, in_f, _lib.DTYPE_F32) == rows * in_f * 4
+    assert lib.smaul_fp8_linear_workspace_size(1024, in_f, _lib.DTYPE_F32) == 0  # in-LDS split instead
     assert lib.smaul_fp8_linear_workspace_size(rows, in_f, _lib.DTYPE_BF16) == 0
     assert lib.smaul_fp8_linear_workspace_size(-1, in_f, _lib.DTYPE_F32) == -1
     gen = torch.Generator().manual_seed(77)
