@@ -4154,8 +4154,12 @@ static constexpr int route_tb(int64_t E) { return E <= 4 ? 8 : E <= 16 ? 4 : 1; 
 static bool route_mfma_ok(int64_t E, int64_t d, int x_dtype) {
   return x_dtype == SMAUL_DTYPE_BF16 && E <= 16 && route_ksw(d) != 0;
 }
-static int route_tpb(int64_t E, int64_t d, int x_dtype) {
-  return route_mfma_ok(E, d, x_dtype) ? ROUTE_MFMA_TPB : route_tb(E) * ROUTE_WAVES;
+// Up to ROUTE_SMALL_T tokens the MFMA router takes 16 tokens per workgroup
+// (more workgroups for a short call; the arithmetic per token is the same).
+constexpr int64_t ROUTE_SMALL_T = 2048;
+static int route_tpb(int64_t T, int64_t E, int64_t d, int x_dtype) {
+  if (route_mfma_ok(E, d, x_dtype)) return T <= ROUTE_SMALL_T ? 16 : ROUTE_MFMA_TPB;
+  return route_tb(E) * ROUTE_WAVES;
 }
 
 // The decode router (T <= 64, bf16, the MFMA router's shapes): one block per
@@ -4193,9 +4197,10 @@ static int launch_router_small(const void* x, const float* gate_w, const float* 
 static int launch_router(const void* x, int x_dtype, const float* gate_w, const float* gate_b,
                          const RouteOut& o, int64_t T, int64_t d, int64_t E, int64_t k,
                          hipStream_t stream) {
-  const int64_t tpb = route_tpb(E, d, x_dtype);
+  const int64_t tpb = route_tpb(T, E, d, x_dtype);
   const int64_t nb = (T + tpb - 1) / tpb;
   if (nb > 2147483647LL) return fail(SMAUL_ERR_UNSUPPORTED, "router: too many tokens");
+  if (route_mfma_ok(E, d, x_dtype) && tpb == 16) return launch_router_small(x, gate_w, gate_b, o, T, d, E, k, stream);
   const bool bf = x_dtype == SMAUL_DTYPE_BF16;
   if (route_mfma_ok(E, d, x_dtype)) {
     const uint16_t* xb = (const uint16_t*)x;
@@ -4573,7 +4578,7 @@ int smaul_rms_norm(const void* x, int act_dtype, const float* weight, void* out,
 //   blockcnt[nb*E] blockoff[nb*E]  (nb = router token blocks)
 //   hdn[T*k, h] (act dtype)  yperm[T*k, d] (act dtype)
 static int64_t route_blocks(int64_t T, int64_t E, int64_t d, int x_dtype) {
-  const int64_t tpb = route_tpb(E, d, x_dtype);
+  const int64_t tpb = route_tpb(T, E, d, x_dtype);
   return (T + tpb - 1) / tpb;
 }
 
@@ -4851,7 +4856,7 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
     if (rc) return rc;
   } else if (nb > 1) {
     rc = launch_scan_scatter(topi, topw, blockcnt, blockoff, counts, seg_off, tile_off, perm_row, perm_w, inv,
-                             T, E, k, bm, route_tpb(E, d, act_dtype), stream);
+                             T, E, k, bm, route_tpb(T, E, d, act_dtype), stream);
     if (rc) return rc;
   }
   rc = smaul_moe_gate_up(x, act_dtype, perm_row, gate_w8, gate_s, up_w8, up_s, hdn, seg_off, tile_off,
