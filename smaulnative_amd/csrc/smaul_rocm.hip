@@ -3880,8 +3880,8 @@ struct CfgDmaDownN {
 // in the first round, so the launch takes one tile's whole latency, and a
 // smaller tile shortens it.  Deeper pipelines cover the DMA latency that the
 // second workgroup of a CU no longer hides.
-struct CfgDmaGU64 {  // 64 rows x 64 outputs (gate+up), 2 x 2 waves of 32 rows x 32 outputs
-  static constexpr int BM = 64, BN = 128, WM = 2, WN = 2, NSTAGE = 3;
+struct CfgDmaGU64 {  // 64 rows x 128 outputs (gate+up), 4 waves of 64 rows x 32 outputs
+  static constexpr int BM = 64, BN = 256, WM = 1, WN = 4, NSTAGE = 2;
 };
 struct CfgDma64x128 {  // 64 rows x 128 outputs
   static constexpr int BM = 64, BN = 128, WM = 1, WN = 4, NSTAGE = 3;
@@ -3904,16 +3904,18 @@ int launch_gemm_dma(const GemmArgs& a, int64_t m_tiles, hipStream_t stream) {
 
 // The dense (one-segment) LDS-DMA GEMM with its tile chosen by grid size:
 // the 128-row tile where its grid fills the workgroup slots (two per CU),
-// else 64 x 128 (gate+up: 64 x 64 outputs), or 32 x 128 where even that
-// leaves CUs without a workgroup; -1 when N is not a multiple of 128.
-// Measured at config 2 (kernel trace, 4096 rows): gate+up 22.0 -> 18.3 us,
-// down (K 1280, N 512) 24.2 -> 11.7 us; 32 x 128 tiles there: 11.4 us.
-enum DenseTile { DT_128x256 = 0, DT_64x128_GU = 1, DT_64x128 = 2, DT_32x128 = 3 };
+// else 64 x 128 (gate+up: 64 rows x 128 outputs, two stages, three
+// workgroups per CU), or 32 x 128 where even that leaves CUs without a
+// workgroup; -1 when N is not a multiple of 128.  Measured at config 2
+// (kernel trace, 4096 rows): gate+up 22.0 -> 18.3 us, down (K 1280, N 512)
+// 24.2 -> 11.7 us; 32 x 128 tiles there: 11.4 us; the gate+up tile of 64
+// outputs on a 2 x 2 wave grid (three stages) 0.9 us slower than 128 outputs.
+enum DenseTile { DT_128x256 = 0, DT_64x256_GU = 1, DT_64x128 = 2, DT_32x128 = 3 };
 int pick_dense_tile(bool swiglu, int64_t rows, int64_t N) {
   if (N % 128 != 0) return -1;
   const int64_t cus = cu_count();
   auto tiles = [&](int64_t bm, int64_t bno) { return ((rows + bm - 1) / bm) * (N / bno); };
-  if (swiglu) return tiles(128, 128) >= 2 * cus ? DT_128x256 : DT_64x128_GU;
+  if (swiglu) return tiles(128, 128) >= 2 * cus ? DT_128x256 : DT_64x256_GU;
   if (N % 256 == 0 && tiles(128, 256) >= 2 * cus) return DT_128x256;
   return tiles(64, 128) >= cus ? DT_64x128 : DT_32x128;
 }
@@ -3924,7 +3926,7 @@ int launch_dense_dma(const GemmArgs& a, int tile, hipStream_t stream) {
   switch (tile) {
     case DT_128x256:
       return launch_gemm_dma<CfgDmaGU, SWIGLU, CANON, OUT_F32, X32>(a, (rows + 127) / 128, stream);
-    case DT_64x128_GU:
+    case DT_64x256_GU:
       if constexpr (SWIGLU) return launch_gemm_dma<CfgDmaGU64, SWIGLU, CANON, OUT_F32>(a, (rows + 63) / 64, stream);
       break;
     case DT_64x128:
