@@ -458,8 +458,8 @@ def test_moe_decode_regime(T, E, k, skew):
 @pytest.mark.parametrize("T,skew", [(64, (9.0, [], 0.0)), (40, (9.0, [3, 4, 5, 6, 7], 9.0)), (7, None)])
 def test_moe_decode_c4_shape(T, skew):
     """Config-4 widths in the decode regime: one expert holding every token
-    (four 16-row tiles), experts left idle (the gate/up kernel's early weight
-    loads assume every expert runs and are re-issued), and a tiny step."""
+    (four 16-row tiles), experts left idle (no segment, no unit), and a tiny
+    step."""
     print(f"case decode c4 T={T} skew={skew}", flush=True)
     d, h, E, k = 1024, 2560, 8, 2
     x, gw, gb, experts = make_moe(640 + T, T, d, h, E, k, skew=skew)
