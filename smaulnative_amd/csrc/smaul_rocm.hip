@@ -108,7 +108,7 @@ __device__ __forceinline__ uint4 ldg16(const void* p) {
 __device__ __forceinline__ float ldgf(const float* p) { return *(g_fp)p; }
 
 // Device-coherent reads of data that other workgroups of the same launch wrote
-// (with device-scope stores, see coh_store16): a raw buffer load with the
+// (with agent-scope atomic stores): a raw buffer load with the
 // device-scope cache policy (sc1) is served past this XCD's L2, which may hold
 // a stale copy of the line.  The descriptor covers `bytes` bytes from p
 // (word 3 is the gfx9 raw-buffer format).
