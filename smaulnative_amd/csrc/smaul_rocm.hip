@@ -3815,6 +3815,11 @@ bool dtype_ok(int dt) { return dt == SMAUL_DTYPE_F32 || dt == SMAUL_DTYPE_BF16; 
 // block_m 16 selects the decode-regime kernels (at most 64 rows per expert:
 // every token appears at most once per expert, so T <= 64 guarantees it).
 constexpr int DECODE_BM = 16;
+// block_m 64: the LDS-DMA kernels on 64-row tiles, for a layer whose 128-row
+// gate/up grid would leave CUs without a workgroup (chosen inside
+// smaul_moe_forward only, where the code-alignment flag is known; every
+// output is the same sum in the same order as on 128-row tiles).
+constexpr int DMA_SMALL_BM = 64;
 
 bool decode_shape_ok(int64_t d, int64_t h, int64_t tile) { return tile == 64 && d % 128 == 0 && h % 128 == 0; }
 
@@ -4368,7 +4373,7 @@ static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* 
     return fail(SMAUL_ERR_UNSUPPORTED, "moe gemm: K must be a multiple of 16 and activations 16-byte aligned");
   const int64_t big_bm = act_dtype == SMAUL_DTYPE_BF16 ? CfgBig::BM : CfgBigF32::BM;
   if (!(block_m == big_bm || block_m == CfgSmall::BM ||
-        (block_m == DECODE_BM && act_dtype == SMAUL_DTYPE_BF16)))
+        ((block_m == DECODE_BM || block_m == DMA_SMALL_BM) && act_dtype == SMAUL_DTYPE_BF16)))
     return fail(SMAUL_ERR_INVALID, "moe gemm: block_m must come from smaul_moe_block_m");
   if (!act || !w1 || !s1 || !out || !seg_off || !tile_off || (swiglu && (!w2 || !s2)))
     return fail(SMAUL_ERR_INVALID, "moe gemm: null pointer");
@@ -4418,6 +4423,16 @@ static int moe_gemm(bool swiglu, const void* act, int act_dtype, const int32_t* 
                    : launch_gemm_dma<CfgDmaDownN, false, false>(a, max_tiles, stream);
     return canon ? launch_gemm_dma<CfgDmaDown, false, true>(a, max_tiles, stream)
                  : launch_gemm_dma<CfgDmaDown, false, false>(a, max_tiles, stream);
+  }
+  if (block_m == DMA_SMALL_BM) {  // no other kernel runs this tile table
+    static_assert(CfgDmaGU64::BM == DMA_SMALL_BM && CfgDma64x128::BM == DMA_SMALL_BM, "64-row tile table");
+    if (!dma_gemm_ok(a, act_dtype, flags, max_tiles * block_m, 128))
+      return fail(SMAUL_ERR_UNSUPPORTED, "moe gemm: block_m 64 needs the LDS-DMA kernels' shapes and aligned codes");
+    if (swiglu)
+      return canon ? launch_gemm_dma<CfgDmaGU64, true, true>(a, max_tiles, stream)
+                   : launch_gemm_dma<CfgDmaGU64, true, false>(a, max_tiles, stream);
+    return canon ? launch_gemm_dma<CfgDma64x128, false, true>(a, max_tiles, stream)
+                 : launch_gemm_dma<CfgDma64x128, false, false>(a, max_tiles, stream);
   }
   if (block_m == big_bm)
     return gemm_dispatch_moe<CfgBig, CfgBigF32>(a, swiglu, act_dtype, max_tiles, canon, stream);
@@ -4743,7 +4758,31 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
   ws += align256(R * d * el);
   int32_t* sync = (int32_t*)ws;
 
-  const int64_t bm = pick_block_m(T, d, h, E, k, tile, act_dtype);
+  int64_t bm = pick_block_m(T, d, h, E, k, tile, act_dtype);
+  if (bm == CfgBig::BM && act_dtype == SMAUL_DTYPE_BF16 &&
+      ((R + CfgBig::BM - 1) / CfgBig::BM + E) * (h / 128) < cu_count()) {
+    // 64-row tiles where both projections fit the LDS-DMA kernels
+    const int64_t mt = (R + DMA_SMALL_BM - 1) / DMA_SMALL_BM + E;
+    GemmArgs g{};
+    g.x = x;
+    g.ldx = d;
+    g.y = hdn;
+    g.ldy = h;
+    g.K = d;
+    g.N = h;
+    g.nt = d / 64;
+    g.tile = tile;
+    GemmArgs dn = g;
+    dn.x = hdn;
+    dn.ldx = h;
+    dn.y = yperm;
+    dn.ldy = d;
+    dn.K = h;
+    dn.N = d;
+    dn.nt = h / 64;
+    if (dma_gemm_ok(g, act_dtype, flags, T, 128) && dma_gemm_ok(dn, act_dtype, flags, mt * DMA_SMALL_BM, 128))
+      bm = DMA_SMALL_BM;
+  }
   // decode regime: the gate/up kernel dispatches for itself
   const bool fused = bm == DECODE_BM && aligned16(x) && h % 16 == 0 &&
                      ds_kbw(d / 64, true) != 0;
