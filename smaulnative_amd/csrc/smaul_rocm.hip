@@ -3816,9 +3816,11 @@ bool dtype_ok(int dt) { return dt == SMAUL_DTYPE_F32 || dt == SMAUL_DTYPE_BF16; 
 // every token appears at most once per expert, so T <= 64 guarantees it).
 constexpr int DECODE_BM = 16;
 // block_m 64: the LDS-DMA kernels on 64-row tiles, for a layer whose 128-row
-// gate/up grid would leave CUs without a workgroup (chosen inside
+// gate/up grid is under four workgroups per CU (chosen inside
 // smaul_moe_forward only, where the code-alignment flag is known; every
-// output is the same sum in the same order as on 128-row tiles).
+// output is the same sum in the same order as on 128-row tiles).  Measured
+// (d 1024, h 2560, E 8, top-2): T 768 80.4 -> 67.7 us, T 2048 122.1 -> 110.5
+// us; at 1440 and 5280 workgroups (T 4096, 16384) 64-row tiles lose 1-6 %.
 constexpr int DMA_SMALL_BM = 64;
 
 bool decode_shape_ok(int64_t d, int64_t h, int64_t tile) { return tile == 64 && d % 128 == 0 && h % 128 == 0; }
@@ -4760,7 +4762,7 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
 
   int64_t bm = pick_block_m(T, d, h, E, k, tile, act_dtype);
   if (bm == CfgBig::BM && act_dtype == SMAUL_DTYPE_BF16 &&
-      ((R + CfgBig::BM - 1) / CfgBig::BM + E) * (h / 128) < cu_count()) {
+      ((R + CfgBig::BM - 1) / CfgBig::BM + E) * (h / 128) < 4 * (int64_t)cu_count()) {
     // 64-row tiles where both projections fit the LDS-DMA kernels
     const int64_t mt = (R + DMA_SMALL_BM - 1) / DMA_SMALL_BM + E;
     GemmArgs g{};
