@@ -423,6 +423,8 @@ def test_moe_golden(tag):
     (200, 128, 320, 2, 2, torch.bfloat16, 32),
     (64, 1024, 2560, 8, 2, torch.bfloat16, 64),        # config-4 decode-sized step
     (17, 64, 160, 1, 1, torch.bfloat16, 64),
+    (300, 256, 384, 2, 1, torch.bfloat16, 64),         # 64-row tiles: two experts, top-1
+    (1000, 128, 256, 3, 2, torch.bfloat16, 64),        # 64-row tiles: K = 128 (two stages)
 ])
 def test_moe_vs_oracle(T, d, h, E, k, dtype, tile):
     print(f"case moe T={T} d={d} h={h} E={E} k={k} {dtype} tile={tile}", flush=True)
