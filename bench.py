@@ -221,6 +221,19 @@ def c2_bench(be, steps, warmup):
     res["fp8_linear"] = dict(lin, workload="fp8_forward (FP8Linear's GEMM, fp32 output) for gate 4096x512->1280, "
                                            "up 4096x512->1280 and down 4096x1280->512: three calls per step "
                                            "(the SwiGLU product between them is not timed)")
+    # the input gradients of the same three projections (training, F3):
+    # fp8_backward_input with fp32 g, as _Fn.backward passes it (kernel/fp8_tile.py:177)
+    gg = [torch.randn(rows, o, generator=gen).to("cuda") for o in (h, h, d)]
+
+    def three_bw():
+        be.fp8_backward_input(gg[0], bufs[0], bufs[1], d, h, 64)
+        be.fp8_backward_input(gg[1], bufs[2], bufs[3], d, h, 64)
+        be.fp8_backward_input(gg[2], bufs[4], bufs[5], h, d, 64)
+    bms = event_median_ms(three_bw, n, warmup)
+    res["fp8_backward_input"] = {
+        "workload": "fp8_backward_input (dx = g . W, fp32) for gate, up (4096x1280 -> 512) and down "
+                    "(4096x512 -> 1280): three calls per step",
+        "ms_per_step": bms, "tflops": flops / (bms * 1e-3) / 1e12, "mfma_frac": flops / (bms * 1e-3) / PEAK_BF16_FLOPS}
     return res, (x, bufs)
 
 

@@ -5,14 +5,20 @@
 // the reference's native kernel kernel/fp8_cpu.cpp:167-259.  Training only;
 // not on the forward path.
 //
-// A workgroup owns a 64 x 64 tile of dx and walks the output dimension o in
-// chunks of 32: the chunk of g (transposed) and the chunk of W decoded to
-// fp32 (lut * s rounded once, as the reference's fast path forms it) are
-// staged in LDS, and each thread accumulates a 4 x 4 block with fused
-// multiply-adds.  The sum over o runs in another order than the reference's
-// eight-way split, so results agree to fp32 rounding (relative 1e-6), not
-// bitwise.  It is a VALU kernel: the backward is not timed here, and an fp32
-// gradient would need three bf16 terms per value to go through MFMA exactly.
+// Two kernels, each a workgroup per 64 x 64 tile of dx walking the output
+// dimension o in chunks of 32, whose sums over o run in another order than
+// the reference's eight-way split: results agree to fp32 rounding (relative
+// 1e-6), not bitwise.
+//  - fp8_backward_input_mfma_kernel (tile a multiple of 64, so the tile's 64
+//    input columns share one scale column kb): dx[r, i] = sum_o (g[r, o] *
+//    s[o, kb]) * lut[w[o, i]].  The products g * s are formed in fp32 and
+//    split exactly into three bf16 terms, the codes decode exactly to bf16,
+//    so every matrix-core product is exact and the sums are fp32.  (The
+//    reference rounds lut * s instead of g * s: the same to fp32 rounding.)
+//  - fp8_backward_input_kernel (any tile): the chunk of W decoded to fp32
+//    (lut * s rounded once, as the reference's fast path forms it) and of g
+//    staged in LDS, each thread a 4 x 4 block of fused multiply-adds.
+#include "e4m3.h"
 #include "smaul_common.h"
 
 using smaul::check_launch;
@@ -46,6 +52,120 @@ __constant__ Lut kLut = Lut();
 
 constexpr int BW_T = 64;   // dx tile: rows and input columns
 constexpr int BW_K = 32;   // output dimension per LDS chunk
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// Four waves, each 32 rows x 32 columns of the tile (v_mfma_f32_32x32x16_bf16:
+// lane l holds row / column l % 32 of the operands at k = 8 (l / 32) + 0..7,
+// and column l % 32, rows (r / 4) 8 + (l / 32) 4 + r % 4 of the sums).  Per
+// chunk of BWM_K = 64 o: every thread turns 16 values of g * s (one row, 16
+// consecutive o) into their three bf16 terms and writes them, and 16 codes of
+// one o (16 consecutive columns) transposed, to LDS; the loads of the next
+// chunk are issued before the chunk's MFMAs.  VEC: g rows and code rows are
+// 16-byte aligned and whole chunks are in range (out_f % 64 == 0, in_f % 64
+// == 0), so they load as 16-byte vectors.
+constexpr int BWM_K = 64;
+
+template <bool CANON, bool VEC>
+__global__ void __launch_bounds__(256)
+fp8_backward_input_mfma_kernel(const float* __restrict__ g, const uint8_t* __restrict__ w,
+                               const float* __restrict__ s, float* __restrict__ dx, int64_t rows, int64_t in_f,
+                               int64_t out_f, int64_t tile, int64_t nt) {
+  __shared__ __attribute__((aligned(16))) uint16_t sa[3][BW_T][BWM_K + 8];  // terms of g * s, [row][o]
+  __shared__ __attribute__((aligned(16))) uint8_t sw[BW_T][BWM_K + 16];     // codes, [column][o]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t r0 = (int64_t)blockIdx.y * BW_T, c0 = (int64_t)blockIdx.x * BW_T;
+  const int64_t kb = c0 / tile;
+  // this thread's staging: g row ar, 16 o from ao; codes of o = wo, 16 columns from wc
+  const int ar = tid >> 2, ao = (tid & 3) * 16;
+  const int wo = tid >> 2, wc = (tid & 3) * 16;
+  const int64_t gr = r0 + ar;
+  float gv[16], sv[16];
+  uint4 cw;
+  auto load = [&](int64_t o0) {
+    if constexpr (VEC) {
+      const float4* gp = (const float4*)(g + (gr < rows ? gr : rows - 1) * out_f + o0 + ao);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 v = gp[q];
+        gv[4 * q] = v.x;
+        gv[4 * q + 1] = v.y;
+        gv[4 * q + 2] = v.z;
+        gv[4 * q + 3] = v.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sv[j] = s[(o0 + ao + j) * nt + kb];
+      cw = *(const uint4*)(w + (o0 + wo) * in_f + c0 + wc);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int64_t o = o0 + ao + j;
+        gv[j] = (gr < rows && o < out_f) ? g[gr * out_f + o] : 0.0f;
+        sv[j] = o < out_f ? s[o * nt + kb] : 0.0f;
+      }
+      const int64_t o = o0 + wo;
+      uint32_t b[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int64_t i = c0 + wc + j;
+        b[j] = (o < out_f && i < in_f) ? w[o * in_f + i] : 0u;  // code 0 decodes to +0
+      }
+      cw = make_uint4(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24), b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24),
+                      b[8] | (b[9] << 8) | (b[10] << 16) | (b[11] << 24),
+                      b[12] | (b[13] << 8) | (b[14] << 16) | (b[15] << 24));
+    }
+  };
+  f32x16_t acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  load(0);
+  for (int64_t o0 = 0; o0 < out_f; o0 += BWM_K) {
+    {
+      uint32_t t[3][8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        float a = gv[2 * q] * sv[2 * q], b = gv[2 * q + 1] * sv[2 * q + 1];
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {  // term p: the bf16 rounding of what terms < p leave (exact differences)
+          t[p][q] = pack_bf16(a, b);
+          a = a - bf2f(t[p][q] & 0xffffu);
+          b = b - bf2f(t[p][q] >> 16);
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        *(uint4*)&sa[p][ar][ao] = make_uint4(t[p][0], t[p][1], t[p][2], t[p][3]);
+        *(uint4*)&sa[p][ar][ao + 8] = make_uint4(t[p][4], t[p][5], t[p][6], t[p][7]);
+      }
+      const uint32_t cwv[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sw[wc + j][wo] = (uint8_t)(cwv[j >> 2] >> ((j & 3) * 8));
+    }
+    __syncthreads();
+    if (o0 + BWM_K < out_f) load(o0 + BWM_K);
+#pragma unroll
+    for (int ks = 0; ks < BWM_K / 16; ++ks) {
+      const int ob = ks * 16 + (lane >> 5) * 8;
+      const int fr = wm * 32 + (lane & 31), fc = wn * 32 + (lane & 31);
+      const uint2 c = *(const uint2*)&sw[fc][ob];
+      uint32_t d[4];
+      decode4<CANON>(c.x, d[0], d[1]);
+      decode4<CANON>(c.y, d[2], d[3]);
+      const bf16x8_t bf = __builtin_bit_cast(bf16x8_t, make_uint4(d[0], d[1], d[2], d[3]));
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8_t*)&sa[p][fr][ob], bf, acc, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t row = r0 + wm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+    const int64_t col = c0 + wn * 32 + (lane & 31);
+    if (row < rows && col < in_f) dx[row * in_f + col] = acc[r];
+  }
+}
 
 __global__ void __launch_bounds__(256)
 fp8_backward_input_kernel(const float* __restrict__ g, const uint8_t* __restrict__ w, const float* __restrict__ s,
@@ -122,8 +242,19 @@ int smaul_fp8_backward_input(const float* g, const uint8_t* w, const float* s, f
   if (!dx || (out_f > 0 && (!g || !w || !s))) return fail(SMAUL_ERR_INVALID, "fp8_backward_input: null pointer");
   const int64_t gx = (in_f + BW_T - 1) / BW_T, gy = (rows + BW_T - 1) / BW_T;
   if (gx > 2147483647LL || gy > 65535) return fail(SMAUL_ERR_UNSUPPORTED, "fp8_backward_input: grid too large");
+  const int64_t nt = (in_f + tile - 1) / tile;
+  if (tile % BW_T == 0) {  // a dx tile's columns share one scale column
+    const bool vec = out_f % BWM_K == 0 && in_f % BW_T == 0 && ((uintptr_t)g & 15) == 0 && ((uintptr_t)w & 15) == 0;
+    if (vec)
+      hipLaunchKernelGGL((fp8_backward_input_mfma_kernel<false, true>), dim3((unsigned)gx, (unsigned)gy), dim3(256), 0,
+                         stream, g, w, s, dx, rows, in_f, out_f, tile, nt);
+    else
+      hipLaunchKernelGGL((fp8_backward_input_mfma_kernel<false, false>), dim3((unsigned)gx, (unsigned)gy), dim3(256),
+                         0, stream, g, w, s, dx, rows, in_f, out_f, tile, nt);
+    return check_launch("fp8_backward_input_mfma_kernel");
+  }
   hipLaunchKernelGGL(fp8_backward_input_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, stream, g, w, s, dx,
-                     rows, in_f, out_f, tile, (in_f + tile - 1) / tile);
+                     rows, in_f, out_f, tile, nt);
   return check_launch("fp8_backward_input_kernel");
 }
 

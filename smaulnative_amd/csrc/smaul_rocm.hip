@@ -39,6 +39,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include "e4m3.h"
 #include "smaul_common.h"
 #include "smaul_rocm.h"
 #include "topk_select.h"
@@ -47,8 +48,6 @@
 
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 using smaul::check_launch;
@@ -65,7 +64,6 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return u >> 16;
 }
-__device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
 
 // Split an fp32 value into two bf16 terms: x ~= hi + lo (error <= 2^-18 |x|).
 __device__ __forceinline__ void split_bf16(float x, uint32_t& hi, uint32_t& lo) {
@@ -73,25 +71,6 @@ __device__ __forceinline__ void split_bf16(float x, uint32_t& hi, uint32_t& lo) 
   lo = f2bf(x - bf2f(hi));
 }
 
-// The reference codebook decodes 0x7F/0xFF to +-448 where OCP E4M3FN has NaN;
-// every other code is identical.  Rewrite those two codes to 0x7E/0xFE (also
-// +-448) so the hardware OCP conversion is exact for all 256 codes.
-__device__ __forceinline__ uint32_t canon4(uint32_t w) {
-  const uint32_t t = w & 0x7f7f7f7fu;
-  const uint32_t m = (t + 0x01010101u) & 0x80808080u;  // bit 7 set where t == 0x7f
-  return w - (m >> 7);
-}
-
-// 4 E4M3 codes (bytes 0..3 of w) -> 4 bf16 packed in two dwords, exact.
-// CANON: the codes are already canonical (no 0x7F/0xFF bytes).
-template <bool CANON>
-__device__ __forceinline__ void decode4(uint32_t w, uint32_t& lo, uint32_t& hi) {
-  if constexpr (!CANON) w = canon4(w);
-  bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
-  bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
-  lo = __builtin_bit_cast(uint32_t, a);
-  hi = __builtin_bit_cast(uint32_t, b);
-}
 
 // Loads through explicit global-address-space pointers.  Pointers read from
 // memory (per-expert weight tables, gathered rows) are otherwise generic, and
@@ -680,11 +659,6 @@ __device__ __forceinline__ void wait_vm() {
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
-  const bf16x2v v = {(__bf16)a, (__bf16)b};  // v_cvt_pk_bf16_f32: round to nearest even
-  return __builtin_bit_cast(uint32_t, v);
-}
 
 template <int BM, int BN, int WM, int WN, int NSTAGE, bool SWIGLU, bool X32 = false>
 struct DmaGemmCfg {

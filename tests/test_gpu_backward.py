@@ -74,6 +74,25 @@ def test_fp8linear_training_step(dtype):
     assert bool((diff <= 2 * ulp + terms * 2.0 ** -18).all())
 
 
+@pytest.mark.parametrize("tile", [64, 128])
+def test_backward_input_raw_codes(tile):
+    """Every one of the 256 codes as stored (0x7F / 0xFF decode to +-448, NaN
+    in OCP E4M3), scales spanning 2^-20..2^4, and a gradient with a wide
+    dynamic range: the matrix-core form (tile a multiple of 64) splits g * s
+    into three bf16 terms exactly and decodes the codes exactly."""
+    rows, in_f, out_f = 200, 320, 512
+    gen = torch.Generator().manual_seed(tile)
+    w = torch.randint(0, 256, (out_f, in_f), generator=gen, dtype=torch.uint8)
+    nt = (in_f + tile - 1) // tile
+    s = torch.exp2(torch.randint(-20, 5, (out_f, nt), generator=gen).float()) * (1 + torch.rand(out_f, nt, generator=gen))
+    g = torch.randn(rows, out_f, generator=gen) * torch.exp2(torch.randint(-30, 30, (rows, 1), generator=gen).float())
+    dx = get_backend("rocm").fp8_backward_input(g.to(DEV), w.to(DEV), s.to(DEV), in_f, out_f, tile)
+    ref = oracle.fp8_backward_input(g, w, s, in_f, out_f, tile)
+    # per row: the rows differ by up to 2^60 in scale
+    err = ((dx.cpu().double() - ref.double()).abs().amax(1) / ref.double().abs().amax(1).clamp_min(1e-300)).max()
+    assert float(err) < 1e-5, float(err)
+
+
 def test_backward_input_zero_sizes_abi():
     """in_f or out_f of 0 are accepted, as by the reference kernel
     (fp8_cpu.cpp:227-228): out_f == 0 is an empty sum (dx all zeros, g / w / s
