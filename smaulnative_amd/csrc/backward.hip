@@ -94,8 +94,11 @@ fp8_backward_input_mfma_kernel(const float* __restrict__ g, const uint8_t* __res
         gv[4 * q + 2] = v.z;
         gv[4 * q + 3] = v.w;
       }
+      // the wave's lanes hold the chunk's 64 scales, lane l that of o = (l & 3) * 16 + (l >> 2),
+      // and each lane gathers its 16 (ao = (l & 3) * 16) with cross-lane reads
+      const float sl = s[(o0 + (lane & 3) * 16 + (lane >> 2)) * nt + kb];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) sv[j] = s[(o0 + ao + j) * nt + kb];
+      for (int j = 0; j < 16; ++j) sv[j] = __shfl(sl, (j << 2) | (lane & 3), 64);
       cw = *(const uint4*)(w + (o0 + wo) * in_f + c0 + wc);
     } else {
 #pragma unroll
