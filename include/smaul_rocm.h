@@ -166,6 +166,10 @@ int smaul_moe_dispatch(const int64_t* topi, const float* topw, int32_t* counts,
  * for all of its rows.  block_m 128 with bf16 activations, tile 64,
  * SMAUL_FLAG_ALIGNED_CODES and 16-byte aligned activations selects the
  * LDS-DMA kernels (the register-staged ones otherwise, on the same tiles).
+ * block_m 64 (never returned by smaul_moe_block_m; smaul_moe_forward picks it
+ * for small bf16 layers) runs the LDS-DMA kernels on 64-row tiles and needs
+ * their conditions (SMAUL_ERR_UNSUPPORTED otherwise); the outputs equal those
+ * of block_m 128 bit for bit.
  */
 int smaul_moe_block_m(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile,
                       int act_dtype);
