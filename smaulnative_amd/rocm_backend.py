@@ -543,13 +543,15 @@ class RocmBackend:
         out["block_m"] = block_m
         return out
 
-    def moe_stages(self, x2, gate_w, gate_b, experts, top_k, tile, events=None):
+    def moe_stages(self, x2, gate_w, gate_b, experts, top_k, tile, events=None, block_m=None):
         """The MoE layer as its five stages, each through its own C-ABI entry.
 
         Same results as ``moe_forward`` (which runs the same kernels from one
         call).  ``events``, if given, is a list of 6 ``torch.cuda.Event``
         recorded on the current stream before the router and after each stage
         (router, dispatch, gate_up, down, combine), for per-kernel timing.
+        ``block_m`` overrides ``smaul_moe_block_m``'s tile height (64: the
+        64-row LDS-DMA tiles that ``moe_forward`` takes for small layers).
         Returns (out [T,d], prob, topi, topw, dispatch dict).
         """
         lib = _lib.load()
@@ -567,7 +569,7 @@ class RocmBackend:
         gw = gate_w.detach().float().contiguous()
         gb = None if gate_b is None else gate_b.detach().float().contiguous()
         R = T * top_k
-        bm = lib.smaul_moe_block_m(T, d, h, E, top_k, tile, act)
+        bm = lib.smaul_moe_block_m(T, d, h, E, top_k, tile, act) if block_m is None else int(block_m)
         max_tiles = (R + bm - 1) // bm + E
         hdn = torch.empty(max(1, R), h, dtype=x2.dtype, device=dev)
         yperm = torch.empty(max(1, R), d, dtype=x2.dtype, device=dev)

@@ -507,6 +507,23 @@ def test_staged_call_equals_fused_call(T, d, h):
     assert torch.equal(counts, disp["counts"])
 
 
+@pytest.mark.parametrize("T,d,h,E,k", [(900, 512, 1280, 8, 2), (3000, 1024, 2560, 8, 2), (300, 256, 384, 2, 1)])
+def test_stage_entries_block_m_64(T, d, h, E, k):
+    """The stage entries on 64-row tiles (block_m 64, which moe_forward takes
+    for small layers) give the bits of 128-row tiles, whatever moe_forward
+    picks for the shape (T = 3000 at d = 1024: above its 64-row threshold)."""
+    print(f"case stages block_m 64 T={T} d={d} h={h} E={E} k={k}", flush=True)
+    x, gw, gb, experts = make_moe(5 + T, T, d, h, E, k)
+    b = be()
+    exd = to_dev_experts(experts)
+    args = (x.to(DEV), gw.to(DEV), gb.to(DEV), exd, k, 64)
+    o64 = b.moe_stages(*args, block_m=64)[0]
+    o128 = b.moe_stages(*args, block_m=128)[0]
+    of = b.moe_forward(*args)[0]
+    torch.cuda.synchronize()
+    assert torch.equal(o64, o128) and torch.equal(o64, of)
+
+
 def test_moe_decode_unsplit_k():
     """K/64 = 18 blocks fits no streaming split (2, 4 or 5 blocks per wave over
     at most 8 waves): both projections run the split-K decode kernel."""
