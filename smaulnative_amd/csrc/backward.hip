@@ -59,9 +59,10 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 // lane l holds row / column l % 32 of the operands at k = 8 (l / 32) + 0..7,
 // and column l % 32, rows (r / 4) 8 + (l / 32) 4 + r % 4 of the sums).  Per
 // chunk of BWM_K = 64 o: every thread turns 16 values of g * s (one row, 16
-// consecutive o) into their three bf16 terms and writes them, and 16 codes of
-// one o (16 consecutive columns) transposed, to LDS; the loads of the next
-// chunk are issued before the chunk's MFMAs.  VEC: g rows and code rows are
+// consecutive o) into their three bf16 terms and writes them to LDS, and
+// transposes a 4 x 4 block of codes (4 o x 4 columns, v_perm) into four
+// column words of 4 o; the loads of the next chunk are issued before the
+// chunk's MFMAs.  VEC: g rows and code rows are
 // 16-byte aligned and whole chunks are in range (out_f % 64 == 0, in_f % 64
 // == 0), so they load as 16-byte vectors.
 constexpr int BWM_K = 64;
@@ -72,7 +73,9 @@ fp8_backward_input_mfma_kernel(const float* __restrict__ g, const uint8_t* __res
                                const float* __restrict__ s, float* __restrict__ dx, int64_t rows, int64_t in_f,
                                int64_t out_f, int64_t tile, int64_t nt) {
   __shared__ __attribute__((aligned(16))) uint16_t sa[3][BW_T][BWM_K + 8];  // terms of g * s, [row][o]
-  __shared__ __attribute__((aligned(16))) uint8_t sw[BW_T][BWM_K + 16];     // codes, [column][o]
+  // codes, [column][o]; rows of 72 bytes: the word writes of a wave meet at
+  // most two to a bank, the 8-byte fragment reads none
+  __shared__ __attribute__((aligned(16))) uint8_t sw[BW_T][BWM_K + 8];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   // Workgroup b runs on XCD b % 8: each XCD takes a contiguous band of the
@@ -88,12 +91,12 @@ fp8_backward_input_mfma_kernel(const float* __restrict__ g, const uint8_t* __res
     c0 = (lin % nc) * BW_T;
   }
   const int64_t kb = c0 / tile;
-  // this thread's staging: g row ar, 16 o from ao; codes of o = wo, 16 columns from wc
+  // this thread's staging: g row ar, 16 o from ao; codes of o wo..wo+3 x columns wc..wc+3
   const int ar = tid >> 2, ao = (tid & 3) * 16;
-  const int wo = tid >> 2, wc = (tid & 3) * 16;
+  const int wo = (tid >> 4) * 4, wc = (tid & 15) * 4;
   const int64_t gr = r0 + ar;
   float gv[16], sv[16];
-  uint4 cw;
+  uint32_t cw[4];  // row wo + r, columns wc..wc+3 (byte c = column wc + c)
   auto load = [&](int64_t o0) {
     if constexpr (VEC) {
       const float4* gp = (const float4*)(g + (gr < rows ? gr : rows - 1) * out_f + o0 + ao);
@@ -110,7 +113,8 @@ fp8_backward_input_mfma_kernel(const float* __restrict__ g, const uint8_t* __res
       const float sl = s[(o0 + (lane & 3) * 16 + (lane >> 2)) * nt + kb];
 #pragma unroll
       for (int j = 0; j < 16; ++j) sv[j] = __shfl(sl, (j << 2) | (lane & 3), 64);
-      cw = *(const uint4*)(w + (o0 + wo) * in_f + c0 + wc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) cw[r] = *(const uint32_t*)(w + (o0 + wo + r) * in_f + c0 + wc);
     } else {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -118,16 +122,17 @@ fp8_backward_input_mfma_kernel(const float* __restrict__ g, const uint8_t* __res
         gv[j] = (gr < rows && o < out_f) ? g[gr * out_f + o] : 0.0f;
         sv[j] = o < out_f ? s[o * nt + kb] : 0.0f;
       }
-      const int64_t o = o0 + wo;
-      uint32_t b[16];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int64_t i = c0 + wc + j;
-        b[j] = (o < out_f && i < in_f) ? w[o * in_f + i] : 0u;  // code 0 decodes to +0
+      for (int r = 0; r < 4; ++r) {
+        const int64_t o = o0 + wo + r;
+        uint32_t v = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int64_t i = c0 + wc + c;
+          v |= ((o < out_f && i < in_f) ? (uint32_t)w[o * in_f + i] : 0u) << (8 * c);  // code 0 decodes to +0
+        }
+        cw[r] = v;
       }
-      cw = make_uint4(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24), b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24),
-                      b[8] | (b[9] << 8) | (b[10] << 16) | (b[11] << 24),
-                      b[12] | (b[13] << 8) | (b[14] << 16) | (b[15] << 24));
     }
   };
   f32x16_t acc;
@@ -152,9 +157,16 @@ fp8_backward_input_mfma_kernel(const float* __restrict__ g, const uint8_t* __res
         *(uint4*)&sa[p][ar][ao] = make_uint4(t[p][0], t[p][1], t[p][2], t[p][3]);
         *(uint4*)&sa[p][ar][ao + 8] = make_uint4(t[p][4], t[p][5], t[p][6], t[p][7]);
       }
-      const uint32_t cwv[4] = {cw.x, cw.y, cw.z, cw.w};
-#pragma unroll
-      for (int j = 0; j < 16; ++j) sw[wc + j][wo] = (uint8_t)(cwv[j >> 2] >> ((j & 3) * 8));
+      // 4 x 4 byte transpose: column word c = (row 0 byte c, ..., row 3 byte c)
+      // (v_perm: selector bytes 0-3 pick from the second operand, 4-7 from the first)
+      const uint32_t lo01 = __builtin_amdgcn_perm(cw[1], cw[0], 0x05010400u);
+      const uint32_t hi01 = __builtin_amdgcn_perm(cw[1], cw[0], 0x07030602u);
+      const uint32_t lo23 = __builtin_amdgcn_perm(cw[3], cw[2], 0x05010400u);
+      const uint32_t hi23 = __builtin_amdgcn_perm(cw[3], cw[2], 0x07030602u);
+      *(uint32_t*)&sw[wc + 0][wo] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+      *(uint32_t*)&sw[wc + 1][wo] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+      *(uint32_t*)&sw[wc + 2][wo] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+      *(uint32_t*)&sw[wc + 3][wo] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
     }
     __syncthreads();
     if (o0 + BWM_K < out_f) load(o0 + BWM_K);
