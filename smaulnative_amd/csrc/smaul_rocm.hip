@@ -4737,7 +4737,8 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
   int64_t bm = pick_block_m(T, d, h, E, k, tile, act_dtype);
   if (bm == CfgBig::BM && act_dtype == SMAUL_DTYPE_BF16 &&
       ((R + CfgBig::BM - 1) / CfgBig::BM + E) * (h / 128) < 4 * (int64_t)cu_count()) {
-    // 64-row tiles where both projections fit the LDS-DMA kernels
+    // a 128-row gate/up grid under four workgroups per CU: 64-row tiles
+    // (DMA_SMALL_BM) where both projections fit the LDS-DMA kernels
     const int64_t mt = (R + DMA_SMALL_BM - 1) / DMA_SMALL_BM + E;
     GemmArgs g{};
     g.x = x;
