@@ -524,6 +524,20 @@ def test_stage_entries_block_m_64(T, d, h, E, k):
     assert torch.equal(o64, o128) and torch.equal(o64, of)
 
 
+def test_moe_64_row_tiles_empty_experts():
+    """64-row tiles with five of eight experts never chosen (empty segments)
+    and one expert holding most rows."""
+    print("case 64-row tiles, empty experts", flush=True)
+    T, d, h, E, k = 700, 256, 384, 8, 2
+    x, gw, gb, experts = make_moe(7, T, d, h, E, k, skew=(9.0, [3, 4, 5, 6, 7], 9.0))
+    ref = oracle.moe_forward(x, gw, gb, experts, k)
+    out, prob, topi, counts = gpu_moe(x, gw, gb, experts, k)
+    assert torch.equal(topi.reshape(-1, k), ref.topi.reshape(-1, k))
+    assert counts.tolist() == ref.counts
+    assert ref.counts[3:] == [0] * 5 and max(ref.counts) == T
+    assert rel_l2(out.float(), ref.out.float()) < 2e-3
+
+
 def test_moe_decode_unsplit_k():
     """K/64 = 18 blocks fits no streaming split (2, 4 or 5 blocks per wave over
     at most 8 waves): both projections run the split-K decode kernel."""
