@@ -482,10 +482,12 @@ def decode_bench(be, steps, warmup, layers=24, T=64, d=1024, h=2560, E=8, k=2):
 
 def peaks():
     """Measured ceilings: the dense bf16 MFMA rate of v_mfma_f32_32x32x16_bf16
-    (smaul_peak_mfma: 8 independent chains per wave, 1 and 2 waves per SIMD)
-    and the HBM read rate of 16-byte loads over a 4 GiB buffer, far beyond the
-    256 MB Infinity Cache (smaul_peak_stream).  Median of 10 after 3 warm-ups,
-    HIP events on the launch stream."""
+    (smaul_peak_mfma: 8 independent chains per wave, 1 and 2 waves per SIMD),
+    the HBM read rate of 16-byte loads over a 4 GiB buffer, far beyond the
+    256 MB Infinity Cache (smaul_peak_stream), and the per-CU rate at which
+    global_load_lds_dwordx4 fills LDS from L2-resident data (smaul_peak_lds_dma,
+    the prefill GEMM's staging).  Median of 10 after 3 warm-ups, HIP events on
+    the launch stream."""
     import torch
     from smaulnative_amd import _lib
     lib = _lib.load()
@@ -512,9 +514,22 @@ def peaks():
                                                                   st), "peak_stream"), 10, 3)
     res["hbm_read_GBps"] = nbytes / (ms * 1e-3) / 1e9
     res["hbm_frac_of_8000"] = res["hbm_read_GBps"] / 8000.0
+    del buf
+    # LDS-DMA fill rate from L2-resident data (the prefill GEMM's staging path): one and two
+    # workgroups of 4 waves per CU, each reading its own 64 KB
+    dma_iters = 400
+    for per_cu in (1, 2):
+        wg = cus * per_cu
+        src = torch.ones(wg * 65536, dtype=torch.uint8, device=dev)
+        dsink = torch.zeros(wg, dtype=torch.int32, device=dev)
+        ms = event_median_ms(lambda: _lib.check(lib.smaul_peak_lds_dma(src.data_ptr(), src.numel(), dsink.data_ptr(),
+                                                                       wg, dma_iters, st), "peak_lds_dma"), 10, 3)
+        gbps = wg * 4 * dma_iters * 8 * 1024 / (ms * 1e-3) / 1e9
+        res[f"lds_dma_GBps_per_cu_{per_cu}_wg"] = gbps / cus
     res["method"] = ("median of 10 launches after 3 warm-ups, HIP events on the launch stream; MFMA: 4096 rounds "
                      "of 8 independent 32x32x16 bf16 MFMAs per wave; HBM: a 4 GiB read with 16-byte loads, "
-                     f"{cus * 8} workgroups of 256 threads")
+                     f"{cus * 8} workgroups of 256 threads; LDS DMA: 400 rounds of 8 x 1 KB "
+                     "global_load_lds_dwordx4 per wave from L2-resident 64 KB regions, 1 or 2 workgroups per CU")
     return res
 
 

@@ -437,9 +437,15 @@ int smaul_fp8_backward_input(const float* g, const uint8_t* w, const float* s, f
  * smaul_peak_stream: reads `bytes` (a multiple of 16) from src with 16-byte
  *   loads, grid-stride over `workgroups` x 256 threads; out (one uint32) is
  *   written only in a case that does not occur.
+ * smaul_peak_lds_dma: `workgroups` x 4 waves, each copying `iters` rounds of
+ *   8 x 1 KB into LDS with global_load_lds_dwordx4 (the prefill GEMM's
+ *   staging) from its workgroup's 64 KB of src (bytes >= workgroups * 64 KB);
+ *   out holds one uint32 per workgroup.
  */
 int smaul_peak_mfma(float* out, int workgroups, int iters, hipStream_t stream);
 int smaul_peak_stream(const void* src, int64_t bytes, uint32_t* out, int workgroups, hipStream_t stream);
+int smaul_peak_lds_dma(const void* src, int64_t bytes, uint32_t* out, int workgroups, int iters,
+                       hipStream_t stream);
 
 /*
  * Host-side self-test of the top-k selection order used by the router (no GPU

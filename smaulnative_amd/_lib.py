@@ -67,6 +67,7 @@ SIGNATURES = {
     "smaul_debug_tail_wait": (_I, [_I, _I]),
     "smaul_peak_mfma": (_I, [_P, _I, _I, _P]),
     "smaul_peak_stream": (_I, [_P, _I64, _P, _I, _P]),
+    "smaul_peak_lds_dma": (_I, [_P, _I64, _P, _I, _I, _P]),
     "smaul_selftest_topk": (_I, [_P, _I64, _I64, _P]),
 }
 

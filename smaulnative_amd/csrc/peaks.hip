@@ -1,8 +1,10 @@
 // peaks.hip -- measured ceilings of MI355X (gfx950) for the roofline of this
 // library's kernels: the dense bf16 MFMA rate of the instruction the prefill
-// GEMM issues (v_mfma_f32_32x32x16_bf16) and the HBM read rate of a stream of
-// 16-byte loads.  Measurement only (bench.py --peaks); no reference
-// counterpart and nothing on the MoE path calls them.
+// GEMM issues (v_mfma_f32_32x32x16_bf16), the HBM read rate of a stream of
+// 16-byte loads, and the rate at which the GEMM's LDS-DMA loads
+// (global_load_lds_dwordx4) fill LDS from L2-resident data.  Measurement only
+// (bench.py --peaks); no reference counterpart and nothing on the MoE path
+// calls them.
 #include "smaul_common.h"
 
 using smaul::check_launch;
@@ -54,6 +56,44 @@ __global__ void __launch_bounds__(256) peak_stream_kernel(const uint4* __restric
   if (x == 0x9e3779b9u) out[0] = x;
 }
 
+// LDS DMA, as the prefill GEMM issues it: each lane copies 16 bytes from
+// base + off to LDS address lds + 16 * lane (M0 = lds).
+typedef __attribute__((address_space(3))) void* lds_vptr_t;
+__device__ __forceinline__ uint32_t lds_offset(const void* p) { return (uint32_t)(uintptr_t)(lds_vptr_t)p; }
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(off), "s"(uniform_ptr(base)) : "memory");
+}
+
+constexpr int PEAK_DMA_REGION = 64;  // 1 KB chunks read by one workgroup (64 KB, L2-resident after a pass)
+constexpr int PEAK_DMA_SLOTS = 8;    // 1 KB LDS slots per wave
+
+// Every wave copies `iters` rounds of 8 chunks of 1 KB from its workgroup's
+// 64 KB region into its LDS slots, two rounds in flight; one word of LDS is
+// stored at the end so the copies are not dead.
+__global__ void __launch_bounds__(256) peak_lds_dma_kernel(const char* __restrict__ src, int iters, uint32_t* out) {
+  __shared__ __attribute__((aligned(1024))) char smem[4 * PEAK_DMA_SLOTS * 1024];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const char* base = src + (size_t)blockIdx.x * PEAK_DMA_REGION * 1024;
+  const uint32_t lds0 = lds_offset(&smem[0]);
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int s = 0; s < PEAK_DMA_SLOTS; ++s)
+      dma16(base + (size_t)(((it * PEAK_DMA_SLOTS + s) * 7 + wave) % PEAK_DMA_REGION) * 1024, lane * 16,
+            lds0 + (wave * PEAK_DMA_SLOTS + s) * 1024);
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) out[blockIdx.x] = *(const uint32_t*)&smem[0];
+}
+
 }  // namespace
 
 extern "C" {
@@ -62,6 +102,15 @@ int smaul_peak_mfma(float* out, int workgroups, int iters, hipStream_t stream) {
   if (!out || workgroups < 1 || iters < 1) return fail(SMAUL_ERR_INVALID, "peak_mfma: bad arguments");
   hipLaunchKernelGGL(peak_mfma_kernel, dim3((unsigned)workgroups), dim3(256), 0, stream, out, iters);
   return check_launch("peak_mfma_kernel");
+}
+
+int smaul_peak_lds_dma(const void* src, int64_t bytes, uint32_t* out, int workgroups, int iters,
+                       hipStream_t stream) {
+  if (!src || !out || workgroups < 1 || iters < 1 || bytes < (int64_t)workgroups * PEAK_DMA_REGION * 1024)
+    return fail(SMAUL_ERR_INVALID, "peak_lds_dma: bad arguments (src needs 64 KB per workgroup)");
+  hipLaunchKernelGGL(peak_lds_dma_kernel, dim3((unsigned)workgroups), dim3(256), 0, stream, (const char*)src, iters,
+                     out);
+  return check_launch("peak_lds_dma_kernel");
 }
 
 int smaul_peak_stream(const void* src, int64_t bytes, uint32_t* out, int workgroups, hipStream_t stream) {
