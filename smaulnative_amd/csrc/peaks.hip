@@ -82,10 +82,12 @@ __global__ void __launch_bounds__(256) peak_lds_dma_kernel(const char* __restric
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const char* base = src + (size_t)blockIdx.x * PEAK_DMA_REGION * 1024;
   const uint32_t lds0 = lds_offset(&smem[0]);
+  static_assert((PEAK_DMA_REGION & (PEAK_DMA_REGION - 1)) == 0, "chunk index taken modulo a power of two");
   for (int it = 0; it < iters; ++it) {
+    const int r = it & (PEAK_DMA_REGION - 1);  // the chunk pattern repeats every 64 rounds; no overflow
 #pragma unroll
     for (int s = 0; s < PEAK_DMA_SLOTS; ++s)
-      dma16(base + (size_t)(((it * PEAK_DMA_SLOTS + s) * 7 + wave) % PEAK_DMA_REGION) * 1024, lane * 16,
+      dma16(base + (size_t)(((r * PEAK_DMA_SLOTS + s) * 7 + wave) & (PEAK_DMA_REGION - 1)) * 1024, lane * 16,
             lds0 + (wave * PEAK_DMA_SLOTS + s) * 1024);
     asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
   }
