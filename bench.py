@@ -205,6 +205,14 @@ def c2_bench(be, steps, warmup):
            "tokens_per_s": rows / (ms * 1e-3), "ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
            "mfma_frac": flops / (ms * 1e-3) / PEAK_BF16_FLOPS, "flops_per_step": flops,
            "timing": f"median of {n} back-to-back calls, each between two HIP events on the launch stream"}
+    # the fp32 activations the config specifies: x and hdn as bf16 hi / lo
+    # planes, twice the MFMA work of the bf16 figure above (frac counts the
+    # algorithmic FLOPs once)
+    xf = x32.to("cuda")
+    fms = event_median_ms(lambda: be.swiffn_forward(xf, bufs, 64), n, warmup)
+    res["f32_x"] = {"ms_per_step": fms, "tokens_per_s": rows / (fms * 1e-3), "tflops": flops / (fms * 1e-3) / 1e12,
+                    "mfma_frac": flops / (fms * 1e-3) / PEAK_BF16_FLOPS,
+                    "workload": "the same FFN with fp32 x (the config's activations): fp32 out and hdn"}
     lin = {}
     for name, xx in (("f32_x", x32.to("cuda")), ("bf16_x", x)):
         g = be.fp8_forward(xx, bufs[0], bufs[1], d, h, 64)

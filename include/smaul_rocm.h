@@ -206,7 +206,12 @@ int smaul_moe_combine(const void* yperm, int act_dtype, const int64_t* topi,
  * codes uint8 [h, d] with fp32 scales [h, ceil(d/tile)]; down codes [d, h],
  * scales [d, ceil(h/tile)]; out: act_dtype [rows, d].  x, codes, out and the
  * workspace 16-byte aligned; d and h multiples of 16.  `workspace` holds
- * smaul_swiffn_workspace_size(rows, h, act_dtype) bytes.
+ * smaul_swiffn_workspace_size(rows, h, act_dtype) bytes.  With fp32 x the
+ * size includes room for bf16 hi / lo planes of x and of hdn: when tile is 64,
+ * d and h are multiples of 128, d <= h and rows > 64, both GEMMs run on the
+ * LDS-DMA kernels over the two planes (products within 2^-18 relative of
+ * fp32); a workspace of only the first align256(rows * h * 4) bytes, or any
+ * other shape, runs the register-staged kernels.
  */
 int64_t smaul_swiffn_workspace_size(int64_t rows, int64_t h, int act_dtype);
 

@@ -138,6 +138,11 @@ struct GemmArgs {
   // reads activation block kt and weight / scale block kt mod (kw / 64).
   // 0: the weights span K.
   int64_t kw;
+  // SwiGLU with fp32 output only: when > 0 the products are stored as their
+  // bf16 hi / lo split (split_bf16), hi at y[row * ldy + col] and lo at
+  // y[row * ldy + y_lo + col] (bf16 elements): the two planes the next GEMM
+  // of fp32 activations reads.
+  int64_t y_lo;
 };
 
 // Where an expert's codes and scales for column n and 64-wide K block kb
@@ -691,10 +696,12 @@ struct DmaGemmCfg {
   static_assert(LDS <= 160 * 1024, "LDS budget");
 };
 
-// OUT_F32 (not SWIGLU): the fp32 sums are stored as they are (the dense
-// fp8_forward contract), straight from the MFMA layout; otherwise they are
-// rounded to bf16 and stored through LDS (plain) or, with the SwiGLU
-// epilogue, as 8-byte row pieces after an exchange inside each quad of lanes.
+// OUT_F32: the fp32 sums are stored as they are (the dense fp8_forward
+// contract), straight from the MFMA layout; with SWIGLU, silu(gate) * up in
+// fp32 (SwiFFN with fp32 activations, whose products the reference keeps in
+// fp32).  Otherwise the sums are rounded to bf16 and stored through LDS
+// (plain) or, with the SwiGLU epilogue, as 8-byte row pieces after an
+// exchange inside each quad of lanes.
 //
 // X32 (OUT_F32 only): fp32 activations.  The stage's rows are staged as fp32
 // and, after its barrier, split in place by all threads into x = hi + lo
@@ -706,8 +713,7 @@ template <int BM, int BN, int WM, int WN, int NSTAGE, bool SWIGLU, bool CANON, b
 // Tiles of at most 128 x 128 staged columns fit three workgroups per CU.
 __global__ void __launch_bounds__(WM * WN * 64, (BM * BN <= 128 * 128 ? 3 : 2))
 fp8_gemm_dma_kernel(GemmArgs p) {
-  static_assert(!(OUT_F32 && SWIGLU), "the SwiGLU epilogue rounds to bf16");
-  static_assert(!X32 || OUT_F32, "fp32 activations are the fp8_forward path");
+  static_assert(!X32 || (OUT_F32 && !SWIGLU), "fp32 activations split in LDS are the fp8_forward path");
   using C = DmaGemmCfg<BM, BN, WM, WN, NSTAGE, SWIGLU, X32>;
   constexpr int NW = C::NW, BNO = C::BNO, TM = C::TM, TN = C::TN, TNO = C::TNO, FM = C::FM, FN = C::FN,
                 FNO = C::FNO, A_BYTES = C::A_BYTES, B_BYTES = C::B_BYTES, STAGE = C::STAGE,
@@ -985,18 +991,23 @@ fp8_gemm_dma_kernel(GemmArgs p) {
   wait_vm<0>();
   if constexpr (OUT_F32) {
     // A lane holds column l32 of each 32x32 tile, rows (r/4)*8 + g*4 + r%4:
-    // each store instruction writes 128 contiguous bytes of two rows.
+    // each store instruction writes 128 contiguous bytes of two rows.  SwiGLU:
+    // tile j (gate) and tile j + FNO (up) hold the same output columns; split
+    // into planes (y_lo > 0), the register epilogue below stores them.
+    if (!SWIGLU || p.y_lo == 0) {  // uniform
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
+        for (int j = 0; j < FNO; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int lr = wm * TM + i * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
-          if (lr < rows_here)
-            ((float*)p.y)[(int64_t)(row0 + lr) * p.ldy + n0 + wn * TN + j * 32 + l32] = acc[i][j][r];
-        }
-    return;
+          for (int r = 0; r < 16; ++r) {
+            const int lr = wm * TM + i * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
+            float v = acc[i][j][r];
+            if constexpr (SWIGLU) v = silu_f(v) * acc[i][j + FNO][r];
+            if (lr < rows_here) ((float*)p.y)[(int64_t)(row0 + lr) * p.ldy + n0 + wn * TNO + j * 32 + l32] = v;
+          }
+      return;
+    }
   }
 
   if constexpr (!SWIGLU) {
@@ -1037,17 +1048,33 @@ fp8_gemm_dma_kernel(GemmArgs p) {
   // ---- SwiGLU epilogue: bf16 rows stored from registers ---------------------
   // A lane holds column l32 of each 32x32 tile, rows (r/4)*8 + g*4 + r%4.
   // Gate and up are rounded to bf16 first, as the reference's FP8Linear
-  // outputs are, then silu(gate)*up is rounded again.  Two exchanges inside
-  // each quad of lanes (DPP quad permutes, no LDS, no barrier) turn a lane's
-  // four rows x one column into one row x four columns: lane 4m+s ends with
-  // row (r/4)*8 + g*4 + s, columns 4m..4m+3, so the 8 lanes of a row store 64
-  // contiguous bytes and the WN waves complete the row.
+  // outputs are, then silu(gate)*up is rounded again (OUT_F32, the planes of
+  // fp32 activations: silu(gate)*up in fp32, stored as its bf16 hi and lo
+  // terms, split_bf16).  Two exchanges inside each quad of lanes (DPP quad
+  // permutes, no LDS, no barrier) turn a lane's four rows x one column into
+  // one row x four columns: lane 4m+s ends with row (r/4)*8 + g*4 + s,
+  // columns 4m..4m+3, so the 8 lanes of a row store 64 contiguous bytes and
+  // the WN waves complete the row.
   const int qs = lane & 3;
   const bool hi2 = (lane & 2) != 0;
   // v_perm selectors for the lane ^ 1 step (src0 = partner, src1 = own):
   // even lanes take own bytes 0-1 then partner bytes 0-1, odd lanes partner
   // bytes 2-3 then own bytes 2-3
   const uint32_t psel = (lane & 1) ? 0x03020706u : 0x05040100u;
+  // d0 = rows +0 (low half), +1 (high half) of column l32, d1 = rows +2, +3
+  // -> this lane's row piece (columns 4m..4m+3 of row +s)
+  auto exchange = [&](uint32_t d0, uint32_t d1) -> uint2 {
+    // lane ^ 1: even lanes take rows +0 / +2 of columns (c, c+1), odd
+    // lanes rows +1 / +3 of columns (c-1, c)
+    const uint32_t e0 =
+        __builtin_amdgcn_perm((uint32_t)__builtin_amdgcn_mov_dpp((int)d0, 0xB1, 0xF, 0xF, false), d0, psel);
+    const uint32_t e1 =
+        __builtin_amdgcn_perm((uint32_t)__builtin_amdgcn_mov_dpp((int)d1, 0xB1, 0xF, 0xF, false), d1, psel);
+    // lane ^ 2: lanes s < 2 keep row +s (e0) and take columns 4m+2..4m+3
+    // of it; lanes s >= 2 keep row +s (e1) and take columns 4m..4m+1
+    const uint32_t rv = (uint32_t)__builtin_amdgcn_mov_dpp((int)(hi2 ? e0 : e1), 0x4E, 0xF, 0xF, false);
+    return make_uint2(hi2 ? rv : e0, hi2 ? e1 : rv);
+  };
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -1058,26 +1085,31 @@ fp8_gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int r = a * 4 + q;
-          const uint32_t gu = pack_bf16(acc[i][j][r], acc[i][j + FNO][r]);  // gate, up rounded to bf16
-          const float gr = __builtin_bit_cast(float, gu << 16);
-          const float ur = __builtin_bit_cast(float, gu & 0xffff0000u);
-          v[q] = silu_f(gr) * ur;
+          if constexpr (OUT_F32) {
+            v[q] = silu_f(acc[i][j][r]) * acc[i][j + FNO][r];
+          } else {
+            const uint32_t gu = pack_bf16(acc[i][j][r], acc[i][j + FNO][r]);  // gate, up rounded to bf16
+            const float gr = __builtin_bit_cast(float, gu << 16);
+            const float ur = __builtin_bit_cast(float, gu & 0xffff0000u);
+            v[q] = silu_f(gr) * ur;
+          }
         }
-        const uint32_t d0 = pack_bf16(v[0], v[1]);  // rows +0 (low half), +1 (high half), column l32
-        const uint32_t d1 = pack_bf16(v[2], v[3]);  // rows +2, +3
-        // lane ^ 1: even lanes take rows +0 / +2 of columns (c, c+1), odd
-        // lanes rows +1 / +3 of columns (c-1, c)
-        const uint32_t e0 =
-            __builtin_amdgcn_perm((uint32_t)__builtin_amdgcn_mov_dpp((int)d0, 0xB1, 0xF, 0xF, false), d0, psel);
-        const uint32_t e1 =
-            __builtin_amdgcn_perm((uint32_t)__builtin_amdgcn_mov_dpp((int)d1, 0xB1, 0xF, 0xF, false), d1, psel);
-        // lane ^ 2: lanes s < 2 keep row +s (e0) and take columns 4m+2..4m+3
-        // of it; lanes s >= 2 keep row +s (e1) and take columns 4m..4m+1
-        const uint32_t rv = (uint32_t)__builtin_amdgcn_mov_dpp((int)(hi2 ? e0 : e1), 0x4E, 0xF, 0xF, false);
-        const uint2 o = make_uint2(hi2 ? rv : e0, hi2 ? e1 : rv);
         const int lr = wm * TM + i * 32 + a * 8 + g * 4 + qs;
-        if (lr < rows_here)
-          *(uint2*)((uint16_t*)p.y + (int64_t)(row0 + lr) * p.ldy + n0 + wn * TNO + j * 32 + (l32 & ~3)) = o;
+        uint16_t* dst = (uint16_t*)p.y + (int64_t)(row0 + lr) * p.ldy + n0 + wn * TNO + j * 32 + (l32 & ~3);
+        if constexpr (OUT_F32) {
+          uint32_t h[4], l[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) split_bf16(v[q], h[q], l[q]);
+          const uint2 oh = exchange(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+          const uint2 ol = exchange(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+          if (lr < rows_here) {
+            *(uint2*)dst = oh;
+            *(uint2*)(dst + p.y_lo) = ol;
+          }
+        } else {
+          const uint2 o = exchange(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+          if (lr < rows_here) *(uint2*)dst = o;
+        }
       }
     }
   }
@@ -4070,6 +4102,14 @@ __global__ void __launch_bounds__(256) split_planes_kernel(const float* __restri
   }
 }
 
+// x [rows, K] fp32 (K % 8 == 0, 16-byte aligned) -> planes [rows, 2K] bf16
+int launch_split_planes(const float* x, uint16_t* planes, int64_t rows, int64_t K, hipStream_t stream) {
+  const int64_t n8 = rows * (K / 8);
+  const int64_t blocks = std::min<int64_t>((n8 + 255) / 256, 4096);
+  hipLaunchKernelGGL(split_planes_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, x, planes, rows, K);
+  return check_launch("split_planes_kernel");
+}
+
 // The two-plane LDS-DMA path of smaul_fp8_linear_ws applies (fp32 x, tile
 // 64, shapes the DMA GEMM takes): the dense tile, else -1.
 int planes_tile(int x_dtype, const void* x, const uint8_t* w, int64_t rows, int64_t in_f, int64_t out_f,
@@ -4119,11 +4159,7 @@ int smaul_fp8_linear_ws(const void* x, int x_dtype, const uint8_t* w, const floa
   a.E = 1;
   if (!dma_gemm_ok(a, SMAUL_DTYPE_BF16, flags | SMAUL_FLAG_ALIGNED_CODES, rows, 128))
     return smaul_fp8_linear(x, x_dtype, w, s, y, y_dtype, rows, in_f, out_f, tile, flags, stream);
-  const int64_t n8 = rows * (in_f / 8);
-  const int64_t blocks = std::min<int64_t>((n8 + 255) / 256, 4096);
-  hipLaunchKernelGGL(split_planes_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (const float*)x,
-                     (uint16_t*)workspace, rows, in_f);
-  const int rc = check_launch("split_planes_kernel");
+  const int rc = launch_split_planes((const float*)x, (uint16_t*)workspace, rows, in_f, stream);
   if (rc != SMAUL_OK) return rc;
   const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
   return canon ? launch_dense_dma<false, true, true>(a, dt, stream) : launch_dense_dma<false, false, true>(a, dt, stream);
@@ -4438,9 +4474,14 @@ int smaul_moe_down(const void* hdn, int act_dtype, const uint8_t* const* down_w,
 // dense form (no segment table, no row gather).  gate and up run as one
 // launch with the SwiGLU epilogue into hdn (the workspace), then down writes
 // out directly.
+// bf16: hdn [rows, h].  fp32: two parts of align256(rows * h * 4) bytes; the
+// register-staged kernels keep hdn in fp32 in the first, the LDS-DMA path
+// (swiffn_f32_planes) puts the bf16 hi / lo planes of x in the first and those
+// of hdn in the second.  A workspace of only the first part runs the
+// register-staged kernels.
 int64_t smaul_swiffn_workspace_size(int64_t rows, int64_t h, int act_dtype) {
   if (rows < 0 || h <= 0 || !dtype_ok(act_dtype)) return -1;
-  return align256(rows * h * (act_dtype == SMAUL_DTYPE_BF16 ? 2 : 4));
+  return act_dtype == SMAUL_DTYPE_BF16 ? align256(rows * h * 2) : align256(rows * h * 4) + align256(rows * h * 4);
 }
 
 static int dense_gemm(bool swiglu, const void* act, int act_dtype, const uint8_t* w1, const float* s1,
@@ -4485,6 +4526,66 @@ static int dense_gemm(bool swiglu, const void* act, int act_dtype, const uint8_t
                : gemm_dispatch_moe<CfgBig, CfgBigF32>(a, swiglu, act_dtype, mt, canon, stream);
 }
 
+// SwiFFN with fp32 activations on the LDS-DMA kernels: x is split into bf16
+// hi / lo planes, gate+up runs over both (K doubled, each weight block read
+// for its hi and its lo half) and its SwiGLU epilogue, in fp32, stores the
+// products already split into the two planes of hdn, over which the down
+// projection runs with fp32 output: every value the reference forms in fp32
+// stays within 2^-18 relative of it.  The planes of x go into the workspace's
+// first part (rows * 2d bf16 <= rows * h fp32), those of hdn into the second.
+// Returns 1 (nothing launched) when the shape does not fit: tile 64, d and h
+// multiples of 128, d <= h, more than 64 rows, and the kernels' offset limits.
+static int swiffn_f32_planes(const float* x, const uint8_t* gw, const float* gs, const uint8_t* uw, const float* us,
+                             const uint8_t* dw, const float* ds, float* out, char* ws, int64_t hdn_bytes,
+                             int64_t rows, int64_t d, int64_t h, int64_t tile, int flags, hipStream_t stream) {
+  if (tile != 64 || d % 128 != 0 || h % 128 != 0 || d > h || rows <= 64) return 1;
+  uint16_t* xplanes = (uint16_t*)ws;
+  uint16_t* hplanes = (uint16_t*)(ws + hdn_bytes);
+  GemmArgs a{};
+  a.x = xplanes;
+  a.ldx = 2 * d;
+  a.w = gw;
+  a.s = gs;
+  a.w2 = uw;
+  a.s2 = us;
+  a.y = hplanes;
+  a.ldy = 2 * h;
+  a.y_lo = h;
+  a.K = 2 * d;
+  a.kw = d;
+  a.N = h;
+  a.nt = d / 64;
+  a.tile = 64;
+  a.R = rows;
+  a.E = 1;
+  a.tiled = (flags & SMAUL_FLAG_TILED_LAYOUT) != 0;
+  GemmArgs b = a;
+  b.y_lo = 0;
+  b.x = hplanes;
+  b.ldx = 2 * h;
+  b.w = dw;
+  b.s = ds;
+  b.w2 = nullptr;
+  b.s2 = nullptr;
+  b.y = out;
+  b.ldy = d;
+  b.K = 2 * h;
+  b.kw = h;
+  b.N = d;
+  b.nt = h / 64;
+  const int fl = flags | SMAUL_FLAG_ALIGNED_CODES;  // swiffn requires 16-byte aligned codes
+  const int dtg = pick_dense_tile(true, rows, h), dtd = pick_dense_tile(false, rows, d);
+  if (dtg < 0 || dtd < 0 || !dma_gemm_ok(a, SMAUL_DTYPE_BF16, fl, rows, 128) ||
+      !dma_gemm_ok(b, SMAUL_DTYPE_BF16, fl, rows, 128))
+    return 1;
+  const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
+  int rc = launch_split_planes(x, xplanes, rows, d, stream);
+  if (rc != SMAUL_OK) return rc;
+  rc = canon ? launch_dense_dma<true, true, true>(a, dtg, stream) : launch_dense_dma<true, false, true>(a, dtg, stream);
+  if (rc != SMAUL_OK) return rc;
+  return canon ? launch_dense_dma<false, true, true>(b, dtd, stream) : launch_dense_dma<false, false, true>(b, dtd, stream);
+}
+
 int smaul_swiffn_forward(const void* x, int act_dtype, const uint8_t* gate_w8, const float* gate_s,
                          const uint8_t* up_w8, const float* up_s, const uint8_t* down_w8, const float* down_s,
                          void* out, void* workspace, int64_t workspace_bytes, int64_t rows, int64_t d, int64_t h,
@@ -4496,9 +4597,10 @@ int smaul_swiffn_forward(const void* x, int act_dtype, const uint8_t* gate_w8, c
   if (d % 16 != 0 || h % 16 != 0) return fail(SMAUL_ERR_UNSUPPORTED, "swiffn: d and h must be multiples of 16");
   if ((flags & SMAUL_FLAG_TILED_LAYOUT) && (tile != 64 || d % 64 != 0 || h % 64 != 0))
     return fail(SMAUL_ERR_INVALID, "swiffn: the tiled layout needs tile 64 and d, h multiples of 64");
-  const int64_t need = smaul_swiffn_workspace_size(rows, h, act_dtype);
-  if (workspace_bytes < need) return fail(SMAUL_ERR_INVALID, "swiffn: workspace %lld < %lld bytes",
-                                          (long long)workspace_bytes, (long long)need);
+  // fp32: the hdn part is required, the planes part optional (see the size query)
+  const int64_t hdn_bytes = align256(rows * h * (act_dtype == SMAUL_DTYPE_BF16 ? 2 : 4));
+  if (workspace_bytes < hdn_bytes) return fail(SMAUL_ERR_INVALID, "swiffn: workspace %lld < %lld bytes",
+                                                (long long)workspace_bytes, (long long)hdn_bytes);
   if (rows == 0) return SMAUL_OK;
   if (!x || !gate_w8 || !gate_s || !up_w8 || !up_s || !down_w8 || !down_s || !out || !workspace)
     return fail(SMAUL_ERR_INVALID, "swiffn: null pointer");
@@ -4506,6 +4608,11 @@ int smaul_swiffn_forward(const void* x, int act_dtype, const uint8_t* gate_w8, c
       !aligned16(down_w8))
     return fail(SMAUL_ERR_UNSUPPORTED, "swiffn: x, codes, out and workspace must be 16-byte aligned");
   if (rows * (h > d ? h : d) > 2147483647LL) return fail(SMAUL_ERR_UNSUPPORTED, "swiffn: rows * width exceeds int32");
+  if (act_dtype == SMAUL_DTYPE_F32 && workspace_bytes >= smaul_swiffn_workspace_size(rows, h, act_dtype)) {
+    const int rc = swiffn_f32_planes((const float*)x, gate_w8, gate_s, up_w8, up_s, down_w8, down_s, (float*)out,
+                                     (char*)workspace, hdn_bytes, rows, d, h, tile, flags, stream);
+    if (rc != 1) return rc;  // 1: the shape does not fit the LDS-DMA kernels
+  }
   int rc = dense_gemm(true, x, act_dtype, gate_w8, gate_s, up_w8, up_s, workspace, rows, d, h, tile, flags, stream);
   if (rc) return rc;
   return dense_gemm(false, workspace, act_dtype, down_w8, down_s, nullptr, nullptr, out, rows, h, d, tile, flags,

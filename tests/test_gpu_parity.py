@@ -220,6 +220,56 @@ def test_fp8_linear_special_codes():
     assert rel_max(y, ref) < 2e-6
 
 
+def test_c2_dense_swiglu_pair_full_size_f32():
+    """Config 2 with the fp32 activations it specifies: x and then hdn split
+    into bf16 hi / lo planes, gate+up with the SwiGLU epilogue kept in fp32,
+    down with fp32 output; every 8th row against the oracle at the fp32 bar."""
+    gen = torch.Generator().manual_seed(1237)
+    rows, d, h = 4096, 512, 1280
+    x = torch.randn(rows, d, generator=gen)
+    ex = oracle.make_expert(d, h, gen)
+    bufs = tuple(t.to(DEV) for t in (ex.gate_w, ex.gate_s, ex.up_w, ex.up_s, ex.down_w, ex.down_s))
+    y = be().swiffn_forward(x.to(DEV), bufs, 64).cpu()
+    assert y.dtype == torch.float32 and y.shape == x.shape and torch.isfinite(y).all()
+    idx = torch.arange(0, rows, 8)
+    ref = oracle.swiffn_forward(x[idx], ex)
+    err = rel_l2(y[idx], ref)
+    print(f"rel_l2={err:.3e}")
+    assert err < 1e-5
+
+
+def test_swiffn_f32_workspace_without_planes():
+    """smaul_swiffn_forward through the C-ABI with fp32 x: a workspace of only
+    the hdn part (what the size query returned before the planes were added)
+    runs the register-staged kernels; the full size takes the planes.  Both
+    within the fp32 bar of the oracle."""
+    from smaulnative_amd import _lib
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(1238)
+    rows, d, h = 300, 256, 640
+    x = torch.randn(rows, d, generator=gen)
+    ex = oracle.make_expert(d, h, gen)
+    ref = oracle.swiffn_forward(x, ex)
+    xd = x.to(DEV)
+    bufs = [t.to(DEV) for t in (ex.gate_w, ex.gate_s, ex.up_w, ex.up_s, ex.down_w, ex.down_s)]
+    full = lib.smaul_swiffn_workspace_size(rows, h, _lib.DTYPE_F32)
+    part = ((rows * h * 4 + 255) // 256) * 256
+    assert full == 2 * part
+    for nbytes in (part, full):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+        out = torch.empty(rows, d, device=DEV)
+        rc = lib.smaul_swiffn_forward(xd.data_ptr(), _lib.DTYPE_F32, *[t.data_ptr() for t in bufs], out.data_ptr(),
+                                      ws.data_ptr(), nbytes, rows, d, h, 64, 0, None)
+        _lib.check(rc, "swiffn_forward")
+        torch.cuda.synchronize()
+        err = rel_l2(out.cpu(), ref)
+        print(f"workspace {nbytes}: rel_l2={err:.3e}")
+        assert err < 1e-5
+    short = torch.empty(part - 256, dtype=torch.uint8, device=DEV)
+    assert lib.smaul_swiffn_forward(xd.data_ptr(), _lib.DTYPE_F32, *[t.data_ptr() for t in bufs], out.data_ptr(),
+                                    short.data_ptr(), part - 256, rows, d, h, 64, 0, None) != 0
+
+
 def test_c2_dense_swiglu_pair_full_size():
     """Config 2: 4096 x 512 -> 2 x 1280 (gate and up in one launch with the
     SwiGLU epilogue), then 1280 -> 512, bf16 x, through the fused entry."""
@@ -241,7 +291,11 @@ def test_c2_dense_swiglu_pair_full_size():
 @pytest.mark.parametrize("rows,d,h,dtype,tile", [
     (37, 256, 640, torch.bfloat16, 64),     # small row count: 32-row register-staged tiles
     (300, 192, 320, torch.bfloat16, 64),    # d not a multiple of 256: register-staged down
-    (300, 256, 640, torch.float32, 64),     # fp32 activations (hi+lo split), no rounding points
+    (300, 256, 640, torch.float32, 64),     # fp32 activations: hi / lo planes through the LDS-DMA kernels
+    (1000, 1024, 2560, torch.float32, 64),  # the same with 128-row gate+up tiles
+    (64, 256, 640, torch.float32, 64),      # fp32, <= 64 rows: register-staged kernels
+    (300, 640, 256, torch.float32, 64),     # fp32, d > h: register-staged kernels
+    (300, 192, 320, torch.float32, 64),     # fp32, d not a multiple of 128: register-staged kernels
     (129, 256, 512, torch.bfloat16, 32),
     (200, 256, 384, torch.bfloat16, 128),
     (1, 512, 1280, torch.bfloat16, 64),
