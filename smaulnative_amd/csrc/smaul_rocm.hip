@@ -4694,6 +4694,8 @@ int64_t smaul_moe_workspace_size(int64_t T, int64_t d, int64_t h, int64_t E, int
   n += align256(R * h * el);
   n += align256(R * d * el);
   n += 256;  // sync words of the decode path's fused combine
+  // fp32 x: its bf16 hi / lo planes for the LDS-DMA GEMMs (moe_f32_planes)
+  if (act_dtype == SMAUL_DTYPE_F32) n += align256(T * d * 4);
   return n;
 }
 
@@ -4797,6 +4799,89 @@ __global__ void wait_timeouts_kernel(int32_t* out, int reset) {
   if (reset) __hip_atomic_fetch_sub(&g_wait_timeouts, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// fp32 activations through the LDS-DMA grouped GEMMs: the tile rows (128,
+// or 64 where a 128-row gate+up grid is under four workgroups per CU, as for
+// bf16) when the shapes fit (tile 64, d and h multiples of 128, codes
+// promised 16-byte aligned, the kernels' 32-bit offsets for the planes of x
+// and of hdn), else 0.
+static int64_t f32_planes_block_m(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k, int64_t tile, int flags,
+                                  int64_t R, int cus) {
+  if (tile != 64 || d % 128 != 0 || h % 128 != 0 || !(flags & SMAUL_FLAG_ALIGNED_CODES)) return 0;
+  const int64_t lim = (int64_t)1 << 31;
+  const int64_t hrows = ((R + CfgBig::BM - 1) / CfgBig::BM + E) * CfgBig::BM;  // >= the rows either tiling indexes
+  if (T * d * 4 >= lim || hrows * h * 4 >= lim || 2 * h * d >= lim) return 0;
+  return ((R + CfgBig::BM - 1) / CfgBig::BM + E) * (h / 128) < 4 * (int64_t)cus ? DMA_SMALL_BM : CfgBig::BM;
+}
+
+// The grouped gate+up and down of fp32 x (after the dispatch, on the tile
+// table of block_m rows): x split into bf16 hi / lo planes ([T][2d]); gate+up
+// over both planes of the gathered rows (K doubled, weight blocks wrapped)
+// with the SwiGLU product kept in fp32 and stored as the planes of hdn
+// ([R][2h], the fp32 hdn's bytes); down over those planes with fp32 output
+// into yperm.  Every value the reference forms in fp32 stays within 2^-18
+// relative of it.
+static int moe_f32_planes(const float* x, uint16_t* xplanes, const int32_t* perm_row, const uint8_t* const* gw,
+                          const float* const* gs, const uint8_t* const* uw, const float* const* us,
+                          const uint8_t* const* dw, const float* const* ds, uint16_t* hplanes, float* yperm,
+                          const int32_t* seg_off, const int32_t* tile_off, int64_t max_tiles, int64_t T, int64_t d,
+                          int64_t h, int64_t E, int64_t bm, int flags, hipStream_t stream) {
+  GemmArgs g{};
+  g.x = xplanes;
+  g.row_idx = perm_row;
+  g.ldx = 2 * d;
+  g.wp = gw;
+  g.sp = gs;
+  g.wp2 = uw;
+  g.sp2 = us;
+  g.y = hplanes;
+  g.ldy = 2 * h;
+  g.y_lo = h;
+  g.K = 2 * d;
+  g.kw = d;
+  g.N = h;
+  g.nt = d / 64;
+  g.tile = 64;
+  g.seg_off = seg_off;
+  g.tile_off = tile_off;
+  g.E = (int)E;
+  g.tiled = (flags & SMAUL_FLAG_TILED_LAYOUT) != 0;
+  GemmArgs dn = g;
+  dn.x = hplanes;
+  dn.row_idx = nullptr;
+  dn.ldx = 2 * h;
+  dn.wp = dw;
+  dn.sp = ds;
+  dn.wp2 = nullptr;
+  dn.sp2 = nullptr;
+  dn.y = yperm;
+  dn.ldy = d;
+  dn.y_lo = 0;
+  dn.K = 2 * h;
+  dn.kw = h;
+  dn.N = d;
+  dn.nt = h / 64;
+  if (!dma_gemm_ok(g, SMAUL_DTYPE_BF16, flags, T, 128) || !dma_gemm_ok(dn, SMAUL_DTYPE_BF16, flags, max_tiles * bm, 128))
+    return fail(SMAUL_ERR_UNSUPPORTED, "moe_forward: fp32 planes shapes outside the LDS-DMA kernels");
+  const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
+  int rc = launch_split_planes(x, xplanes, T, d, stream);
+  if (rc != SMAUL_OK) return rc;
+  if (bm == DMA_SMALL_BM) {
+    rc = canon ? launch_gemm_dma<CfgDmaGU64, true, true, true>(g, max_tiles, stream)
+               : launch_gemm_dma<CfgDmaGU64, true, false, true>(g, max_tiles, stream);
+    if (rc != SMAUL_OK) return rc;
+    return canon ? launch_gemm_dma<CfgDma64x128, false, true, true>(dn, max_tiles, stream)
+                 : launch_gemm_dma<CfgDma64x128, false, false, true>(dn, max_tiles, stream);
+  }
+  rc = canon ? launch_gemm_dma<CfgDmaGU, true, true, true>(g, max_tiles, stream)
+             : launch_gemm_dma<CfgDmaGU, true, false, true>(g, max_tiles, stream);
+  if (rc != SMAUL_OK) return rc;
+  if (d % CfgDmaDown::BN != 0 || max_tiles * (d / CfgDmaDown::BN) < 8 * (int64_t)cu_count())
+    return canon ? launch_gemm_dma<CfgDmaDownN, false, true, true>(dn, max_tiles, stream)
+                 : launch_gemm_dma<CfgDmaDownN, false, false, true>(dn, max_tiles, stream);
+  return canon ? launch_gemm_dma<CfgDmaDown, false, true, true>(dn, max_tiles, stream)
+               : launch_gemm_dma<CfgDmaDown, false, false, true>(dn, max_tiles, stream);
+}
+
 static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, const float* gate_b,
                             const uint8_t* const* gate_w8, const float* const* gate_s,
                             const uint8_t* const* up_w8, const float* const* up_s,
@@ -4840,8 +4925,16 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
   void* yperm = ws;
   ws += align256(R * d * el);
   int32_t* sync = (int32_t*)ws;
+  ws += 256;
+  uint16_t* xplanes = act_dtype == SMAUL_DTYPE_F32 ? (uint16_t*)ws : nullptr;
 
   int64_t bm = pick_block_m(T, d, h, E, k, tile, act_dtype);
+  // fp32 x on the LDS-DMA kernels over bf16 hi / lo planes (128- or 64-row
+  // tiles, by the same grid rule as bf16), else the register-staged kernels
+  const int64_t f32p_bm = act_dtype == SMAUL_DTYPE_F32
+                              ? f32_planes_block_m(T, d, h, E, k, tile, flags, R, cu_count())
+                              : 0;
+  if (f32p_bm) bm = f32p_bm;
   if (bm == CfgBig::BM && act_dtype == SMAUL_DTYPE_BF16 &&
       ((R + CfgBig::BM - 1) / CfgBig::BM + E) * (h / 128) < 4 * (int64_t)cu_count()) {
     // a 128-row gate/up grid under four workgroups per CU: 64-row tiles
@@ -4984,11 +5077,16 @@ static int moe_forward_impl(const void* x, int act_dtype, const float* gate_w, c
                              T, E, k, bm, route_tpb(T, E, d, act_dtype), stream);
     if (rc) return rc;
   }
-  rc = smaul_moe_gate_up(x, act_dtype, perm_row, gate_w8, gate_s, up_w8, up_s, hdn, seg_off, tile_off,
-                         max_tiles, E, d, h, tile, bm, flags, stream);
-  if (rc) return rc;
-  rc = smaul_moe_down(hdn, act_dtype, down_w8, down_s, yperm, seg_off, tile_off, max_tiles, E, d, h, tile,
-                      bm, flags, stream);
+  if (f32p_bm) {
+    rc = moe_f32_planes((const float*)x, xplanes, perm_row, gate_w8, gate_s, up_w8, up_s, down_w8, down_s,
+                        (uint16_t*)hdn, (float*)yperm, seg_off, tile_off, max_tiles, T, d, h, E, bm, flags, stream);
+  } else {
+    rc = smaul_moe_gate_up(x, act_dtype, perm_row, gate_w8, gate_s, up_w8, up_s, hdn, seg_off, tile_off,
+                           max_tiles, E, d, h, tile, bm, flags, stream);
+    if (rc) return rc;
+    rc = smaul_moe_down(hdn, act_dtype, down_w8, down_s, yperm, seg_off, tile_off, max_tiles, E, d, h, tile,
+                        bm, flags, stream);
+  }
   if (rc) return rc;
   return finish_combine(yperm, act_dtype, topi, topw, inv, out, T, d, k, nrm, nr, stream);
 }

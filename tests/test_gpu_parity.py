@@ -472,7 +472,11 @@ def test_moe_golden(tag):
     (1024, 1024, 2560, 8, 2, torch.bfloat16, 64),      # config-3 shape, fewer tokens
     (600, 256, 640, 8, 3, torch.bfloat16, 64),
     (512, 512, 1280, 4, 2, torch.bfloat16, 64),        # config-1 MoE layer shape
-    (333, 256, 640, 8, 2, torch.float32, 64),          # fp32 activations (hi+lo split)
+    (333, 256, 640, 8, 2, torch.float32, 64),          # fp32 x: hi / lo planes, 64-row LDS-DMA tiles
+    (4096, 1024, 2560, 8, 2, torch.float32, 64),       # fp32 x: planes, 128-row tiles, 128x128 down
+    (2048, 512, 1024, 8, 2, torch.float32, 64),        # fp32 x: planes, 128x256 down tiles
+    (40, 256, 640, 4, 2, torch.float32, 64),           # fp32 x, decode-sized: planes on 64-row tiles
+    (300, 192, 640, 4, 2, torch.float32, 64),          # fp32 x, d not a multiple of 128: register-staged
     (256, 256, 512, 4, 1, torch.bfloat16, 128),
     (200, 128, 320, 2, 2, torch.bfloat16, 32),
     (64, 1024, 2560, 8, 2, torch.bfloat16, 64),        # config-4 decode-sized step
