@@ -242,7 +242,10 @@ int smaul_rms_norm(const void* x, int act_dtype, const float* weight, void* out,
  * kernel, with the same results: the first workgroups to finish their units
  * wait for the rest through a counter in the workspace (cleared by the
  * gate/up kernel of the same call), so two calls must not share one
- * workspace concurrently.
+ * workspace concurrently.  With fp32 x (tile 64, d and h multiples of 128,
+ * SMAUL_FLAG_ALIGNED_CODES) both grouped GEMMs run on the LDS-DMA kernels over
+ * bf16 hi / lo planes of x and of the hidden rows (products within 2^-18
+ * relative of fp32); the fp32 workspace size includes the planes of x.
  */
 int64_t smaul_moe_workspace_size(int64_t T, int64_t d, int64_t h, int64_t E, int64_t k,
                                  int act_dtype);
