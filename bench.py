@@ -31,9 +31,12 @@ Extra objects on the same JSON line:
 - ``c5``: config 5 (the large skewed layer, T=65536 d=2048 h=5120 E=16), run
   before the config-3 timed region so that region starts under sustained load
   rather than in the clock transient after idle;
-- ``c2``: config 2 (one dense SwiGLU FFN, 4096 x 512 -> 2 x 1280 -> 512), and
-  FP8Linear's GEMM (fp8_forward) at the same shapes with fp32 and bf16 x;
-- ``c1``: the config-1 MoE layer shape (512 tokens, d=512, E=4).
+- ``c2``: config 2 (one dense SwiGLU FFN, 4096 x 512 -> 2 x 1280 -> 512) with
+  bf16 x and with the fp32 x the config names, and FP8Linear's GEMM
+  (fp8_forward) at the same shapes with fp32 and bf16 x;
+- ``c1``: the config-1 MoE layer shape (512 tokens, d=512, E=4);
+- ``c3_f32_x``: the config-3 layer with fp32 hidden states (bf16 hi / lo
+  planes through the same kernels), beside the bf16 headline.
 Only one GPU is measured: ``--gpus`` above 1 exits with a message.
 """
 from __future__ import annotations
@@ -243,6 +246,20 @@ def c2_bench(be, steps, warmup):
                     "(4096x512 -> 1280): three calls per step",
         "ms_per_step": bms, "tflops": flops / (bms * 1e-3) / 1e12, "mfma_frac": flops / (bms * 1e-3) / PEAK_BF16_FLOPS}
     return res, (x, bufs)
+
+
+def c3_f32_bench(be, xd, gwd, gbd, exd, k, steps, warmup):
+    """The config-3 layer with the fp32 hidden states the config names (the
+    same values as the bf16 headline, widened): both grouped GEMMs over bf16
+    hi / lo planes, the SwiGLU product, the down output and the combine in
+    fp32.  Reported beside the bf16 headline, not instead of it."""
+    xf = xd.float()
+    sec, _ = time_layer(be, xf, gwd, gbd, exd, k, steps, warmup)
+    T, d = xf.shape
+    fl = sum(layer_flops(T, d, exd[0][0].shape[0], len(exd), k).values())
+    return {"workload": "C3 layer with fp32 x (T=16384 d=1024 h=2560 E=8 top-2)", "ms_per_step": sec * 1e3,
+            "tokens_per_s": T / sec, "layer_mfma_frac": fl / sec / PEAK_BF16_FLOPS,
+            "note": "frac counts the algorithmic FLOPs once; the two planes double the MFMA work"}, None
 
 
 def c1_bench(be, steps, warmup):
@@ -677,6 +694,7 @@ def main():
     if not args.no_c2:
         leg("c2", lambda: c2_bench(be, args.steps, args.warmup))
     leg("c1", lambda: c1_bench(be, args.steps, args.warmup))
+    leg("c3_f32_x", lambda: c3_f32_bench(be, xd, gwd, gbd, exd, k, max(5, args.steps // 2), 2))
     if not args.no_decode:
         leg("decode", lambda: decode_bench(be, max(5, args.steps), args.warmup))
         legs["c4"] = legs.pop("decode", None)
