@@ -668,6 +668,37 @@ def test_moe_raw_codes_any_flags(T, flags, block_m):
     assert err < 2e-3
 
 
+@pytest.mark.parametrize("T,d,h,layout", [(700, 512, 1280, "raw"), (700, 512, 1280, "raw-aligned"),
+                                           (8192, 256, 1024, "raw-aligned"), (700, 512, 1280, "tiled"),
+                                           (8192, 256, 1024, "tiled")])
+def test_moe_fp32_x_abi_layouts(T, d, h, layout):
+    """fp32 x through the C-ABI on the caller's buffers: raw stored codes
+    (0x7F/0xFF included) without SMAUL_FLAG_ALIGNED_CODES run the
+    register-staged kernels; with it, and with tiled canonical copies, the
+    LDS-DMA kernels over bf16 hi / lo planes (64-row tiles at T = 700, 128-row
+    at T = 8192).  All within the fp32 bar of the oracle."""
+    from smaulnative_amd import _lib
+    print(f"case moe fp32 abi T={T} d={d} h={h} {layout}", flush=True)
+    E, k = 8, 2
+    x, gw, gb, experts = make_moe(777 + T, T, d, h, E, k, dtype=torch.float32)
+    gen = torch.Generator().manual_seed(6)
+    for ex in experts:   # 0x7F (= 448, like 0x7E) where the quantizer chose 0x7E
+        for w in (ex.gate_w, ex.up_w, ex.down_w):
+            w[(w == 0x7E) & (torch.rand(w.shape, generator=gen) < 0.5)] = 0x7F
+    ref = oracle.moe_forward(x, gw, gb, experts, k, 64)
+    if layout == "tiled":
+        flags = _lib.FLAG_TILED_LAYOUT | _lib.FLAG_CANONICAL_CODES | _lib.FLAG_ALIGNED_CODES
+        out, topi, counts = abi_moe(x, gw, gb, experts, k, 64, flags, tiled_copies(to_dev_experts(experts)))
+    else:
+        flags = _lib.FLAG_ALIGNED_CODES if layout == "raw-aligned" else 0
+        out, topi, counts = abi_moe(x, gw, gb, experts, k, 64, flags)
+    assert torch.equal(topi, ref.topi.reshape(-1, k))
+    assert counts.tolist() == ref.counts
+    err = rel_l2(out, ref.out)
+    print(f"rel_l2={err:.3e}")
+    assert err < 1e-5
+
+
 def tiled_copies(ex_dev):
     """The experts' buffers rewritten by smaul_fp8_tile_layout (canonical codes)."""
     from smaulnative_amd import _lib
