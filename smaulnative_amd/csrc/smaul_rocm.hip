@@ -4533,12 +4533,13 @@ static int dense_gemm(bool swiglu, const void* act, int act_dtype, const uint8_t
 // projection runs with fp32 output: every value the reference forms in fp32
 // stays within 2^-18 relative of it.  The planes of x go into the workspace's
 // first part (rows * 2d bf16 <= rows * h fp32), those of hdn into the second.
-// Returns 1 (nothing launched) when the shape does not fit: tile 64, d and h
-// multiples of 128, d <= h, more than 64 rows, and the kernels' offset limits.
+// Returns -1 (nothing launched) when the shape does not fit: tile 64, d and h
+// multiples of 128, d <= h, more than 64 rows, and the kernels' offset limits;
+// otherwise a status.
 static int swiffn_f32_planes(const float* x, const uint8_t* gw, const float* gs, const uint8_t* uw, const float* us,
                              const uint8_t* dw, const float* ds, float* out, char* ws, int64_t hdn_bytes,
                              int64_t rows, int64_t d, int64_t h, int64_t tile, int flags, hipStream_t stream) {
-  if (tile != 64 || d % 128 != 0 || h % 128 != 0 || d > h || rows <= 64) return 1;
+  if (tile != 64 || d % 128 != 0 || h % 128 != 0 || d > h || rows <= 64) return -1;
   uint16_t* xplanes = (uint16_t*)ws;
   uint16_t* hplanes = (uint16_t*)(ws + hdn_bytes);
   GemmArgs a{};
@@ -4577,7 +4578,7 @@ static int swiffn_f32_planes(const float* x, const uint8_t* gw, const float* gs,
   const int dtg = pick_dense_tile(true, rows, h), dtd = pick_dense_tile(false, rows, d);
   if (dtg < 0 || dtd < 0 || !dma_gemm_ok(a, SMAUL_DTYPE_BF16, fl, rows, 128) ||
       !dma_gemm_ok(b, SMAUL_DTYPE_BF16, fl, rows, 128))
-    return 1;
+    return -1;
   const bool canon = (flags & SMAUL_FLAG_CANONICAL_CODES) != 0;
   int rc = launch_split_planes(x, xplanes, rows, d, stream);
   if (rc != SMAUL_OK) return rc;
@@ -4611,7 +4612,7 @@ int smaul_swiffn_forward(const void* x, int act_dtype, const uint8_t* gate_w8, c
   if (act_dtype == SMAUL_DTYPE_F32 && workspace_bytes >= smaul_swiffn_workspace_size(rows, h, act_dtype)) {
     const int rc = swiffn_f32_planes((const float*)x, gate_w8, gate_s, up_w8, up_s, down_w8, down_s, (float*)out,
                                      (char*)workspace, hdn_bytes, rows, d, h, tile, flags, stream);
-    if (rc != 1) return rc;  // 1: the shape does not fit the LDS-DMA kernels
+    if (rc != -1) return rc;  // -1: the shape does not fit the LDS-DMA kernels
   }
   int rc = dense_gemm(true, x, act_dtype, gate_w8, gate_s, up_w8, up_s, workspace, rows, d, h, tile, flags, stream);
   if (rc) return rc;
