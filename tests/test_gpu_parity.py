@@ -995,6 +995,7 @@ def test_rms_norm(T, d, dtype, weighted):
     (40, 2048, 256, 4, 2, torch.bfloat16, True),    # two chunks per lane
     (300, 256, 640, 8, 2, torch.bfloat16, True),    # prefill path
     (33, 192, 320, 4, 3, torch.float32, False),     # fp32 activations
+    (300, 256, 640, 8, 2, torch.float32, True),     # fp32 activations on the hi / lo planes GEMMs
     (5, 4160, 128, 4, 2, torch.bfloat16, True),     # d > 4096: combine, then the norm kernel
 ])
 def test_moe_forward_norm(T, d, h, E, k, dtype, weighted):
@@ -1026,6 +1027,7 @@ def test_moe_forward_norm(T, d, h, E, k, dtype, weighted):
     (40, 2048, 256, 4, 2, 16, 4, torch.bfloat16),   # two chunks per lane, 16 next experts
     (300, 256, 640, 8, 2, 6, 2, torch.bfloat16),    # prefill path, ragged last 16-token block, E < EMAX
     (33, 192, 320, 4, 3, 4, 3, torch.float32),      # fp32: the next router runs as its own kernel
+    (300, 256, 640, 8, 2, 6, 2, torch.float32),     # fp32 on the hi / lo planes GEMMs, then norm and router
     (5, 4160, 128, 4, 2, 4, 2, torch.bfloat16),     # d > 4096: combine, norm, router kernels
     (7, 512, 384, 4, 2, 8, 3, torch.bfloat16),      # one partial 16-token block, fused router
     (20, 1024, 1024, 8, 2, 16, 4, torch.bfloat16),  # combine in the down kernel's tail: 3 workgroups, 16 experts
